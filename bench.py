@@ -1,0 +1,320 @@
+"""Benchmark of the gfx950 quantized GEMM path on one MI355X.
+
+Headline (BASELINE.json metric): int4 x int4 per-channel GEMM TOPS at
+M=N=K=8192 (config C2) through ``amd_strix_halo_kernels.mm``, as a fraction of
+the gfx950 dense int8 MFMA peak.  Secondary lines in the same JSON object:
+C3 (int4 subchannel-256 ReLU2, 4096x16384x4096), C4 (int8 fused SwiGLU,
+4096 x 11008 x 4096, TOPS count up + gate) and C5 (ragged MoE forward and
+K-ragged backward, G=8, M=8192, K=2048, N=1408).
+
+    python bench.py [--steps K] [--warmup W] [--no-secondary] [--no-cpu-baseline]
+
+A step is one API call over operands already resident in HBM; the timed region
+is exactly K steps bracketed by a device synchronisation on both sides.
+Kernel durations come from HIP events recorded around every launch on the
+stream the kernel runs on (torch's current stream).  No cache flush between
+steps (steady state, the operands of C2 fit the 256 MB MALL); a cold run that
+overwrites a 1 GiB buffer before each launch is reported beside it.  The CPU
+baseline is the repository's C oracle (the same unpack -> int32 matmul ->
+scale -> bf16 path) timed on a bounded row slice of the C2 operands on the
+host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "strix-halo-int4-gemms_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "int4 GEMM TOPS @8192³ (% gfx950 int8 MFMA peak); fused SwiGLU TOPS"
+INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
+HBM_PEAK_GBS = 8000.0
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _time_steps(torch, fn, steps: int, warmup: int):
+    """Runs fn warmup + steps times; returns (wall ms/step, mean kernel ms)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    kern = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    kern.sort()
+    return wall_ms, sum(kern) / len(kern), kern[len(kern) // 2]
+
+
+def _cold_ms(torch, fn, reps: int = 5) -> float:
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    times = []
+    for _ in range(reps):
+        flush.fill_(1)
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    del flush
+    times.sort()
+    return times[len(times) // 2]
+
+
+def _rand_int4_packed(torch, rows, cols, gen):
+    """Uniform int4 codes in [-8, 7] packed two per byte along cols."""
+    from amd_strix_halo_kernels import pack_int4_k_major
+
+    q = torch.randint(-8, 8, (rows, cols), dtype=torch.int8, device="cuda", generator=gen)
+    return pack_int4_k_major(q)
+
+
+def _uniform_bf16(torch, shape, lo, hi, gen):
+    return (torch.rand(shape, device="cuda", generator=gen) * (hi - lo) + lo).to(torch.bfloat16)
+
+
+def bench_c2(torch, shk, steps, warmup):
+    m = n = k = 8192
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    a = _rand_int4_packed(torch, m, k, gen)                      # [M, K/2]
+    b = _rand_int4_packed(torch, n, k, gen).t().contiguous()     # [K/2, N]
+    sa = _uniform_bf16(torch, (m,), 0.005, 0.02, gen)
+    sb = _uniform_bf16(torch, (n,), 0.005, 0.02, gen)
+    kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL),
+                                         epilogue=shk.Epilogue.NONE, m=m, n=n, k=k)
+
+    def step():
+        return shk.mm(a, b, a_scale=sa, b_scale=sb)
+
+    wall, kern_mean, kern_med = _time_steps(torch, step, steps, warmup)
+    cold = _cold_ms(torch, step)
+    ops = 2 * m * n * k
+    bytes_alg = m * k // 2 + k * n // 2 + 2 * m + 2 * n + 2 * m * n
+    return {
+        "m": m, "n": n, "k": k, "kernel": kernel.kernel_id, "ops": ops, "bytes": bytes_alg,
+        "wall_ms": wall, "kernel_ms": kern_mean, "kernel_ms_median": kern_med, "cold_kernel_ms": cold,
+        "host": (a, b, sa, sb),
+    }
+
+
+def bench_c3(torch, shk, steps, warmup):
+    m, k, n, s = 4096, 4096, 16384, 256
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    a = _rand_int4_packed(torch, m, k, gen)
+    b = _rand_int4_packed(torch, n, k, gen).t().contiguous()
+    sa = _uniform_bf16(torch, (m, k // s), 0.005, 0.02, gen)
+    sb = _uniform_bf16(torch, (k // s, n), 0.005, 0.02, gen)
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, s)
+
+    def step():
+        return shk.mm(a, b, a_scale=sa, b_scale=sb, scale=spec, epilogue=shk.Epilogue.RELU2)
+
+    wall, kern, _ = _time_steps(torch, step, steps, warmup)
+    ops = 2 * m * n * k
+    return {"tops": ops / (kern * 1e-3) / 1e12, "kernel_ms": kern, "wall_ms": wall,
+            "frac_int8_peak": ops / (kern * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS}
+
+
+def bench_c4(torch, shk, steps, warmup):
+    m, k, d = 4096, 4096, 11008
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda", generator=gen)
+    b = torch.randint(-127, 128, (k, 2 * d), dtype=torch.int8, device="cuda", generator=gen)
+    sa = _uniform_bf16(torch, (m,), 1e-4, 1e-3, gen)
+    sb = _uniform_bf16(torch, (2 * d,), 1e-4, 1e-3, gen)
+
+    def step():
+        return shk.fused_swiglu_up_gate(a, b, a_scale=sa, b_scale=sb, dtype=shk.OperandDType.INT8)
+
+    wall, kern, _ = _time_steps(torch, step, steps, warmup)
+    ops = 2 * m * (2 * d) * k
+    return {"tops": ops / (kern * 1e-3) / 1e12, "kernel_ms": kern, "wall_ms": wall,
+            "frac_int8_peak": ops / (kern * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS}
+
+
+def _multinomial_sizes(torch, rows, groups, seed):
+    g = torch.Generator().manual_seed(seed)
+    # Dirichlet(1) = normalised exponentials; multinomial counts; then the
+    # smallest group's rows move to the largest so one group is empty.
+    e = -torch.log(torch.rand(groups, generator=g, dtype=torch.float64))
+    probs = e / e.sum()
+    idx = torch.multinomial(probs, rows, replacement=True, generator=g)
+    sizes = torch.bincount(idx, minlength=groups).to(torch.int64)
+    if not (sizes == 0).any():
+        lo, hi = int(sizes.argmin()), int(sizes.argmax())
+        sizes[hi] += sizes[lo]
+        sizes[lo] = 0
+    return sizes
+
+
+def bench_c5(torch, shk, steps, warmup):
+    groups, rows, k, n = 8, 8192, 2048, 1408
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    sizes = _multinomial_sizes(torch, rows, groups, 5)
+    lhs = _rand_int4_packed(torch, rows, k, gen)
+    rhs = torch.stack([_rand_int4_packed(torch, n, k, gen).t().contiguous() for _ in range(groups)])
+    sa = _uniform_bf16(torch, (rows,), 0.005, 0.02, gen)
+    sb = _uniform_bf16(torch, (groups, n), 0.005, 0.02, gen)
+    gs = sizes.to(device="cuda", dtype=torch.int32)
+
+    def fwd():
+        return shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb)
+
+    wall_f, kern_f, _ = _time_steps(torch, fwd, steps, warmup)
+    ops = 2 * rows * n * k
+    bytes_f = rows * k // 2 + groups * k * n // 2 + 2 * rows + 2 * groups * n + 2 * rows * n
+
+    cap = int(sizes.max()) + int(sizes.max()) % 2
+    x = _rand_int4_packed(torch, groups * 2048, cap, gen).view(groups, 2048, cap // 2)
+    dy = torch.stack([_rand_int4_packed(torch, n, cap, gen).t().contiguous() for _ in range(groups)])
+    sa_b = _uniform_bf16(torch, (groups, 2048), 0.005, 0.02, gen)
+    sb_b = _uniform_bf16(torch, (groups, n), 0.005, 0.02, gen)
+    out_b = torch.empty((groups, 2048, n), device="cuda", dtype=torch.float32)
+
+    def bwd():
+        return shk.ragged_dot_int4_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, out=out_b)
+
+    wall_b, kern_b, _ = _time_steps(torch, bwd, steps, warmup)
+    ops_b = 2 * 2048 * n * rows
+    bytes_b = groups * 2048 * cap // 2 + groups * cap * n // 2 + 2 * groups * (2048 + n) + 4 * groups * 2048 * n
+    return {
+        "group_sizes": sizes.tolist(),
+        "fwd": {"kernel_ms": kern_f, "wall_ms": wall_f, "tops": ops / (kern_f * 1e-3) / 1e12,
+                "gbs": bytes_f / (kern_f * 1e-3) / 1e9,
+                "frac_hbm": bytes_f / (kern_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "frac_int8_peak": ops / (kern_f * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS},
+        "bwd": {"kernel_ms": kern_b, "wall_ms": wall_b, "tops": ops_b / (kern_b * 1e-3) / 1e12,
+                "gbs": bytes_b / (kern_b * 1e-3) / 1e9,
+                "frac_hbm": bytes_b / (kern_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
+    }
+
+
+def cpu_baseline(torch, host, target_s: float = 12.0):
+    """Times the C oracle's whole dense path on a row slice of the C2 operands."""
+    import numpy as np
+
+    from oracle import native as oracle_native
+
+    if not oracle_native.available():
+        from oracle import build as obuild
+
+        obuild.build(verbose=False)
+    a, b, sa, sb = host
+    a_np = a.cpu().numpy()
+    b_np = b.cpu().numpy()
+    sa_np = sa.view(torch.int16).cpu().numpy().view(np.uint16)
+    sb_np = sb.view(torch.int16).cpu().numpy().view(np.uint16)
+    m, n, k = a_np.shape[0], b_np.shape[1], 2 * a_np.shape[1]
+    threads = oracle_native.default_threads()
+    # calibrate on 32 rows, then size the sample to ~target_s
+    t0 = time.perf_counter()
+    oracle_native.dense_int4_nn(a_np, b_np, sa_np, sb_np, m=m, n=n, k=k, row0=0, rows=32, threads=threads)
+    t_cal = time.perf_counter() - t0
+    rows = int(min(m, max(32, 32 * target_s / max(t_cal, 1e-3))))
+    rows = max(32, rows - rows % 32)
+    t0 = time.perf_counter()
+    oracle_native.dense_int4_nn(a_np, b_np, sa_np, sb_np, m=m, n=n, k=k, row0=0, rows=rows, threads=threads)
+    secs = time.perf_counter() - t0
+    ops = 2 * rows * n * k
+    return {"value": ops / secs / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"C2 rows 0..{rows - 1} of 8192 (N=K=8192, full unpack->int32 matmul->scale->bf16), "
+                      f"{secs:.1f} s"}
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    args = p.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build runs the hot path on a single MI355X "
+              "(multi-GPU sharding is a design note, not built); use --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import amd_strix_halo_kernels as shk
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    _log("bench: C2 int4 per-channel 8192^3")
+    c2 = bench_c2(torch, shk, args.steps, args.warmup)
+    tops_kernel = c2["ops"] / (c2["kernel_ms"] * 1e-3) / 1e12
+    tops_wall = c2["ops"] / (c2["wall_ms"] * 1e-3) / 1e12
+    secondary = {}
+    if not args.no_secondary:
+        _log("bench: C3 int4 sc256 relu2")
+        secondary["c3_int4_sc256_relu2_4096x16384x4096"] = bench_c3(torch, shk, max(10, args.steps // 2),
+                                                                    args.warmup)
+        _log("bench: C4 int8 swiglu")
+        secondary["c4_int8_swiglu_4096x11008x4096"] = bench_c4(torch, shk, max(10, args.steps // 2), args.warmup)
+        _log("bench: C5 ragged fwd/bwd")
+        secondary["c5_ragged_g8_m8192_k2048_n1408"] = bench_c5(torch, shk, max(10, args.steps // 2), args.warmup)
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("bench: CPU baseline (C oracle)")
+        cpu = cpu_baseline(torch, c2["host"])
+    achieved = tops_kernel
+    line = {
+        "metric": METRIC,
+        "value": tops_wall,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": c2["wall_ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: int4 x int4 per-channel GEMM, epilogue none, M=N=K=8192, bf16 out",
+            "operands": "packed int4 (two nibbles per byte along K), int8 MFMA, int32 accumulation",
+            "kernel": c2["kernel"],
+            "parallelism": "single GPU",
+        },
+        "frac_int8_mfma_peak": tops_wall / INT8_MFMA_PEAK_TOPS,
+        "kernel_ms": c2["kernel_ms"],
+        "kernel_ms_median": c2["kernel_ms_median"],
+        "cold_kernel_ms": c2["cold_kernel_ms"],
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": INT8_MFMA_PEAK_TOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / INT8_MFMA_PEAK_TOPS,
+            "traffic": None,
+            "note": "int8 MFMA tera-ops/s; algorithmic 2*M*N*K per launch over the HIP-event launch duration",
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

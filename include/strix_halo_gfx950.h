@@ -1,0 +1,200 @@
+/*
+ * C ABI of the gfx950 (MI355X) quantized GEMM library
+ * (libamd_strix_halo_kernels_gfx950.so).
+ *
+ * This library replaces the reference's HSACO loader/dispatcher
+ * (native/src/dispatch.cpp) and its per-kernel JSON launch metadata
+ * (the kernels/amdgcn JSON files) with kernels compiled into the library and a static
+ * kernel table.  The Python host layer (amd_strix_halo_kernels.native) binds
+ * these symbols with ctypes.
+ *
+ * Conventions (same as the reference dispatcher, dispatch.cpp:18-23,220-222):
+ *   - every launch function returns 0 on success and 1 on failure;
+ *   - on failure amd_strix_halo_kernels_last_error() returns a message that
+ *     stays valid until the next call on the same thread;
+ *   - all device pointers are borrowed; the library never allocates or frees
+ *     device memory; workspaces are passed in by the caller;
+ *   - launches are asynchronous on the given stream (a hipStream_t passed as
+ *     uintptr_t, 0 = the null stream) on device `device_index`; the calling
+ *     thread's current device is restored before returning.
+ * Kernels are selected by table index (amd_strix_halo_kernels_kernel_table_*);
+ * the library derives grid, block and LDS size from the table entry.
+ */
+#ifndef STRIX_HALO_GFX950_H
+#define STRIX_HALO_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Kernel families in the table. */
+#define SHK_FAMILY_DENSE 0
+#define SHK_FAMILY_RAGGED_FWD 1
+#define SHK_FAMILY_RAGGED_BWD 2
+
+/* Layouts (reference metadata.GemmLayout, metadata.py:35-45). */
+#define SHK_LAYOUT_NN 0
+#define SHK_LAYOUT_NT 1
+#define SHK_LAYOUT_TN 2
+#define SHK_LAYOUT_TT 3
+
+/* Scale modes (reference metadata.ScaleMode, metadata.py:24-26). */
+#define SHK_SCALE_PER_CHANNEL 0
+#define SHK_SCALE_SUBCHANNEL 1
+
+/* Epilogue kinds of a table entry: PLAIN serves Epilogue.NONE and
+ * Epilogue.RELU2 (chosen per launch), SWIGLU serves Epilogue.SWIGLU. */
+#define SHK_EPI_KIND_PLAIN 0
+#define SHK_EPI_KIND_SWIGLU 2
+
+/* Per-launch epilogue (reference metadata.Epilogue, metadata.py:29-32). */
+#define SHK_EPILOGUE_NONE 0
+#define SHK_EPILOGUE_RELU2 1
+#define SHK_EPILOGUE_SWIGLU 2
+
+/* Output modes.  BF16 and F32 hold the scaled result; I32 writes the exact
+ * int32 accumulators (the integer matmul before any scale) for verification:
+ * for SwiGLU entries the I32 output is [M, 2*D] with up columns then gate
+ * columns; for subchannel entries it is the int32 sum over all K. */
+#define SHK_OUT_BF16 0
+#define SHK_OUT_F32 1
+#define SHK_OUT_I32 2
+
+typedef struct shk_kernel_desc {
+  int32_t index;
+  int32_t family;          /* SHK_FAMILY_* */
+  int32_t dtype_bits;      /* 4 (packed int4) or 8 (int8) */
+  int32_t layout;          /* SHK_LAYOUT_* */
+  int32_t scale_mode;      /* SHK_SCALE_* */
+  int32_t min_subchannel;  /* smallest subchannel size served (subchannel entries) */
+  int32_t max_subchannel;  /* largest subchannel size served (subchannel entries) */
+  int32_t epilogue_kind;   /* SHK_EPI_KIND_* */
+  int32_t block_m;         /* output rows per workgroup (ragged fwd: task rows) */
+  int32_t block_n;         /* output columns per workgroup */
+  int32_t block_k;         /* logical K per LDS stage */
+  int32_t num_waves;       /* 64-lane waves per workgroup */
+  int32_t num_stages;      /* LDS stages (double buffered = 2) */
+  int32_t lds_bytes;       /* LDS per workgroup */
+  int32_t group_size_m;    /* tile-row swizzle width (dense) */
+} shk_kernel_desc;
+
+/* ---- status (reference dispatch.cpp:206-222) ---------------------------- */
+
+/* Replaces amd_strix_halo_kernels_dispatch_version (dispatch.cpp:206).
+ * Version 2 = gfx950 table-driven dispatch. */
+int amd_strix_halo_kernels_dispatch_version(void);
+
+/* Replaces amd_strix_halo_kernels_has_compiled_code_objects
+ * (dispatch.cpp:208-210): 1, the gfx950 code objects are linked in. */
+int amd_strix_halo_kernels_has_compiled_code_objects(void);
+
+/* Replaces amd_strix_halo_kernels_has_hip_runtime (dispatch.cpp:212-214):
+ * 1 when the HIP runtime reports at least one device. */
+int amd_strix_halo_kernels_has_hip_runtime(void);
+
+/* Replaces amd_strix_halo_kernels_has_linked_kernels (dispatch.cpp:216-218):
+ * 1 when a gfx950 device is present to run the linked kernels. */
+int amd_strix_halo_kernels_has_linked_kernels(void);
+
+/* Replaces amd_strix_halo_kernels_last_error (dispatch.cpp:220-222). */
+const char* amd_strix_halo_kernels_last_error(void);
+
+/* Target architecture string of the linked code objects ("gfx950"). */
+const char* amd_strix_halo_kernels_arch(void);
+
+/* ---- kernel table (replaces the kernels/amdgcn JSON metadata and the registry tile
+ * seeds, registry.py:112-176, read by native.py:165-169) ----------------- */
+
+int amd_strix_halo_kernels_kernel_table_size(void);
+/* Copies entry `index` into *out.  Returns 0, or 1 for a bad index. */
+int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out);
+
+/* ---- dense GEMM -----------------------------------------------------------
+ * Replaces amd_strix_halo_kernels_launch_hsaco (dispatch.cpp:224-283) as
+ * called by native.launch_generated_kernel (native.py:690-767).
+ * Computes out = epilogue(scale(A @ B)) for logical shape (m, n, k), with
+ * A/B packed int4 (two nibbles per byte along K) or int8 per the entry's
+ * dtype and layout (NN: A[m, k'], B[k', b_cols]; NT: B[b_cols, k'];
+ * TN: A[k', m]; k' = k/2 for int4).  b_cols = n, or 2*n for SwiGLU entries
+ * where B holds [up | gate].  Scales are bf16: per-channel a_scale[m],
+ * b_scale[b_cols]; subchannel S: a_scale[m, ceil(k/S)],
+ * b_scale[ceil(k/S), b_cols].  Requires m % block_m == 0, n % block_n == 0,
+ * k % block_k == 0 and (subchannel) k % S == 0 (reference
+ * template_config.py:22-38).  `gate` of the reference signature is dropped:
+ * SwiGLU is fused. */
+int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintptr_t stream,
+                                       const void* a, const void* b, const void* a_scale,
+                                       const void* b_scale, void* out, int32_t m, int32_t n,
+                                       int32_t k, int32_t subchannel, int32_t epilogue,
+                                       int32_t out_mode);
+
+/* ---- ragged task list -------------------------------------------------------
+ * Device-side replacement of calculate_group_info (ragged.py:201-323, the
+ * Triton kernel ragged.py:127-185).  From int32 group_sizes[groups] builds,
+ * for tasks t < capacity:
+ *   tasks_i32[4*t + {0,1,2,3}] = group_id, block_start, actual_start, actual_end
+ * and writes num_tasks to *num_tasks_i32; slots t >= num_tasks are zero.
+ * If info_i64 is non-null it also receives the six int64 arrays of
+ * RaggedGroupInfo, each `capacity` long, in the order group_id, block_start,
+ * actual_start, actual_end, start_within_block, actual_size.
+ * Negative sizes count as zero (torch.clamp(min=0), ragged.py:256).
+ * If the tasks do not fit in `capacity`, *num_tasks_i32 receives the true
+ * count, the arrays receive the first `capacity` tasks, and the ragged
+ * forward refuses to run any task (the caller sizes capacity with
+ * amd_strix_halo_kernels_ragged_task_capacity). */
+int amd_strix_halo_kernels_ragged_group_info(int device_index, uintptr_t stream,
+                                             const int32_t* group_sizes, int32_t groups,
+                                             int32_t tile, int32_t align_tile, int32_t capacity,
+                                             int32_t* tasks_i32, int32_t* num_tasks_i32,
+                                             int64_t* info_i64);
+
+/* Upper bound on the number of row tasks for `rows` rows in `groups` groups. */
+int32_t amd_strix_halo_kernels_ragged_task_capacity(int32_t rows, int32_t groups, int32_t tile,
+                                                    int32_t align_tile);
+
+/* ---- ragged forward ---------------------------------------------------------
+ * Replaces amd_strix_halo_kernels_launch_ragged_fwd_hsaco (dispatch.cpp:286-389)
+ * as called by native.launch_ragged_fwd_kernel (native.py:533-600).
+ * out[rows of group g, :] = lhs[rows, :] @ rhs[g] with the task list built
+ * above (tasks_i32 / num_tasks_i32 device pointers, `capacity` slots; the
+ * grid covers capacity tasks and tasks >= *num_tasks_i32 exit).
+ * Layouts: NN lhs[m, k'], rhs[G, k', n]; NT rhs[G, n, k']; TN lhs[k', m];
+ * TT both.  Scales bf16: per-channel a_scale[m], b_scale[G, n]; subchannel S
+ * a_scale[m, ceil(k/S)], b_scale[G, ceil(k/S), n].  out_mode BF16 or F32
+ * (or I32 raw) [m, n].  The entry's block_m must equal the task tile. */
+int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index, uintptr_t stream,
+                                             const void* lhs, const void* rhs, const void* a_scale,
+                                             const void* b_scale, const int32_t* tasks_i32,
+                                             const int32_t* num_tasks_i32, int32_t capacity,
+                                             void* out, int32_t m, int32_t n, int32_t k_packed,
+                                             int32_t groups, int32_t subchannel, int32_t out_mode);
+
+/* ---- ragged backward --------------------------------------------------------
+ * Replaces amd_strix_halo_kernels_launch_ragged_bwd_hsaco (dispatch.cpp:391-457)
+ * as called by native.launch_ragged_bwd_kernel (native.py:603-667).
+ * out[g] = op(lhs[g]) @ op(rhs[g]) over the first group_sizes[g] (int32,
+ * device) logical K values; K beyond group_sizes[g] reads as zero, including
+ * the high nibble of an odd length (ragged.py:734-739).  Layouts: NN
+ * lhs[G, m, k'], rhs[G, k', n]; NT rhs[G, n, k']; TN lhs[G, k', m].
+ * Scales bf16: per-channel a_scale[G, m], b_scale[G, n]; subchannel S
+ * a_scale[G, m, ceil(2k'/S)], b_scale[G, ceil(2k'/S), n].  out is fp32
+ * [G, m, n].  split_k > 1 requires `out` to be zero-filled by the caller
+ * (as the reference does, ragged.py:1330-1331): per-channel splits add exact
+ * int32 partials and a finalize pass applies the scales (result identical to
+ * split_k = 1); subchannel splits own whole scale groups and add fp32
+ * partials atomically. */
+int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index, uintptr_t stream,
+                                             const void* lhs, const void* rhs, const void* a_scale,
+                                             const void* b_scale, const int32_t* group_sizes,
+                                             void* out, int32_t m, int32_t n, int32_t k_packed,
+                                             int32_t groups, int32_t subchannel, int32_t split_k,
+                                             int32_t out_mode);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRIX_HALO_GFX950_H */

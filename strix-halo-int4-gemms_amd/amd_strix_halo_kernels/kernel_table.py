@@ -1,0 +1,144 @@
+"""Python mirror of the gfx950 kernel table compiled into the library.
+
+The library (csrc/k_dense.hip, csrc/k_ragged.hip) appends its kernels in a
+fixed order; this module lists the same entries in the same order so that the
+registry can be built without loading the library.  ``native`` checks the
+mirror against ``amd_strix_halo_kernels_kernel_table_entry`` the first time it
+loads the library and refuses to launch on a mismatch.
+
+This table replaces the reference's tuned gfx1151 tile seeds
+(registry.py:112-176) and per-kernel JSON launch metadata.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+FAMILY_DENSE = 0
+FAMILY_RAGGED_FWD = 1
+FAMILY_RAGGED_BWD = 2
+
+LAYOUT_NN = 0
+LAYOUT_NT = 1
+LAYOUT_TN = 2
+LAYOUT_TT = 3
+LAYOUT_CODES = {"nn": LAYOUT_NN, "nt": LAYOUT_NT, "tn": LAYOUT_TN, "tt": LAYOUT_TT}
+
+SCALE_PER_CHANNEL = 0
+SCALE_SUBCHANNEL = 1
+
+EPI_KIND_PLAIN = 0
+EPI_KIND_SWIGLU = 2
+
+EPILOGUE_NONE = 0
+EPILOGUE_RELU2 = 1
+EPILOGUE_SWIGLU = 2
+
+OUT_BF16 = 0
+OUT_F32 = 1
+OUT_I32 = 2
+
+
+@dataclass(frozen=True)
+class KernelDesc:
+    """One entry of the library's kernel table (struct shk_kernel_desc)."""
+
+    index: int
+    family: int
+    dtype_bits: int
+    layout: int
+    scale_mode: int
+    min_subchannel: int
+    max_subchannel: int
+    epilogue_kind: int
+    block_m: int
+    block_n: int
+    block_k: int
+    num_waves: int
+    num_stages: int
+    lds_bytes: int
+    group_size_m: int
+
+    def serves_subchannel(self, size: int | None) -> bool:
+        if self.scale_mode == SCALE_PER_CHANNEL:
+            return size is None
+        return size is not None and self.min_subchannel <= size <= self.max_subchannel
+
+
+def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8):
+    brows = 2 * bn if swiglu else bn
+    lds = 2 * (bm * bk + brows * bk)
+    return KernelDesc(
+        index=index,
+        family=family,
+        dtype_bits=bits,
+        layout=layout,
+        scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
+        min_subchannel=(32 if mk == 32 else 64) if subch else 0,
+        max_subchannel=(32 if mk == 32 else 256) if subch else 0,
+        epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
+        block_m=bm,
+        block_n=bn,
+        block_k=bk,
+        num_waves=wm * wn,
+        num_stages=2,
+        lds_bytes=lds,
+        group_size_m=group_m,
+    )
+
+
+def _build() -> tuple[KernelDesc, ...]:
+    out: list[KernelDesc] = []
+
+    def add(**kw):
+        out.append(_desc(len(out), **kw))
+
+    for bits in (4, 8):
+        big_bk = 128 if bits == 4 else 64
+        for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
+            d = dict(family=FAMILY_DENSE, bits=bits, layout=layout)
+            add(**d, bm=256, bn=256, bk=big_bk, wm=2, wn=2)
+            add(**d, bm=128, bn=128, bk=64, wm=2, wn=2)
+            add(**d, bm=64, bn=64, bk=64, wm=2, wn=2)
+            add(**d, bm=256, bn=128, bk=big_bk, wm=2, wn=2, swiglu=True)
+            add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, swiglu=True)
+            add(**d, bm=256, bn=128, bk=big_bk, wm=4, wn=2, subch=True)
+            add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True)
+            add(**d, bm=256, bn=64, bk=big_bk, wm=4, wn=2, swiglu=True, subch=True)
+            add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, swiglu=True, subch=True)
+            add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True, mk=32)
+            add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, swiglu=True, subch=True, mk=32)
+    for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN, LAYOUT_TT):
+        for subch, mk in ((False, 64), (True, 64), (True, 32)):
+            f = dict(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1)
+            add(**f, bm=16, bn=128, bk=128, wm=1, wn=4)
+            add(**f, bm=32, bn=128, bk=128, wm=2, wn=2)
+            add(**f, bm=64, bn=128, bk=128, wm=2, wn=2)
+            add(**f, bm=128, bn=128, bk=128, wm=2, wn=2)
+        for subch, mk in ((False, 64), (True, 64), (True, 32)):
+            add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1, bm=128, bn=128,
+                bk=128, wm=2, wn=2)
+    return tuple(out)
+
+
+TABLE: tuple[KernelDesc, ...] = _build()
+
+
+def entries(family: int) -> tuple[KernelDesc, ...]:
+    return tuple(d for d in TABLE if d.family == family)
+
+
+def find_ragged(family: int, *, layout: int, subchannel: int | None, block_m: int | None = None) -> KernelDesc:
+    """Ragged kernel for a layout and scale mode (and task rows for the forward)."""
+    for d in TABLE:
+        if d.family != family or d.layout != layout or not d.serves_subchannel(subchannel):
+            continue
+        if block_m is not None and d.block_m != block_m:
+            continue
+        return d
+    raise LookupError(
+        f"no gfx950 ragged kernel for family={family}, layout={layout}, subchannel={subchannel}, block_m={block_m}"
+    )
+
+
+RAGGED_FWD_BLOCK_M = tuple(sorted({d.block_m for d in entries(FAMILY_RAGGED_FWD)}))

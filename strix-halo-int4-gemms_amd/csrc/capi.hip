@@ -1,0 +1,374 @@
+// C ABI of the gfx950 quantized GEMM library: kernel table, argument
+// validation, launch geometry and error reporting.  Declarations and the
+// reference interface each symbol replaces are in include/strix_halo_gfx950.h.
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "shk_table.h"
+
+namespace {
+
+using shk::Entry;
+
+thread_local std::string g_last_error;
+
+int fail(const std::string& msg) {
+  g_last_error = msg;
+  return 1;
+}
+
+int fail_hip(const char* what, hipError_t err) {
+  // Clear the sticky error so the next call starts clean (dispatch.cpp:150-156).
+  (void)hipGetLastError();
+  return fail(std::string(what) + " failed: " + hipGetErrorString(err));
+}
+
+const std::vector<Entry>& table() {
+  static const std::vector<Entry> t = [] {
+    std::vector<Entry> v;
+    shk::append_dense_4_0(v);
+    shk::append_dense_4_1(v);
+    shk::append_dense_4_2(v);
+    shk::append_dense_8_0(v);
+    shk::append_dense_8_1(v);
+    shk::append_dense_8_2(v);
+    shk::append_ragged_0(v);
+    shk::append_ragged_1(v);
+    shk::append_ragged_2(v);
+    shk::append_ragged_3(v);
+    for (size_t i = 0; i < v.size(); ++i) v[i].d.index = (int32_t)i;
+    return v;
+  }();
+  return t;
+}
+
+// Makes `device` current for the duration of a launch and restores the
+// caller's device afterwards.
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+    if (prev_ != device) {
+      err_ = hipSetDevice(device);
+      switched_ = err_ == hipSuccess;
+    }
+  }
+  ~DeviceGuard() {
+    if (switched_ && prev_ >= 0) (void)hipSetDevice(prev_);
+  }
+  hipError_t error() const { return err_; }
+
+ private:
+  int prev_ = -1;
+  bool switched_ = false;
+  hipError_t err_ = hipSuccess;
+};
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int lookup(int index, int family, const Entry** out) {
+  const auto& t = table();
+  if (index < 0 || index >= (int)t.size()) {
+    return fail("kernel index " + std::to_string(index) + " is out of range [0, " + std::to_string(t.size()) +
+                ")");
+  }
+  if (t[index].d.family != family) {
+    return fail("kernel index " + std::to_string(index) + " belongs to another kernel family");
+  }
+  *out = &t[index];
+  return 0;
+}
+
+// Subchannel size check shared by the three families.
+int check_subchannel(const shk_kernel_desc& d, int subchannel) {
+  if (d.scale_mode == SHK_SCALE_PER_CHANNEL) {
+    if (subchannel != 0) return fail("per-channel kernels take subchannel = 0");
+    return 0;
+  }
+  const bool pow2 = subchannel > 0 && (subchannel & (subchannel - 1)) == 0;
+  if (!pow2 || subchannel < d.min_subchannel || subchannel > d.max_subchannel) {
+    return fail("subchannel size " + std::to_string(subchannel) + " is not served by this kernel (supports " +
+                std::to_string(d.min_subchannel) + ".." + std::to_string(d.max_subchannel) + ")");
+  }
+  return 0;
+}
+
+int check_out_mode(int out_mode) {
+  if (out_mode != SHK_OUT_BF16 && out_mode != SHK_OUT_F32 && out_mode != SHK_OUT_I32)
+    return fail("unknown output mode " + std::to_string(out_mode));
+  return 0;
+}
+
+// Largest K for which the x16-widened int4 products of one int32 accumulator
+// cannot overflow: 128 * 128 * K < 2^31.
+constexpr int kMaxInt4AccK = 131072;
+
+}  // namespace
+
+extern "C" {
+
+int amd_strix_halo_kernels_dispatch_version(void) { return 2; }
+
+int amd_strix_halo_kernels_has_compiled_code_objects(void) { return 1; }
+
+int amd_strix_halo_kernels_has_hip_runtime(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n > 0 ? 1 : 0;
+}
+
+int amd_strix_halo_kernels_has_linked_kernels(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  for (int i = 0; i < n; ++i) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, i) != hipSuccess) {
+      (void)hipGetLastError();
+      continue;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) return 1;
+  }
+  return 0;
+}
+
+const char* amd_strix_halo_kernels_last_error(void) { return g_last_error.c_str(); }
+
+const char* amd_strix_halo_kernels_arch(void) { return "gfx950"; }
+
+int amd_strix_halo_kernels_kernel_table_size(void) { return (int)table().size(); }
+
+int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out) {
+  g_last_error.clear();
+  if (out == nullptr) return fail("out must be non-null");
+  const auto& t = table();
+  if (index < 0 || index >= (int)t.size()) return fail("kernel index out of range");
+  *out = t[index].d;
+  return 0;
+}
+
+int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintptr_t stream, const void* a,
+                                       const void* b, const void* a_scale, const void* b_scale, void* out,
+                                       int32_t m, int32_t n, int32_t k, int32_t subchannel, int32_t epilogue,
+                                       int32_t out_mode) {
+  g_last_error.clear();
+  const Entry* e = nullptr;
+  if (lookup(kernel_index, SHK_FAMILY_DENSE, &e)) return 1;
+  const shk_kernel_desc& d = e->d;
+  if (a == nullptr || b == nullptr || a_scale == nullptr || b_scale == nullptr || out == nullptr)
+    return fail("a, b, a_scale, b_scale, and out pointers must be non-null");
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail("M, N, and K must be positive; got (" + std::to_string(m) + ", " + std::to_string(n) + ", " +
+                std::to_string(k) + ")");
+  std::string why;
+  if (m % d.block_m) why += "M=" + std::to_string(m) + " is not divisible by BLOCK_M=" + std::to_string(d.block_m);
+  if (n % d.block_n) {
+    if (!why.empty()) why += "; ";
+    why += "N=" + std::to_string(n) + " is not divisible by BLOCK_N=" + std::to_string(d.block_n);
+  }
+  if (k % d.block_k) {
+    if (!why.empty()) why += "; ";
+    why += "K=" + std::to_string(k) + " is not divisible by BLOCK_K*SPLIT_K=" + std::to_string(d.block_k);
+  }
+  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && k % subchannel) {
+    if (!why.empty()) why += "; ";
+    why += "K=" + std::to_string(k) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
+  }
+  if (!why.empty()) return fail("kernel " + std::to_string(kernel_index) + " requires tile-multiple shape: " + why);
+  if (check_subchannel(d, subchannel)) return 1;
+  if (check_out_mode(out_mode)) return 1;
+  const bool swiglu = d.epilogue_kind == SHK_EPI_KIND_SWIGLU;
+  if (swiglu ? epilogue != SHK_EPILOGUE_SWIGLU : (epilogue != SHK_EPILOGUE_NONE && epilogue != SHK_EPILOGUE_RELU2))
+    return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
+  if (d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
+    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
+                std::to_string(k));
+  if (!aligned(out, 16) || !aligned(b_scale, 8) || !aligned(a_scale, 2))
+    return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
+
+  const long kbytes = (long)k * d.dtype_bits / 8;
+  const int b_cols = swiglu ? 2 * n : n;
+  shk::DenseArgs p{};
+  p.a = static_cast<const uint8_t*>(a);
+  p.b = static_cast<const uint8_t*>(b);
+  p.a_scale = static_cast<const uint16_t*>(a_scale);
+  p.b_scale = static_cast<const uint16_t*>(b_scale);
+  p.out = out;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  const bool a_km = d.layout != SHK_LAYOUT_TN;
+  const bool b_km = d.layout == SHK_LAYOUT_NT;
+  p.lda = a_km ? kbytes : m;
+  p.ldb = b_km ? kbytes : b_cols;
+  p.b_cols = b_cols;
+  p.subchannel = subchannel;
+  p.scale_cols = subchannel > 0 ? (k + subchannel - 1) / subchannel : 1;
+  p.epilogue = epilogue == SHK_EPILOGUE_RELU2 ? shk::EPI_RELU2 : shk::EPI_NONE;
+  p.out_mode = out_mode;
+  p.a_aligned = a_km ? (aligned(a, 16) && p.lda % 16 == 0) : (aligned(a, 8) && p.lda % 8 == 0);
+  p.b_aligned = b_km ? (aligned(b, 16) && p.ldb % 16 == 0) : (aligned(b, 8) && p.ldb % 8 == 0);
+  p.group_m = d.group_size_m;
+  if (!p.a_aligned || !p.b_aligned)
+    return fail(std::string("dense kernels need ") + (a_km ? "16" : "8") + "-byte aligned A and " +
+                (b_km ? "16" : "8") + "-byte aligned B data pointers");
+  const long tiles = (long)(m / d.block_m) * (n / d.block_n);
+  if (tiles > 0x7FFFFFFFL) return fail("too many output tiles");
+
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const hipError_t err = e->dense(p, dim3((unsigned)tiles), reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail_hip("kernel launch", err);
+  return 0;
+}
+
+int32_t amd_strix_halo_kernels_ragged_task_capacity(int32_t rows, int32_t groups, int32_t tile,
+                                                    int32_t align_tile) {
+  if (rows < 0 || groups < 0 || tile <= 0 || align_tile <= 0) return 0;
+  (void)align_tile;  // align_tile <= tile bounds every group's extra block by one
+  const long cap = (long)rows / tile + 2L * groups + 1;
+  return cap > 0x7FFFFFFFL ? 0x7FFFFFFF : (int32_t)cap;
+}
+
+int amd_strix_halo_kernels_ragged_group_info(int device_index, uintptr_t stream, const int32_t* group_sizes,
+                                             int32_t groups, int32_t tile, int32_t align_tile, int32_t capacity,
+                                             int32_t* tasks_i32, int32_t* num_tasks_i32, int64_t* info_i64) {
+  g_last_error.clear();
+  if (groups < 0) return fail("groups must be non-negative");
+  if (groups > shk::max_info_groups())
+    return fail("at most " + std::to_string(shk::max_info_groups()) + " groups are supported");
+  if (tile <= 0) return fail("tile must be positive");
+  if (align_tile <= 0) return fail("align_tile must be positive");
+  if (tile % align_tile != 0) return fail("tile must be a multiple of align_tile");
+  if (capacity < 0) return fail("capacity must be non-negative");
+  if (num_tasks_i32 == nullptr) return fail("num_tasks pointer must be non-null");
+  if (capacity > 0 && tasks_i32 == nullptr) return fail("tasks pointer must be non-null");
+  if (groups > 0 && group_sizes == nullptr) return fail("group_sizes pointer must be non-null");
+  if (!aligned(tasks_i32, 16)) return fail("tasks buffer must be 16-byte aligned");
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const hipError_t err = shk::launch_group_info(group_sizes, groups, tile, align_tile, capacity, tasks_i32,
+                                                num_tasks_i32, info_i64, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail_hip("group info launch", err);
+  return 0;
+}
+
+int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index, uintptr_t stream,
+                                             const void* lhs, const void* rhs, const void* a_scale,
+                                             const void* b_scale, const int32_t* tasks_i32,
+                                             const int32_t* num_tasks_i32, int32_t capacity, void* out, int32_t m,
+                                             int32_t n, int32_t k_packed, int32_t groups, int32_t subchannel,
+                                             int32_t out_mode) {
+  g_last_error.clear();
+  const Entry* e = nullptr;
+  if (lookup(kernel_index, SHK_FAMILY_RAGGED_FWD, &e)) return 1;
+  const shk_kernel_desc& d = e->d;
+  if (lhs == nullptr || rhs == nullptr || a_scale == nullptr || b_scale == nullptr || out == nullptr ||
+      tasks_i32 == nullptr || num_tasks_i32 == nullptr)
+    return fail("lhs, rhs, scales, task list and out pointers must be non-null");
+  if (m < 0 || n < 0 || k_packed < 0 || groups < 0 || capacity < 0) return fail("sizes must be non-negative");
+  if (check_subchannel(d, subchannel)) return 1;
+  if (check_out_mode(out_mode)) return 1;
+  const int k = 2 * k_packed;
+  if (d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
+    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
+  if (!aligned(tasks_i32, 16)) return fail("tasks buffer must be 16-byte aligned");
+  if (m == 0 || n == 0 || capacity == 0) return 0;
+  shk::RaggedFwdArgs p{};
+  p.lhs = static_cast<const uint8_t*>(lhs);
+  p.rhs = static_cast<const uint8_t*>(rhs);
+  p.a_scale = static_cast<const uint16_t*>(a_scale);
+  p.b_scale = static_cast<const uint16_t*>(b_scale);
+  p.tasks = tasks_i32;
+  p.num_tasks = num_tasks_i32;
+  p.capacity = capacity;
+  p.out = out;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  p.groups = groups;
+  const bool a_km = d.layout == SHK_LAYOUT_NN || d.layout == SHK_LAYOUT_NT;
+  const bool b_km = d.layout == SHK_LAYOUT_NT || d.layout == SHK_LAYOUT_TT;
+  p.lda = a_km ? k_packed : m;
+  p.ldb = b_km ? k_packed : n;
+  p.subchannel = subchannel;
+  p.scale_cols = subchannel > 0 ? (k + subchannel - 1) / subchannel : 1;
+  p.out_mode = out_mode;
+  p.a_aligned = a_km ? (aligned(lhs, 16) && p.lda % 16 == 0) : (aligned(lhs, 8) && p.lda % 8 == 0);
+  p.b_aligned = b_km ? (aligned(rhs, 16) && p.ldb % 16 == 0) : (aligned(rhs, 8) && p.ldb % 8 == 0);
+  p.out_vec = (n % 4 == 0) && aligned(out, 16) && aligned(b_scale, 8);
+  const long tiles_n = (n + d.block_n - 1) / d.block_n;
+  const long grid = (long)capacity * tiles_n;
+  if (grid > 0x7FFFFFFFL) return fail("ragged forward grid is too large");
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const hipError_t err = e->fwd(p, dim3((unsigned)grid), reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail_hip("ragged forward launch", err);
+  return 0;
+}
+
+int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index, uintptr_t stream,
+                                             const void* lhs, const void* rhs, const void* a_scale,
+                                             const void* b_scale, const int32_t* group_sizes, void* out,
+                                             int32_t m, int32_t n, int32_t k_packed, int32_t groups,
+                                             int32_t subchannel, int32_t split_k, int32_t out_mode) {
+  g_last_error.clear();
+  const Entry* e = nullptr;
+  if (lookup(kernel_index, SHK_FAMILY_RAGGED_BWD, &e)) return 1;
+  const shk_kernel_desc& d = e->d;
+  if (lhs == nullptr || rhs == nullptr || a_scale == nullptr || b_scale == nullptr || out == nullptr ||
+      group_sizes == nullptr)
+    return fail("lhs, rhs, scales, group_sizes and out pointers must be non-null");
+  if (m < 0 || n < 0 || k_packed < 0 || groups < 0) return fail("sizes must be non-negative");
+  if (split_k < 1 || split_k > 65535) return fail("split_k must be in [1, 65535]");
+  if (check_subchannel(d, subchannel)) return 1;
+  if (out_mode != SHK_OUT_F32 && out_mode != SHK_OUT_I32)
+    return fail("ragged backward writes fp32 (or raw int32) output");
+  const int k_cap = 2 * k_packed;
+  if (d.scale_mode == SHK_SCALE_PER_CHANNEL && k_cap > kMaxInt4AccK)
+    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
+  if (m == 0 || n == 0 || groups == 0) return 0;
+  shk::RaggedBwdArgs p{};
+  p.lhs = static_cast<const uint8_t*>(lhs);
+  p.rhs = static_cast<const uint8_t*>(rhs);
+  p.a_scale = static_cast<const uint16_t*>(a_scale);
+  p.b_scale = static_cast<const uint16_t*>(b_scale);
+  p.group_sizes = group_sizes;
+  p.out = out;
+  p.M = m;
+  p.N = n;
+  p.k_cap = k_cap;
+  p.groups = groups;
+  const bool a_km = d.layout == SHK_LAYOUT_NN || d.layout == SHK_LAYOUT_NT;
+  const bool b_km = d.layout == SHK_LAYOUT_NT || d.layout == SHK_LAYOUT_TT;
+  p.lda = a_km ? k_packed : m;
+  p.ldb = b_km ? k_packed : n;
+  p.subchannel = subchannel;
+  p.scale_cols = subchannel > 0 ? (k_cap + subchannel - 1) / subchannel : 1;
+  p.split_k = split_k;
+  p.out_mode = out_mode;
+  p.a_aligned = a_km ? (aligned(lhs, 16) && p.lda % 16 == 0) : (aligned(lhs, 8) && p.lda % 8 == 0);
+  p.b_aligned = b_km ? (aligned(rhs, 16) && p.ldb % 16 == 0) : (aligned(rhs, 8) && p.ldb % 8 == 0);
+  p.out_vec = (n % 4 == 0) && aligned(out, 16) && aligned(b_scale, 8);
+  const long tiles = (long)groups * ((m + d.block_m - 1) / d.block_m) * ((n + d.block_n - 1) / d.block_n);
+  if (tiles > 0x7FFFFFFFL) return fail("ragged backward grid is too large");
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = e->bwd(p, dim3((unsigned)tiles, (unsigned)split_k), s);
+  if (err != hipSuccess) return fail_hip("ragged backward launch", err);
+  if (split_k > 1 && d.scale_mode == SHK_SCALE_PER_CHANNEL && out_mode == SHK_OUT_F32) {
+    err = shk::launch_bwd_finalize(static_cast<float*>(out), p.a_scale, p.b_scale, groups, m, n, s);
+    if (err != hipSuccess) return fail_hip("ragged backward finalize launch", err);
+  }
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+// Internal kernel-table plumbing shared by the kernel translation units and
+// the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "../../include/strix_halo_gfx950.h"
+#include "shk_gemm.h"
+
+namespace shk {
+
+using DenseLaunchFn = hipError_t (*)(const DenseArgs&, dim3, hipStream_t);
+using RaggedFwdLaunchFn = hipError_t (*)(const RaggedFwdArgs&, dim3, hipStream_t);
+using RaggedBwdLaunchFn = hipError_t (*)(const RaggedBwdArgs&, dim3, hipStream_t);
+
+struct Entry {
+  shk_kernel_desc d;
+  DenseLaunchFn dense;
+  RaggedFwdLaunchFn fwd;
+  RaggedBwdLaunchFn bwd;
+};
+
+template <class C>
+hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL(dense_gemm_kernel<C>, grid, dim3(C::NT), 0, s, a);
+  return hipGetLastError();
+}
+template <class C>
+hipError_t launch_fwd_t(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL(ragged_fwd_kernel<C>, grid, dim3(C::NT), 0, s, a);
+  return hipGetLastError();
+}
+template <class C>
+hipError_t launch_bwd_t(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL(ragged_bwd_kernel<C>, grid, dim3(C::NT), 0, s, a);
+  return hipGetLastError();
+}
+
+template <class C>
+constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
+  return shk_kernel_desc{
+      -1,
+      family,
+      C::BITS,
+      layout,
+      C::SUBCH ? SHK_SCALE_SUBCHANNEL : SHK_SCALE_PER_CHANNEL,
+      C::SUBCH ? (C::MK == 32 ? 32 : 64) : 0,
+      C::SUBCH ? (C::MK == 32 ? 32 : 256) : 0,
+      C::SWIGLU ? SHK_EPI_KIND_SWIGLU : SHK_EPI_KIND_PLAIN,
+      C::BM,
+      C::BN,
+      C::BK,
+      C::NT / 64,
+      2,
+      C::LDS_BYTES,
+      group_m,
+  };
+}
+
+template <class C>
+Entry dense_entry(int layout, int group_m) {
+  return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_dense_t<C>, nullptr, nullptr};
+}
+template <class C>
+Entry fwd_entry(int layout) {
+  return Entry{desc_of<C>(SHK_FAMILY_RAGGED_FWD, layout, 1), nullptr, &launch_fwd_t<C>, nullptr};
+}
+template <class C>
+Entry bwd_entry(int layout) {
+  return Entry{desc_of<C>(SHK_FAMILY_RAGGED_BWD, layout, 1), nullptr, nullptr, &launch_bwd_t<C>};
+}
+
+// Each kernel translation unit appends its entries in a fixed order
+// (append_dense_<bits>_<layout>, append_ragged_<layout>).
+void append_dense_4_0(std::vector<Entry>& t);
+void append_dense_4_1(std::vector<Entry>& t);
+void append_dense_4_2(std::vector<Entry>& t);
+void append_dense_8_0(std::vector<Entry>& t);
+void append_dense_8_1(std::vector<Entry>& t);
+void append_dense_8_2(std::vector<Entry>& t);
+void append_ragged_0(std::vector<Entry>& t);
+void append_ragged_1(std::vector<Entry>& t);
+void append_ragged_2(std::vector<Entry>& t);
+void append_ragged_3(std::vector<Entry>& t);
+int max_info_groups();
+
+// Non-table kernels (ragged.hip).
+hipError_t launch_group_info(const int32_t* sizes, int groups, int tile, int align, int capacity,
+                             int32_t* tasks, int32_t* num_tasks, int64_t* info, hipStream_t s);
+hipError_t launch_bwd_finalize(float* out, const uint16_t* a_scale, const uint16_t* b_scale, int groups,
+                               int m, int n, hipStream_t s);
+
+}  // namespace shk

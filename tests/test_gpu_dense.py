@@ -1,0 +1,183 @@
+"""GPU parity of the dense path (mm / fused_swiglu_up_gate / explicit_mm)
+against the CPU oracle.
+
+Bar: the int32 accumulators are bit-exact against the
+integer matmul; bf16 outputs are within 2 bf16 ulp of the oracle (per-channel
+and subchannel NONE / RELU2 come out bit-identical; SwiGLU may differ by an
+ulp through exp).  Mirrors the reference's every-registry-kernel check
+(tests/test_native_generated.py:74-108) and adds the BASELINE configs at full
+size, checked on sampled rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import ref
+from tests._util import bf16_bits, dense_case, max_ulp, stable_seed, to_dev
+
+torch = pytest.importorskip("torch")
+
+import amd_strix_halo_kernels as shk  # noqa: E402
+from amd_strix_halo_kernels import native  # noqa: E402
+from amd_strix_halo_kernels.template_config import representative_generation_shape  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+ULP_TOL = 2
+
+
+def _run_kernel(kernel, a_arg, b_arg, sa, sb, device):
+    a = to_dev(torch, a_arg, device)
+    b = to_dev(torch, b_arg, device)
+    ta = to_dev(torch, sa, device)
+    tb = to_dev(torch, sb, device)
+    out = shk.explicit_mm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    raw = native.launch_generated_kernel_i32(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    torch.cuda.synchronize()
+    return bf16_bits(torch, out), raw.cpu().numpy()
+
+
+def _kernel_params(kernel):
+    bits = 4 if kernel.a_dtype is shk.OperandDType.INT4 else 8
+    sub = kernel.scale.subchannel_size if kernel.scale.mode is shk.ScaleMode.SUBCHANNEL else None
+    return bits, kernel.layout.value, sub, kernel.epilogue.value
+
+
+@pytest.mark.parametrize("kernel", shk.default_registry.all(), ids=lambda k: k.kernel_id)
+def test_every_registry_kernel_matches_oracle(kernel, device):
+    bits, layout, sub, epi = _kernel_params(kernel)
+    shape = representative_generation_shape(kernel)
+    k = max(shape.k, 2 * kernel.tile.block_k)  # at least two K stages
+    if sub:
+        k = -(-k // sub) * sub
+    m, n = 2 * shape.m, 2 * shape.n  # several tiles
+    seed = stable_seed(kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=epi == "swiglu")
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q)), "int32 accumulators differ"
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=bits, layout=layout, a_scale=sa, b_scale=sb,
+                                   subchannel=sub, epilogue=epi)
+    if epi == "swiglu":
+        assert max_ulp(got, want) <= ULP_TOL
+    else:
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+@pytest.mark.parametrize("scale", ["pc", "sc32", "sc64", "sc128", "sc256"])
+@pytest.mark.parametrize("epilogue", ["none", "relu2", "swiglu"])
+def test_surface_api_matches_oracle(bits, layout, scale, epilogue, device):
+    m, n, k = 256, 256, 512
+    sub = None if scale == "pc" else int(scale[2:])
+    seed = stable_seed(bits, layout, scale, epilogue)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=epilogue == "swiglu")
+    dtype = shk.OperandDType.INT4 if bits == 4 else shk.OperandDType.INT8
+    spec = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL) if sub is None else shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, sub)
+    lay = shk.GemmLayout(layout)
+    a, b = to_dev(torch, a_arg, device), to_dev(torch, b_arg, device)
+    ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
+    print(f"case bits={bits} {layout} {scale} {epilogue}", flush=True)
+    if epilogue == "swiglu":
+        out = shk.fused_swiglu_up_gate(a, b, a_scale=ta, b_scale=tb, dtype=dtype, layout=lay, scale=spec)
+    else:
+        out = shk.mm(a, b, a_scale=ta, b_scale=tb, dtype=dtype, layout=lay, scale=spec,
+                     epilogue=shk.Epilogue(epilogue))
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (m, n)
+    got = bf16_bits(torch, out)
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=bits, layout=layout, a_scale=sa, b_scale=sb, subchannel=sub,
+                                   epilogue=epilogue)
+    if epilogue == "swiglu":
+        assert max_ulp(got, want) <= ULP_TOL
+    else:
+        assert np.array_equal(got, want)
+
+
+def test_config_c1_plumbing_exact(device):
+    """C1: 128x1024x64 int4 per-channel, randn*0.1 fake-quantized, unit scales."""
+    r = ref.rng(1)
+    a_q = ref.randn_bf16_fake_quant(r, (128, 64), bits=4)
+    b_q = ref.randn_bf16_fake_quant(r, (64, 1024), bits=4)
+    a_arg, b_arg = ref.pack_operands(a_q, b_q, bits=4, layout="nn")
+    sa = ref.bf16_from_f32(np.ones(128))
+    sb = ref.bf16_from_f32(np.ones(1024))
+    out = shk.mm(to_dev(torch, a_arg, device), to_dev(torch, b_arg, device), a_scale=to_dev(torch, sa, device),
+                 b_scale=to_dev(torch, sb, device))
+    got = bf16_bits(torch, out)
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=4, a_scale=sa, b_scale=sb)
+    assert np.array_equal(got, want)
+    # unit scales: the output is the integer matmul, rounded to bf16
+    assert np.array_equal(got, ref.bf16_round(ref.int_matmul(a_q, b_q).astype(np.float32)))
+
+
+def _sampled_rows(m: int, count: int, seed: int) -> np.ndarray:
+    r = ref.rng(seed)
+    blocks = r.choice(m // 16, size=count // 16, replace=False)
+    return np.sort(np.concatenate([np.arange(b * 16, b * 16 + 16) for b in blocks]))
+
+
+def _big_dense(device, *, bits, m, n, k, sub, epilogue, seed, scale_lo=0.005, scale_hi=0.02):
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout="nn", m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=epilogue == "swiglu", scale_lo=scale_lo,
+                                                 scale_hi=scale_hi)
+    dtype = shk.OperandDType.INT4 if bits == 4 else shk.OperandDType.INT8
+    spec = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL) if sub is None else shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, sub)
+    a, b = to_dev(torch, a_arg, device), to_dev(torch, b_arg, device)
+    ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
+    if epilogue == "swiglu":
+        kernel = shk.default_registry.select(dtype=dtype, scale=spec, epilogue=shk.Epilogue.SWIGLU, m=m, n=n, k=k)
+        out = shk.fused_swiglu_up_gate(a, b, a_scale=ta, b_scale=tb, dtype=dtype, scale=spec)
+    else:
+        kernel = shk.default_registry.select(dtype=dtype, scale=spec, epilogue=shk.Epilogue(epilogue), m=m, n=n,
+                                             k=k)
+        out = shk.mm(a, b, a_scale=ta, b_scale=tb, dtype=dtype, scale=spec, epilogue=shk.Epilogue(epilogue))
+    raw = native.launch_generated_kernel_i32(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    torch.cuda.synchronize()
+    rows = _sampled_rows(m, 64, seed)
+    got = bf16_bits(torch, out[torch.from_numpy(rows).to(device)])
+    raw_rows = raw[torch.from_numpy(rows).to(device)].cpu().numpy()
+    assert np.array_equal(raw_rows, ref.int_matmul(a_q[rows], b_q)), "int32 accumulators differ"
+    a_rows = a_arg[rows]
+    sa_rows = sa[rows]
+    want = ref.reference_gemm_bf16(a_rows, b_arg, bits=bits, a_scale=sa_rows, b_scale=sb, subchannel=sub,
+                                   epilogue=epilogue)
+    return got, want, kernel
+
+
+def test_config_c2_8192_cubed(device):
+    got, want, kernel = _big_dense(device, bits=4, m=8192, n=8192, k=8192, sub=None, epilogue="none", seed=2)
+    assert kernel.tile.block_m == 256 and kernel.tile.block_n == 256
+    assert np.array_equal(got, want)
+
+
+def test_config_c3_subchannel_relu2(device):
+    got, want, _ = _big_dense(device, bits=4, m=4096, n=16384, k=4096, sub=256, epilogue="relu2", seed=3)
+    assert np.array_equal(got, want)
+
+
+def test_config_c4_int8_swiglu(device):
+    got, want, _ = _big_dense(device, bits=8, m=4096, n=11008, k=4096, sub=None, epilogue="swiglu", seed=4,
+                              scale_lo=1e-4, scale_hi=1e-3)
+    assert max_ulp(got, want) <= ULP_TOL
+
+
+def test_shape_and_layout_errors(device):
+    a = torch.zeros((100, 32), dtype=torch.uint8, device=device)
+    b = torch.zeros((32, 64), dtype=torch.uint8, device=device)
+    with pytest.raises(LookupError):
+        shk.mm(a, b, a_scale=torch.ones(100, dtype=torch.bfloat16, device=device),
+               b_scale=torch.ones(64, dtype=torch.bfloat16, device=device))
+    kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL),
+                                         epilogue=shk.Epilogue.NONE, m=64, n=64, k=64)
+    a = torch.zeros((64, 32), dtype=torch.uint8, device=device)
+    b = torch.zeros((32, 96), dtype=torch.uint8, device=device)
+    with pytest.raises(ValueError, match="tile-multiple"):
+        shk.explicit_mm(a, b, kernel=kernel, a_scale=torch.ones(64, dtype=torch.bfloat16, device=device),
+                        b_scale=torch.ones(96, dtype=torch.bfloat16, device=device))
+    with pytest.raises(ValueError, match="require a_scale and b_scale"):
+        shk.explicit_mm(a[:, :32], b[:, :64].contiguous(), kernel=kernel)

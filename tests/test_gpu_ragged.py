@@ -1,0 +1,277 @@
+"""GPU parity of the ragged path (calculate_group_info, ragged_dot_int4,
+ragged_dot_int4_bwd) against the CPU oracle.
+
+The cases mirror the reference's tests/test_ragged_dot.py (:154-586): every
+layout, per-channel and subchannel-32 scales, split_k 1 and 2, empty groups,
+odd K with garbage in the padding, and the even-K fast path; plus the
+BASELINE C5 MoE shape at full size.  Per-channel results are bit-identical to
+the oracle (same op order, exact int32 sums); subchannel split-K adds fp32
+partials in another order and is held to a relative 1e-5.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import ref
+from tests._util import bf16_bits, max_ulp, stable_seed, to_dev
+
+torch = pytest.importorskip("torch")
+
+import amd_strix_halo_kernels as shk  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = [shk.GemmLayout.NN, shk.GemmLayout.NT, shk.GemmLayout.TN, shk.GemmLayout.TT]
+SCALES = [shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL), shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 32)]
+
+
+def _pack_fwd(a_q, b_q, layout):
+    """Physical forward operands (test_ragged_dot.py:54-65)."""
+    lhs = ref.pack_int4_k_major(a_q)
+    if layout in (shk.GemmLayout.TN, shk.GemmLayout.TT):
+        lhs = np.ascontiguousarray(lhs.T)
+    rhs = []
+    for g in range(b_q.shape[0]):
+        p = ref.pack_int4_k_major(b_q[g].T)
+        rhs.append(p if layout in (shk.GemmLayout.NT, shk.GemmLayout.TT) else np.ascontiguousarray(p.T))
+    return lhs, np.ascontiguousarray(np.stack(rhs))
+
+
+def _pack_bwd(a_q, b_q, layout):
+    """Physical backward operands (test_ragged_dot.py:68-81)."""
+    lhs, rhs = [], []
+    for g in range(a_q.shape[0]):
+        l = ref.pack_int4_k_major(a_q[g])
+        lhs.append(np.ascontiguousarray(l.T) if layout in (shk.GemmLayout.TN, shk.GemmLayout.TT) else l)
+        r = ref.pack_int4_k_major(b_q[g].T)
+        rhs.append(r if layout in (shk.GemmLayout.NT, shk.GemmLayout.TT) else np.ascontiguousarray(r.T))
+    return np.ascontiguousarray(np.stack(lhs)), np.ascontiguousarray(np.stack(rhs))
+
+
+# ---------------------------------------------------------------------------
+# task list
+
+
+@pytest.mark.parametrize(
+    "sizes,tile,tid_size",
+    [([512] * 8, 64, None), ([300, 0, 1000, 17, 2779], 64, None), ([1] * 16, 32, None), ([4096], 128, None),
+     ([7, 9, 0, 40], 16, None), ([512] * 8, 64, 600), ([17, 31, 24], 32, None), ([2, 0, 7], 16, 4),
+     ([0, 0, 0], 16, None), ([0, 0, 0], 16, 5)],
+)
+def test_group_info_device_matches_oracle(sizes, tile, tid_size, device):
+    gs = torch.tensor(sizes, dtype=torch.int32, device=device)
+    info = shk.calculate_group_info(gs, tile, tid_size=tid_size)
+    want = ref.calculate_group_info(np.array(sizes), tile, tid_size=tid_size)
+    assert info.num_tasks == want.num_tasks
+    for f in ("group_id", "block_start", "actual_start", "actual_end", "start_within_block", "actual_size"):
+        got = getattr(info, f)
+        assert got.is_cuda and got.dtype == torch.int64
+        assert np.array_equal(got.cpu().numpy(), getattr(want, f)), f
+
+
+def test_group_info_device_random_against_oracle(device):
+    r = ref.rng(77)
+    for _ in range(40):
+        g = int(r.integers(1, 40))
+        sizes = r.integers(0, 300, size=g)
+        tile = int(r.choice([16, 32, 64, 128]))
+        align = int(r.choice([1, 2, 4, 8]))
+        info = shk.calculate_group_info(torch.tensor(sizes, device=device), tile, align_tile=align)
+        want = ref.calculate_group_info(sizes, tile, align_tile=align)
+        assert info.num_tasks == want.num_tasks
+        assert np.array_equal(info.actual_end.cpu().numpy(), want.actual_end)
+        assert np.array_equal(info.block_start.cpu().numpy(), want.block_start)
+        assert np.array_equal(info.group_id.cpu().numpy(), want.group_id)
+
+
+# ---------------------------------------------------------------------------
+# forward
+
+
+def _fwd_case(seed, m, k, n, sizes, scale, *, std=0.1):
+    r = ref.rng(seed)
+    groups = len(sizes)
+    a_q = ref.randint4(r, (m, k))
+    b_q = ref.randint4(r, (groups, k, n))
+    if scale.mode is shk.ScaleMode.PER_CHANNEL:
+        sa = ref.uniform_bf16(r, (m,), 0.008, 0.012)
+        sb = ref.uniform_bf16(r, (groups, n), 0.009, 0.011)
+    else:
+        cols = -(-k // scale.subchannel_size)
+        sa = ref.uniform_bf16(r, (m, cols), 0.008, 0.012)
+        sb = ref.uniform_bf16(r, (groups, cols, n), 0.009, 0.011)
+    return a_q, b_q, sa, sb
+
+
+def _run_fwd(device, a_q, b_q, sizes, sa, sb, scale, layout, config, output_dtype):
+    lhs, rhs = _pack_fwd(a_q, b_q, layout)
+    out = shk.ragged_dot_int4(
+        to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
+        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), scale=scale, config=config,
+        layout=layout, output_dtype=output_dtype)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("output_dtype", ["float32", "bfloat16"])
+def test_ragged_fwd_small_reference_case(output_dtype, device):
+    """test_ragged_dot.py:240-303: m=9, k=32, n=16, sizes [2, 0, 7]."""
+    scale = SCALES[0]
+    sizes = [2, 0, 7]
+    a_q, b_q, sa, sb = _fwd_case(19, 9, 32, 16, sizes, scale)
+    cfg = shk.RaggedDotConfig(block_m=16, block_n=16, block_k=32, group_size_tasks=4, num_warps=4, num_stages=3)
+    dt = getattr(torch, output_dtype)
+    out = _run_fwd(device, a_q, b_q, sizes, sa, sb, scale, shk.GemmLayout.NN, cfg, dt)
+    want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb)
+    if output_dtype == "float32":
+        assert np.array_equal(out.cpu().numpy(), want)
+    else:
+        assert np.array_equal(bf16_bits(torch, out), ref.bf16_round(want))
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("scale", SCALES, ids=lambda s: s.label)
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128])
+def test_ragged_fwd_all_layouts(layout, scale, block_m, device):
+    """test_ragged_dot.py:306-368: m=17, k=64, n=24, sizes [5, 0, 12]."""
+    sizes = [5, 0, 12]
+    a_q, b_q, sa, sb = _fwd_case(stable_seed("fwd", layout.value, scale.label, block_m), 17, 64, 24, sizes, scale)
+    cfg = shk.RaggedDotConfig(block_m=block_m, block_n=16, block_k=32, group_size_tasks=2)
+    out = _run_fwd(device, a_q, b_q, sizes, sa, sb, scale, layout, cfg, torch.float32)
+    want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb,
+                                    subchannel=scale.subchannel_size)
+    assert np.array_equal(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("scale", [SCALES[0], SCALES[1], shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 64),
+                                   shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 256)], ids=lambda s: s.label)
+def test_ragged_fwd_even_k_and_larger(scale, device):
+    """test_ragged_dot.py:448-513 (even K) plus a multi-stage K and N tail."""
+    for m, k, n, sizes in ((33, 64, 24, [5, 12, 16]), (300, 512, 200, [100, 0, 37, 163])):
+        if scale.subchannel_size and k % scale.subchannel_size and scale.subchannel_size > k:
+            continue
+        a_q, b_q, sa, sb = _fwd_case(stable_seed("even", m, scale.label), m, k, n, sizes, scale)
+        out = _run_fwd(device, a_q, b_q, sizes, sa, sb, scale, shk.GemmLayout.NN, shk.RaggedDotConfig(),
+                       torch.bfloat16)
+        want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=scale.subchannel_size)
+        assert np.array_equal(bf16_bits(torch, out), ref.bf16_round(want))
+
+
+def test_config_c5_forward_full(device):
+    """C5: G=8, M=8192, K=2048, N=1408, multinomial group sizes with an empty group."""
+    r = ref.rng(5)
+    sizes = ref.multinomial_group_sizes(r, 8192, 8)
+    assert (sizes == 0).any() and sizes.sum() == 8192
+    a_q = ref.randint4(r, (8192, 2048))
+    b_q = ref.randint4(r, (8, 2048, 1408))
+    sa = ref.uniform_bf16(r, (8192,), 0.005, 0.02)
+    sb = ref.uniform_bf16(r, (8, 1408), 0.005, 0.02)
+    out = _run_fwd(device, a_q, b_q, sizes.tolist(), sa, sb, SCALES[0], shk.GemmLayout.NN, shk.RaggedDotConfig(),
+                   torch.bfloat16)
+    want = ref.ragged_fwd_reference(a_q, b_q, sizes, sa, sb)
+    assert np.array_equal(bf16_bits(torch, out), ref.bf16_round(want))
+
+
+# ---------------------------------------------------------------------------
+# backward
+
+
+def _bwd_case(seed, groups, m, kcap, n, scale):
+    r = ref.rng(seed)
+    a_q = ref.randint4(r, (groups, m, kcap))
+    b_q = ref.randint4(r, (groups, kcap, n))
+    if scale.mode is shk.ScaleMode.PER_CHANNEL:
+        sa = ref.uniform_bf16(r, (groups, m), 0.008, 0.012)
+        sb = ref.uniform_bf16(r, (groups, n), 0.009, 0.011)
+    else:
+        cols = -(-kcap // scale.subchannel_size)
+        sa = ref.uniform_bf16(r, (groups, m, cols), 0.008, 0.012)
+        sb = ref.uniform_bf16(r, (groups, cols, n), 0.009, 0.011)
+    return a_q, b_q, sa, sb
+
+
+def _run_bwd(device, a_q, b_q, sizes, sa, sb, scale, layout, split_k):
+    lhs, rhs = _pack_bwd(a_q, b_q, layout)
+    out = shk.ragged_dot_int4_bwd(
+        to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
+        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), scale=scale,
+        config=shk.RaggedBwdDotConfig(block_m=16, block_n=16, block_k=16, split_k=split_k), layout=layout)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _check_bwd(got, want, scale, split_k):
+    if scale.mode is shk.ScaleMode.SUBCHANNEL and split_k > 1:
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-7)
+    else:
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("scale", SCALES, ids=lambda s: s.label)
+@pytest.mark.parametrize("split_k", [1, 2])
+def test_ragged_bwd_tile_aligned(layout, scale, split_k, device):
+    """test_ragged_dot.py:371-445: G=3, m=16, K cap 32, n=20, sizes [32, 0, 32]."""
+    sizes = [32, 0, 32]
+    a_q, b_q, sa, sb = _bwd_case(stable_seed("bwd-al", layout.value, scale.label, split_k), 3, 16, 32, 20, scale)
+    got = _run_bwd(device, a_q, b_q, sizes, sa, sb, scale, layout, split_k)
+    want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=scale.subchannel_size)
+    _check_bwd(got, want, scale, split_k)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("scale", SCALES, ids=lambda s: s.label)
+@pytest.mark.parametrize("split_k", [1, 2])
+def test_ragged_bwd_odd_k_garbage_padding(layout, scale, split_k, device):
+    """test_ragged_dot.py:516-586: K cap 39, sizes [5, 0, 37]; the padding
+    beyond each group's K holds random values that must not contribute."""
+    sizes = [5, 0, 37]
+    a_q, b_q, sa, sb = _bwd_case(stable_seed("bwd-odd", layout.value, scale.label, split_k), 3, 16, 39, 20, scale)
+    got = _run_bwd(device, a_q, b_q, sizes, sa, sb, scale, layout, split_k)
+    want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=scale.subchannel_size)
+    _check_bwd(got, want, scale, split_k)
+
+
+@pytest.mark.parametrize("split_k", [1, 3])
+@pytest.mark.parametrize("scale", [SCALES[0], shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 128),
+                                   shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 256)], ids=lambda s: s.label)
+def test_ragged_bwd_multi_stage(scale, split_k, device):
+    sizes = [700, 0, 1, 1023, 512]
+    a_q, b_q, sa, sb = _bwd_case(stable_seed("bwd-ms", scale.label, split_k), 5, 200, 1024, 136, scale)
+    got = _run_bwd(device, a_q, b_q, sizes, sa, sb, scale, shk.GemmLayout.NN, split_k)
+    want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=scale.subchannel_size)
+    _check_bwd(got, want, scale, split_k)
+
+
+def test_config_c5_backward_full(device):
+    """C5 backward: dW[g] = X_g^T dY_g, lhs [8, 2048, cap/2], rhs [8, cap/2, 1408]."""
+    r = ref.rng(55)
+    sizes = ref.multinomial_group_sizes(r, 8192, 8)
+    cap = int(sizes.max()) + (int(sizes.max()) % 2)
+    a_q = ref.randint4(r, (8, 2048, cap))
+    b_q = ref.randint4(r, (8, cap, 1408))
+    sa = ref.uniform_bf16(r, (8, 2048), 0.005, 0.02)
+    sb = ref.uniform_bf16(r, (8, 1408), 0.005, 0.02)
+    got = _run_bwd(device, a_q, b_q, sizes.tolist(), sa, sb, SCALES[0], shk.GemmLayout.NN, 1)
+    want = ref.ragged_bwd_reference(a_q, b_q, sizes, sa, sb)
+    assert np.array_equal(got, want)
+
+
+def test_ragged_errors(device):
+    gs = torch.tensor([4, 4], device=device, dtype=torch.int32)
+    lhs = torch.zeros((8, 16), device=device, dtype=torch.uint8)
+    rhs = torch.zeros((2, 16, 8), device=device, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="weight-matched layout"):
+        shk.ragged_dot_int4(lhs, rhs, gs, a_scale=torch.ones((8, 1), device=device, dtype=torch.bfloat16),
+                            b_scale=torch.ones((2, 8, 1), device=device, dtype=torch.bfloat16),
+                            scale=shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 32))
+    with pytest.raises(ValueError, match="sum\\(group_sizes\\) must equal lhs rows 8"):
+        shk.ragged_dot_int4(lhs, rhs, torch.tensor([4, 5], device=device))
+    with pytest.raises(ValueError, match="non-negative"):
+        shk.ragged_dot_int4(lhs, rhs, torch.tensor([12, -4], device=device))
+    with pytest.raises(ValueError, match="logical padded K 32"):
+        shk.ragged_dot_int4_bwd(torch.zeros((2, 8, 16), device=device, dtype=torch.uint8),
+                                torch.zeros((2, 16, 8), device=device, dtype=torch.uint8),
+                                torch.tensor([33, 0], device=device))
