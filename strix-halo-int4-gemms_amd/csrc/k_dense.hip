@@ -29,7 +29,8 @@ using C = Cfg<kBits, kAKmajor, kBKmajor, BM, BN, BK, WM, WN, SWIGLU, SUBCH, MK, 
 // B rows, so a 256x128 output tile multiplies 256 B columns.  Subchannel tiles
 // keep an fp32 sum per accumulator in VGPRs, so they run eight waves of 64x64
 // (two waves per SIMD: one wave's scale flush overlaps the other's MFMAs).
-// int8 stages are 64 deep so the prefetched stage fits in registers.
+// int8 stages are 64 deep so the prefetched stage and two fragment sets fit
+// in registers.
 constexpr int kBigBK = kBits == 4 ? 128 : 64;
 
 void append_all(std::vector<Entry>& t) {

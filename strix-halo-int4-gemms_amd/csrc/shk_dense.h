@@ -1,0 +1,158 @@
+// Dense GEMM kernel on the pipelined engine (tile-multiple shapes, aligned
+// operands; both checked on the host).
+#pragma once
+
+#include "shk_fast.h"
+
+namespace shk {
+
+// Writes one tile's results.  `value(i, j, r)` gives the scaled, epilogue-
+// applied fp32 value, `raw(i, j, r)` the int32 written in verification mode.
+template <class C, class E, class Value, class Raw>
+__device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int m0, int n0, Value value, Raw raw) {
+  const bool swiglu_raw = C::SWIGLU && p.out_mode == OUT_I32;
+  const long ldo = swiglu_raw ? 2L * p.N : (long)p.N;
+  if (p.out_mode == OUT_I32) {
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN2; ++j) {
+        if (!C::SWIGLU && j >= C::FN) continue;
+        const long col = (j < C::FN ? 0 : p.N) + n0 + e.out_col(j);
+        int* o = reinterpret_cast<int*>(p.out) + (long)(m0 + e.out_row(i)) * ldo + col;
+        *reinterpret_cast<int4*>(o) = make_int4(raw(i, j, 0), raw(i, j, 1), raw(i, j, 2), raw(i, j, 3));
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const long idx = (long)(m0 + e.out_row(i)) * p.N + n0 + e.out_col(j);
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = value(i, j, r);
+      if (p.out_mode == OUT_BF16) {
+        const uint32_t lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + idx) = make_uint2(lo, hi);
+      } else {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+}
+
+template <class C>
+__global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
+  const int tiles_m = p.M / C::BM;
+  const int tiles_n = p.N / C::BN;
+  int tm, tn;
+  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
+  const int m0 = tm * C::BM;
+  const int n0 = tn * C::BN;
+  const unsigned long long kbytes = (unsigned long long)p.K * C::BITS / 8;
+  const int gate = C::SWIGLU ? p.N : 0;
+
+  FastEngine<C> e;
+  e.init_reads();
+  if (C::A_KMAJOR) {  // A [M, kbytes]
+    e.ra = make_rsrc(p.a + (long)m0 * p.lda, (unsigned long long)(p.M - m0) * p.lda);
+    e.sa.init((uint32_t)p.lda, 0);
+  } else {            // A [kbytes, M]
+    e.ra = make_rsrc(p.a + m0, kbytes * p.M - m0);
+    e.sa.init((uint32_t)p.lda, 0);
+  }
+  if (C::B_KMAJOR) {  // B [b_cols, kbytes]
+    e.rb = make_rsrc(p.b + (long)n0 * p.ldb, (unsigned long long)(p.b_cols - n0) * p.ldb);
+    e.sb.init((uint32_t)p.ldb, (uint32_t)gate);
+  } else {            // B [kbytes, b_cols]
+    e.rb = make_rsrc(p.b + n0, kbytes * p.b_cols - n0);
+    e.sb.init((uint32_t)p.ldb, (uint32_t)gate);
+  }
+  const int nst = p.K / C::BK;
+  const bool raw = p.out_mode == OUT_I32;
+
+  if constexpr (C::SUBCH) {
+    SubAcc<C> s;
+    s.zero();
+    const int S = p.subchannel;
+    auto on_step = [&](int ke) {
+      if (ke % S == 0) {
+        const int g = ke / S - 1;
+        float sa[C::FM];
+        if (raw) {
+#pragma unroll
+          for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::FN2; ++j)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                s.f[i][j][r] = __int_as_float(__float_as_int(s.f[i][j][r]) + e.true_acc(e.acc[i][j][r]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < C::FM; ++i)
+            sa[i] = load_bf16(p.a_scale + (long)(m0 + e.out_row(i)) * p.scale_cols + g);
+#pragma unroll
+          for (int j = 0; j < C::FN2; ++j) {
+            float sb[4];
+            const int col = (j < C::FN ? 0 : gate) + n0 + e.out_col(j);
+            load_bf16x4(p.b_scale + (long)g * p.b_cols + col, 4, true, sb);
+#pragma unroll
+            for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float t = (float)e.acc[i][j][r] * sa[i];
+                t = t * sb[r];
+                s.f[i][j][r] = s.f[i][j][r] + t;
+              }
+          }
+        }
+        e.zero_acc();
+      }
+    };
+    e.run(smem, nst, on_step);
+    auto raw_of = [&](int i, int j, int r) { return __float_as_int(s.f[i][j][r]); };
+    if (C::SWIGLU) {
+      dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) {
+        return swiglu(s.f[i][j][r] * C::ACC_UNSCALE, s.f[i][j + C::FN][r] * C::ACC_UNSCALE);
+      }, raw_of);
+    } else if (p.epilogue == EPI_RELU2) {
+      dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) {
+        return apply_epi(s.f[i][j][r] * C::ACC_UNSCALE, EPI_RELU2);
+      }, raw_of);
+    } else {
+      dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) { return s.f[i][j][r] * C::ACC_UNSCALE; }, raw_of);
+    }
+  } else {
+    auto nop = [](int) {};
+    e.run(smem, nst, nop);
+    float sa[C::FM];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) sa[i] = load_bf16(p.a_scale + m0 + e.out_row(i));
+    float sb[C::FN2][4];
+#pragma unroll
+    for (int j = 0; j < C::FN2; ++j) {
+      if (!C::SWIGLU && j >= C::FN) continue;
+      load_bf16x4(p.b_scale + (j < C::FN ? 0 : gate) + n0 + e.out_col(j), 4, true, sb[j]);
+    }
+    auto scaled = [&](int i, int j, int r) {
+      float x = (float)e.acc[i][j][r] * sa[i];
+      x = x * sb[j][r];
+      return x * C::ACC_UNSCALE;
+    };
+    auto raw_of = [&](int i, int j, int r) { return e.true_acc(e.acc[i][j][r]); };
+    if (C::SWIGLU) {
+      dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) {
+        return swiglu(scaled(i, j, r), scaled(i, j + C::FN, r));
+      }, raw_of);
+    } else if (p.epilogue == EPI_RELU2) {
+      dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) { return apply_epi(scaled(i, j, r), EPI_RELU2); },
+                     raw_of);
+    } else {
+      dense_store<C>(e, p, m0, n0, scaled, raw_of);
+    }
+  }
+}
+
+}  // namespace shk

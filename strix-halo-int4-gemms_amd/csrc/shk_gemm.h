@@ -367,140 +367,7 @@ __device__ __forceinline__ void dense_tile_coords(int pid, int tiles_m, int tile
   tn = in_grp / gsz;
 }
 
-template <class C>
-__global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
-  const int tiles_m = p.M / C::BM;
-  const int tiles_n = p.N / C::BN;
-  int tm, tn;
-  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
-  const int m0 = tm * C::BM;
-  const int n0 = tn * C::BN;
-
-  RowSource asrc, bsrc;
-  if (C::A_KMAJOR) {  // A [M, K*bits/8]
-    asrc.base0 = p.a + (long)m0 * p.lda;
-  } else {            // A [K*bits/8, M]
-    asrc.base0 = p.a + m0;
-  }
-  asrc.base1 = asrc.base0;
-  asrc.ld = p.lda;
-  asrc.rows_valid = C::BM;
-  const int gate_off = C::SWIGLU ? p.N : 0;
-  if (C::B_KMAJOR) {  // B [b_cols, K*bits/8]
-    bsrc.base0 = p.b + (long)n0 * p.ldb;
-    bsrc.base1 = p.b + (long)(gate_off + n0) * p.ldb;
-  } else {            // B [K*bits/8, b_cols]
-    bsrc.base0 = p.b + n0;
-    bsrc.base1 = p.b + gate_off + n0;
-  }
-  bsrc.ld = p.ldb;
-  bsrc.rows_valid = C::BN;
-
-  Engine<C> e;
-  e.init();
-  const int nst = (p.K + C::BK - 1) / C::BK;
-  auto stage_k = [](int i) { return i * C::BK; };
-  const bool raw = p.out_mode == OUT_I32;
-
-  if (C::SUBCH) {
-    SubAcc<C> s;
-    s.zero();
-    const int S = p.subchannel;
-    auto on_step = [&](int kb, int ke) {
-      if ((ke % S) == 0 || ke >= p.K) {
-        const int g = kb / S;
-        subchannel_flush<C>(
-            e, s, [&](int i) { return p.a_scale + (long)(m0 + e.out_row(i)) * p.scale_cols + g; },
-            [&](int j) {
-              const int col = (j < C::FN ? 0 : gate_off) + n0 + e.out_col(j);
-              return p.b_scale + (long)g * p.b_cols + col;
-            },
-            [](int) { return 4; }, true, raw);
-      }
-    };
-    e.mainloop(smem, asrc, bsrc, nst, stage_k, p.K, p.a_aligned, p.b_aligned, on_step);
-    // Epilogue
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      const int m = m0 + e.out_row(i);
-#pragma unroll
-      for (int j = 0; j < C::FN; ++j) {
-        const int n = n0 + e.out_col(j);
-        float v[4];
-        int rv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (raw) {
-            rv[r] = __float_as_int(s.f[i][j][r]);
-            v[r] = 0.0f;
-          } else {
-            float x = s.f[i][j][r] * C::ACC_UNSCALE;
-            if (C::SWIGLU) {
-              const float g = s.f[i][j + C::FN][r] * C::ACC_UNSCALE;
-              x = swiglu(x, g);
-            } else {
-              x = apply_epi(x, p.epilogue);
-            }
-            v[r] = x;
-            rv[r] = 0;
-          }
-        }
-        const long ldo = (C::SWIGLU && raw) ? 2L * p.N : (long)p.N;
-        store_row4(p.out, (long)m * ldo + n, v, rv, 4, true, p.out_mode);
-        if (C::SWIGLU && raw) {
-          int rg[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rg[r] = __float_as_int(s.f[i][j + C::FN][r]);
-          store_row4(p.out, (long)m * ldo + p.N + n, v, rg, 4, true, p.out_mode);
-        }
-      }
-    }
-  } else {
-    e.mainloop(smem, asrc, bsrc, nst, stage_k, p.K, p.a_aligned, p.b_aligned, [](int, int) {});
-    float sa[C::FM];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) sa[i] = load_bf16(p.a_scale + m0 + e.out_row(i));
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const int n = n0 + e.out_col(j);
-      float sb[4], sg[4];
-      load_bf16x4(p.b_scale + n, 4, true, sb);
-      if (C::SWIGLU) load_bf16x4(p.b_scale + gate_off + n, 4, true, sg);
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i) {
-        const int m = m0 + e.out_row(i);
-        float v[4];
-        int rv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int a = e.acc[i][j][r];
-          rv[r] = e.true_acc(a);
-          float x = (float)a * sa[i];
-          x = x * sb[r];
-          x = x * C::ACC_UNSCALE;
-          if (C::SWIGLU) {
-            float g = (float)e.acc[i][j + C::FN][r] * sa[i];
-            g = g * sg[r];
-            g = g * C::ACC_UNSCALE;
-            x = swiglu(x, g);
-          } else {
-            x = apply_epi(x, p.epilogue);
-          }
-          v[r] = x;
-        }
-        const long ldo = (C::SWIGLU && raw) ? 2L * p.N : (long)p.N;
-        store_row4(p.out, (long)m * ldo + n, v, rv, 4, true, p.out_mode);
-        if (C::SWIGLU && raw) {
-          int rg[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rg[r] = e.true_acc(e.acc[i][j + C::FN][r]);
-          store_row4(p.out, (long)m * ldo + p.N + n, v, rg, 4, true, p.out_mode);
-        }
-      }
-    }
-  }
-}
+// dense_gemm_kernel is defined in shk_dense.h on the pipelined engine.
 
 // ===========================================================================
 // Ragged forward: out[rows of group g] = lhs[rows] @ rhs[g]

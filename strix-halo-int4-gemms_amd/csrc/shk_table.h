@@ -7,7 +7,7 @@
 #include <vector>
 
 #include "../../include/strix_halo_gfx950.h"
-#include "shk_gemm.h"
+#include "shk_dense.h"
 
 namespace shk {
 
