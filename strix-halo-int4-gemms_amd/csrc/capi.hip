@@ -216,6 +216,10 @@ int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintp
   p.a_aligned = a_km ? (aligned(a, 16) && p.lda % 16 == 0) : (aligned(a, 8) && p.lda % 8 == 0);
   p.b_aligned = b_km ? (aligned(b, 16) && p.ldb % 16 == 0) : (aligned(b, 8) && p.ldb % 8 == 0);
   p.group_m = d.group_size_m;
+  // Operands are addressed with 32-bit buffer offsets.
+  if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
+      (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))
+    return fail("dense operands must each be smaller than 4 GiB");
   if (!p.a_aligned || !p.b_aligned)
     return fail(std::string("dense kernels need ") + (a_km ? "16" : "8") + "-byte aligned A and " +
                 (b_km ? "16" : "8") + "-byte aligned B data pointers");

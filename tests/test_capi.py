@@ -1,0 +1,167 @@
+"""C ABI of libamd_strix_halo_kernels_gfx950.so, checked without a GPU.
+
+The library must load on a machine without a GPU, export every symbol that
+include/strix_halo_gfx950.h declares, report its status, describe its kernel
+table, and reject bad launches with rc=1 and a readable last_error before it
+touches the HIP runtime (the reference's dispatcher contract,
+native/src/dispatch.cpp:18-23, 206-283).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import threading
+from pathlib import Path
+
+import pytest
+
+from amd_strix_halo_kernels import kernel_table as kt
+from amd_strix_halo_kernels import native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "strix_halo_gfx950.h"
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return native.load_dispatch_library()
+
+
+def _declared_functions() -> list[str]:
+    # declarations start a line with a return type: "int name(", "const char* name("
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:const\s+)?\w+\s*\*?\s*(amd_strix_halo_kernels_\w+)\(", text, re.M)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_status_functions(lib):
+    assert lib.amd_strix_halo_kernels_dispatch_version() == 2
+    assert lib.amd_strix_halo_kernels_has_compiled_code_objects() == 1
+    assert lib.amd_strix_halo_kernels_arch() == b"gfx950"
+    assert lib.amd_strix_halo_kernels_has_hip_runtime() in (0, 1)
+    assert lib.amd_strix_halo_kernels_has_linked_kernels() in (0, 1)
+    status = native.dispatch_runtime_status()
+    assert status.dispatch_version == 2 and status.has_compiled_code_objects
+
+
+def test_kernel_table_matches_python_mirror(lib):
+    table = native.library_kernel_table(lib)
+    assert table == kt.TABLE
+    assert [d.index for d in table] == list(range(len(table)))
+    desc = native._Desc()
+    assert lib.amd_strix_halo_kernels_kernel_table_entry(len(table), ctypes.byref(desc)) == 1
+    assert b"out of range" in lib.amd_strix_halo_kernels_last_error()
+
+
+def _dense_index(**want) -> int:
+    for d in kt.entries(kt.FAMILY_DENSE):
+        if all(getattr(d, k) == v for k, v in want.items()):
+            return d.index
+    raise LookupError(want)
+
+
+def _gemm(lib, index, m, n, k, *, sub=0, epi=0, mode=0, out=FAKE, ptr=FAKE):
+    return lib.amd_strix_halo_kernels_launch_gemm(index, 0, 0, ptr, ptr, ptr, ptr, out, m, n, k, sub, epi, mode)
+
+
+def _err(lib) -> str:
+    return lib.amd_strix_halo_kernels_last_error().decode()
+
+
+def test_gemm_rejects_bad_index_and_family(lib):
+    assert _gemm(lib, len(kt.TABLE) + 5, 64, 64, 64) == 1
+    assert "out of range" in _err(lib)
+    fwd = kt.entries(kt.FAMILY_RAGGED_FWD)[0].index
+    assert _gemm(lib, fwd, 64, 64, 64) == 1
+    assert "another kernel family" in _err(lib)
+
+
+def test_gemm_rejects_null_pointers(lib):
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
+    assert _gemm(lib, idx, 64, 64, 64, ptr=0) == 1
+    assert "non-null" in _err(lib)
+
+
+def test_gemm_tile_multiple_messages_follow_the_reference(lib):
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, scale_mode=0, epilogue_kind=0)
+    assert _gemm(lib, idx, 100, 256, 128) == 1
+    assert "M=100 is not divisible by BLOCK_M=256" in _err(lib)
+    assert _gemm(lib, idx, 256, 100, 96) == 1
+    msg = _err(lib)
+    assert "N=100 is not divisible by BLOCK_N=256" in msg
+    assert "K=96 is not divisible by BLOCK_K*SPLIT_K=128" in msg
+    assert _gemm(lib, idx, 0, 256, 128) == 1
+    assert "must be positive" in _err(lib)
+
+
+def test_gemm_rejects_mismatched_modes(lib):
+    pc = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
+    sc = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=1, epilogue_kind=0,
+                      min_subchannel=64)
+    assert _gemm(lib, pc, 64, 64, 64, sub=64) == 1
+    assert "subchannel = 0" in _err(lib)
+    assert _gemm(lib, sc, 64, 64, 128, sub=32) == 1
+    assert "not served" in _err(lib)
+    assert _gemm(lib, pc, 64, 64, 64, epi=2) == 1
+    assert "epilogue" in _err(lib)
+    assert _gemm(lib, pc, 64, 64, 64, mode=7) == 1
+    assert "output mode" in _err(lib)
+    assert _gemm(lib, pc, 64, 64, 262144) == 1
+    assert "K <= 131072" in _err(lib)
+    assert _gemm(lib, pc, 64, 64, 64, out=FAKE + 4) == 1
+    assert "aligned" in _err(lib)
+
+
+def test_ragged_entry_points_validate_before_launch(lib):
+    I = lib.amd_strix_halo_kernels_ragged_group_info
+    assert I(0, 0, FAKE, 3, 32, 12, 8, FAKE, FAKE, None) == 1
+    assert "multiple of align_tile" in _err(lib)
+    assert I(0, 0, FAKE, 1 << 20, 32, 8, 8, FAKE, FAKE, None) == 1
+    assert "groups are supported" in _err(lib)
+    bwd = kt.entries(kt.FAMILY_RAGGED_BWD)[0].index
+    B = lib.amd_strix_halo_kernels_launch_ragged_bwd
+    assert B(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 16, 16, 2, 0, 0, 0) == 1
+    assert "split_k" in _err(lib)
+    assert B(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 16, 16, 2, 0, 1, 0) == 1
+    assert "fp32" in _err(lib)
+    fwd = kt.entries(kt.FAMILY_RAGGED_FWD)[0].index
+    F = lib.amd_strix_halo_kernels_launch_ragged_fwd
+    assert F(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 16, 16, 16, 2, 32, 0) == 1
+    assert "subchannel = 0" in _err(lib)
+
+
+@pytest.mark.parametrize("rows,groups,tile,align", [(8192, 8, 64, 8), (0, 3, 16, 8), (17, 40, 16, 16), (1, 1, 128, 8)])
+def test_task_capacity_bounds_the_task_list(lib, rows, groups, tile, align):
+    from oracle import ref
+
+    cap = lib.amd_strix_halo_kernels_ragged_task_capacity(rows, groups, tile, align)
+    assert cap == rows // tile + 2 * groups + 1
+    # worst case: every group starts one row past an aligned boundary
+    r = ref.rng(rows + groups)
+    for _ in range(20):
+        sizes = r.multinomial(rows, r.dirichlet(ref.np.ones(groups))) if rows else ref.np.zeros(groups, int)
+        assert ref.calculate_group_info(sizes, tile, align_tile=align).num_tasks <= cap
+
+
+def test_last_error_is_thread_local(lib):
+    assert _gemm(lib, -1, 64, 64, 64) == 1
+    mine = _err(lib)
+    seen = {}
+
+    def other():
+        idx = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
+        _gemm(lib, idx, 64, 64, 64, ptr=0)
+        seen["msg"] = _err(lib)
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert "non-null" in seen["msg"]
+    assert _err(lib) == mine
