@@ -65,9 +65,11 @@ class KernelDesc:
         return size is not None and self.min_subchannel <= size <= self.max_subchannel
 
 
-def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8):
+def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0):
+    # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
+    # source bytes per tile row; 0: register-staged engine, two widened stages.
     brows = 2 * bn if swiglu else bn
-    lds = 2 * (bm * bk + brows * bk)
+    lds = pipe * (bm + brows) * 64 if pipe else 2 * (bm * bk + brows * bk)
     return KernelDesc(
         index=index,
         family=family,
@@ -81,7 +83,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         block_n=bn,
         block_k=bk,
         num_waves=wm * wn,
-        num_stages=2,
+        num_stages=pipe or 2,
         lds_bytes=lds,
         group_size_m=group_m,
     )
@@ -97,10 +99,10 @@ def _build() -> tuple[KernelDesc, ...]:
         big_bk = 128 if bits == 4 else 64
         for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
             d = dict(family=FAMILY_DENSE, bits=bits, layout=layout)
-            add(**d, bm=256, bn=256, bk=big_bk, wm=2, wn=2)
+            add(**d, bm=256, bn=256, bk=big_bk, wm=2, wn=2, pipe=4)
+            add(**d, bm=256, bn=128, bk=big_bk, wm=2, wn=2, swiglu=True, pipe=4)
             add(**d, bm=128, bn=128, bk=64, wm=2, wn=2)
             add(**d, bm=64, bn=64, bk=64, wm=2, wn=2)
-            add(**d, bm=256, bn=128, bk=big_bk, wm=2, wn=2, swiglu=True)
             add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, swiglu=True)
             add(**d, bm=256, bn=128, bk=big_bk, wm=4, wn=2, subch=True)
             add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True)

@@ -48,13 +48,19 @@ def hipcc() -> str:
     return path
 
 
+# The direct-to-LDS dense objects hold 256 accumulators per lane; the
+# iterative ILP machine scheduler keeps them in place in AGPRs, where the
+# default scheduler's allocation rotates them through copies every K step.
+DMA_FLAGS = ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+
+
 def translation_units() -> list[tuple[str, Path, list[str]]]:
     units: list[tuple[str, Path, list[str]]] = []
     for bits in (4, 8):
         for layout in (0, 1, 2):
-            units.append(
-                (f"dense_{bits}_{layout}", CSRC / "k_dense.hip", [f"-DSHK_BITS={bits}", f"-DSHK_LAYOUT={layout}"])
-            )
+            defs = [f"-DSHK_BITS={bits}", f"-DSHK_LAYOUT={layout}"]
+            units.append((f"dense_dma_{bits}_{layout}", CSRC / "k_dense.hip", [*defs, "-DSHK_DENSE_DMA=1", *DMA_FLAGS]))
+            units.append((f"dense_{bits}_{layout}", CSRC / "k_dense.hip", [*defs, "-DSHK_DENSE_DMA=0"]))
     for layout in (0, 1, 2, 3):
         units.append((f"ragged_{layout}", CSRC / "k_ragged.hip", [f"-DSHK_LAYOUT={layout}"]))
     units.append(("capi", CSRC / "capi.hip", []))

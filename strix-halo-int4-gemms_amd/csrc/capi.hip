@@ -28,11 +28,17 @@ int fail_hip(const char* what, hipError_t err) {
 const std::vector<Entry>& table() {
   static const std::vector<Entry> t = [] {
     std::vector<Entry> v;
+    shk::append_dense_dma_4_0(v);
     shk::append_dense_4_0(v);
+    shk::append_dense_dma_4_1(v);
     shk::append_dense_4_1(v);
+    shk::append_dense_dma_4_2(v);
     shk::append_dense_4_2(v);
+    shk::append_dense_dma_8_0(v);
     shk::append_dense_8_0(v);
+    shk::append_dense_dma_8_1(v);
     shk::append_dense_8_1(v);
+    shk::append_dense_dma_8_2(v);
     shk::append_dense_8_2(v);
     shk::append_ragged_0(v);
     shk::append_ragged_1(v);
@@ -213,16 +219,21 @@ int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintp
   p.scale_cols = subchannel > 0 ? (k + subchannel - 1) / subchannel : 1;
   p.epilogue = epilogue == SHK_EPILOGUE_RELU2 ? shk::EPI_RELU2 : shk::EPI_NONE;
   p.out_mode = out_mode;
-  p.a_aligned = a_km ? (aligned(a, 16) && p.lda % 16 == 0) : (aligned(a, 8) && p.lda % 8 == 0);
-  p.b_aligned = b_km ? (aligned(b, 16) && p.ldb % 16 == 0) : (aligned(b, 8) && p.ldb % 8 == 0);
+  // 16-byte pieces for K-major operands and for every operand of the
+  // direct-to-LDS tiles (more than two stages); 8-byte rows otherwise.
+  const bool dma = d.num_stages > 2;
+  const int a_need = (a_km || dma) ? 16 : 8;
+  const int b_need = (b_km || dma) ? 16 : 8;
+  p.a_aligned = aligned(a, a_need) && p.lda % a_need == 0;
+  p.b_aligned = aligned(b, b_need) && p.ldb % b_need == 0;
   p.group_m = d.group_size_m;
   // Operands are addressed with 32-bit buffer offsets.
   if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
       (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))
     return fail("dense operands must each be smaller than 4 GiB");
   if (!p.a_aligned || !p.b_aligned)
-    return fail(std::string("dense kernels need ") + (a_km ? "16" : "8") + "-byte aligned A and " +
-                (b_km ? "16" : "8") + "-byte aligned B data pointers");
+    return fail("kernel " + std::to_string(kernel_index) + " needs " + std::to_string(a_need) +
+                "-byte aligned A and " + std::to_string(b_need) + "-byte aligned B data pointers");
   const long tiles = (long)(m / d.block_m) * (n / d.block_n);
   if (tiles > 0x7FFFFFFFL) return fail("too many output tiles");
 

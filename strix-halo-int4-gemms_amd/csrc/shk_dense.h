@@ -2,9 +2,12 @@
 // operands; both checked on the host).
 #pragma once
 
-#include "shk_fast.h"
+#include "shk_dma.h"
 
 namespace shk {
+
+template <class C>
+using DenseEngine = typename std::conditional<(C::PIPE > 0), DmaEngine<C>, FastEngine<C>>::type;
 
 // Writes one tile's results.  `value(i, j, r)` gives the scaled, epilogue-
 // applied fp32 value, `raw(i, j, r)` the int32 written in verification mode.
@@ -51,25 +54,11 @@ __global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
   dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
-  const unsigned long long kbytes = (unsigned long long)p.K * C::BITS / 8;
   const int gate = C::SWIGLU ? p.N : 0;
 
-  FastEngine<C> e;
+  DenseEngine<C> e;
   e.init_reads();
-  if (C::A_KMAJOR) {  // A [M, kbytes]
-    e.ra = make_rsrc(p.a + (long)m0 * p.lda, (unsigned long long)(p.M - m0) * p.lda);
-    e.sa.init((uint32_t)p.lda, 0);
-  } else {            // A [kbytes, M]
-    e.ra = make_rsrc(p.a + m0, kbytes * p.M - m0);
-    e.sa.init((uint32_t)p.lda, 0);
-  }
-  if (C::B_KMAJOR) {  // B [b_cols, kbytes]
-    e.rb = make_rsrc(p.b + (long)n0 * p.ldb, (unsigned long long)(p.b_cols - n0) * p.ldb);
-    e.sb.init((uint32_t)p.ldb, (uint32_t)gate);
-  } else {            // B [kbytes, b_cols]
-    e.rb = make_rsrc(p.b + n0, kbytes * p.b_cols - n0);
-    e.sb.init((uint32_t)p.ldb, (uint32_t)gate);
-  }
+  e.setup(p, m0, n0, gate);
   const int nst = p.K / C::BK;
   const bool raw = p.out_mode == OUT_I32;
 

@@ -266,6 +266,22 @@ struct FastEngine {
   }
   __device__ __forceinline__ int true_acc(int v) const { return v >> C::ACC_SHIFT; }
 
+  __device__ __forceinline__ void setup(const DenseArgs& p, int m0, int n0, int gate) {
+    const unsigned long long kbytes = (unsigned long long)p.K * C::BITS / 8;
+    if (C::A_KMAJOR) {  // A [M, kbytes]
+      ra = make_rsrc(p.a + (long)m0 * p.lda, (unsigned long long)(p.M - m0) * p.lda);
+    } else {            // A [kbytes, M]
+      ra = make_rsrc(p.a + m0, kbytes * p.M - m0);
+    }
+    sa.init((uint32_t)p.lda, 0);
+    if (C::B_KMAJOR) {  // B [b_cols, kbytes]
+      rb = make_rsrc(p.b + (long)n0 * p.ldb, (unsigned long long)(p.b_cols - n0) * p.ldb);
+    } else {            // B [kbytes, b_cols]
+      rb = make_rsrc(p.b + n0, kbytes * p.b_cols - n0);
+    }
+    sb.init((uint32_t)p.ldb, (uint32_t)gate);
+  }
+
   // Stage-source position for the stagers (bytes along K for K-major sources,
   // first source row for MN-major sources; the same number for both).
   static __device__ __forceinline__ uint32_t kpos(int stage) { return (uint32_t)stage * (C::BK * C::BITS / 8); }

@@ -32,7 +32,7 @@ enum OutMode : int { OUT_BF16 = 0, OUT_F32 = 1, OUT_I32 = 2 };
 enum EpiKind : int { EPI_NONE = 0, EPI_RELU2 = 1 };
 
 template <int BITS_, bool A_KMAJOR_, bool B_KMAJOR_, int BM_, int BN_, int BK_, int WM_, int WN_,
-          bool SWIGLU_, bool SUBCH_, int MK_, bool GUARDED_ = true>
+          bool SWIGLU_, bool SUBCH_, int MK_, bool GUARDED_ = true, int PIPE_ = 0>
 struct Cfg {
   static constexpr int BITS = BITS_;
   static constexpr bool A_KMAJOR = A_KMAJOR_;
@@ -49,6 +49,9 @@ struct Cfg {
   // rows, N tails, masked K); unguarded ones (dense, tile-multiple shapes with
   // aligned operands checked on the host) only have the vector path.
   static constexpr bool GUARDED = GUARDED_;
+  // PIPE > 0 selects the direct-to-LDS engine (shk_dma.h) with a ring of PIPE
+  // packed stages; 0 the register-staged engine with two widened stages.
+  static constexpr int PIPE = PIPE_;
   static constexpr int NT = 64 * WM * WN;
   static constexpr int BROWS = SWIGLU ? 2 * BN : BN;  // B rows staged per stage
   static constexpr int BHALF = BN;
@@ -60,7 +63,8 @@ struct Cfg {
   static constexpr int A_STAGE = BM * BK;
   static constexpr int B_STAGE = BROWS * BK;
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int LDS_BYTES = 2 * STAGE;
+  static constexpr int LDS_BYTES = PIPE ? PIPE * (BM + BROWS) * 64 : 2 * STAGE;
+  static constexpr int NUM_STAGES = PIPE ? PIPE : 2;
   static constexpr float ACC_UNSCALE = (BITS == 4) ? (1.0f / 256.0f) : 1.0f;
   static constexpr int ACC_SHIFT = (BITS == 4) ? 8 : 0;
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");

@@ -53,7 +53,7 @@ constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
       C::BN,
       C::BK,
       C::NT / 64,
-      2,
+      C::NUM_STAGES,
       C::LDS_BYTES,
       group_m,
   };
@@ -73,7 +73,14 @@ Entry bwd_entry(int layout) {
 }
 
 // Each kernel translation unit appends its entries in a fixed order
-// (append_dense_<bits>_<layout>, append_ragged_<layout>).
+// (append_dense_dma_<bits>_<layout>, append_dense_<bits>_<layout>,
+// append_ragged_<layout>).
+void append_dense_dma_4_0(std::vector<Entry>& t);
+void append_dense_dma_4_1(std::vector<Entry>& t);
+void append_dense_dma_4_2(std::vector<Entry>& t);
+void append_dense_dma_8_0(std::vector<Entry>& t);
+void append_dense_dma_8_1(std::vector<Entry>& t);
+void append_dense_dma_8_2(std::vector<Entry>& t);
 void append_dense_4_0(std::vector<Entry>& t);
 void append_dense_4_1(std::vector<Entry>& t);
 void append_dense_4_2(std::vector<Entry>& t);
