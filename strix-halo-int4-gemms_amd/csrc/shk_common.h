@@ -75,6 +75,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Two fp32 values -> packed bf16 pair with v_cvt_pk_bf16_f32 (round to
+// nearest even, subnormals kept).  Only for values that are not NaN: the
+// instruction keeps a NaN's payload where torch writes 0x7FC0.
+typedef float shk_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 shk_bf2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_nonan(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(shk_f2{a, b}, shk_bf2));
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }

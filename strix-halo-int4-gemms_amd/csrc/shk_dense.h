@@ -11,8 +11,11 @@ using DenseEngine = typename std::conditional<(C::PIPE > 0), DmaEngine<C>, FastE
 
 // Writes one tile's results.  `value(i, j, r)` gives the scaled, epilogue-
 // applied fp32 value, `raw(i, j, r)` the int32 written in verification mode.
+// `no_nan` (uniform across the wave) promises that no value is NaN, which
+// allows the hardware bf16 conversion.
 template <class C, class E, class Value, class Raw>
-__device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int m0, int n0, Value value, Raw raw) {
+__device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int m0, int n0, Value value, Raw raw,
+                                            bool no_nan = false) {
   const bool swiglu_raw = C::SWIGLU && p.out_mode == OUT_I32;
   const long ldo = swiglu_raw ? 2L * p.N : (long)p.N;
   if (p.out_mode == OUT_I32) {
@@ -36,12 +39,21 @@ __device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int 
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = value(i, j, r);
       if (p.out_mode == OUT_BF16) {
-        const uint32_t lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
-        const uint32_t hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+        uint32_t lo, hi;
+        if (no_nan) {
+          lo = pack_bf16x2_nonan(v[0], v[1]);
+          hi = pack_bf16x2_nonan(v[2], v[3]);
+        } else {
+          lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+          hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+        }
         *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + idx) = make_uint2(lo, hi);
       } else {
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + idx) = make_float4(v[0], v[1], v[2], v[3]);
       }
+      // one fragment at a time: keeps the accumulator reads from being
+      // hoisted ahead of their use, which would need more VGPRs than exist
+      __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -125,11 +137,22 @@ __global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
       if (!C::SWIGLU && j >= C::FN) continue;
       load_bf16x4(p.b_scale + (j < C::FN ? 0 : gate) + n0 + e.out_col(j), 4, true, sb[j]);
     }
+    // (float(acc) * a_scale) * b_scale on the true accumulator (the shift
+    // removes the int4 widening factor exactly).
     auto scaled = [&](int i, int j, int r) {
-      float x = (float)e.acc[i][j][r] * sa[i];
-      x = x * sb[j][r];
-      return x * C::ACC_UNSCALE;
+      float x = (float)e.true_acc(e.acc[i][j][r]) * sa[i];
+      return x * sb[j][r];
     };
+    // Finite scales times a finite int32 sum give no NaN (at most +-inf),
+    // and neither does ReLU^2 of such a value.
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) finite = finite && (__float_as_uint(sa[i]) & 0x7F800000u) != 0x7F800000u;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) finite = finite && (__float_as_uint(sb[j][r]) & 0x7F800000u) != 0x7F800000u;
+    const bool no_nan = __all(finite);
     auto raw_of = [&](int i, int j, int r) { return e.true_acc(e.acc[i][j][r]); };
     if (C::SWIGLU) {
       dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) {
@@ -137,9 +160,9 @@ __global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
       }, raw_of);
     } else if (p.epilogue == EPI_RELU2) {
       dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) { return apply_epi(scaled(i, j, r), EPI_RELU2); },
-                     raw_of);
+                     raw_of, no_nan);
     } else {
-      dense_store<C>(e, p, m0, n0, scaled, raw_of);
+      dense_store<C>(e, p, m0, n0, scaled, raw_of, no_nan);
     }
   }
 }

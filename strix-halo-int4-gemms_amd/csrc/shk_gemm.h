@@ -286,9 +286,10 @@ __device__ __forceinline__ void subchannel_flush(Engine<C>& e, SubAcc<C>& s, ARo
   e.zero_acc();
 }
 
+// relu keeps NaN (torch.relu does): only values below zero become zero.
 __device__ __forceinline__ float apply_epi(float v, int epi) {
   if (epi == EPI_RELU2) {
-    v = v > 0.0f ? v : 0.0f;
+    v = v < 0.0f ? 0.0f : v;
     v = v * v;
   }
   return v;

@@ -181,3 +181,45 @@ def test_shape_and_layout_errors(device):
                         b_scale=torch.ones(96, dtype=torch.bfloat16, device=device))
     with pytest.raises(ValueError, match="require a_scale and b_scale"):
         shk.explicit_mm(a[:, :32], b[:, :64].contiguous(), kernel=kernel)
+
+
+# bf16 scale bit patterns that exercise the store path: subnormal, smallest
+# normal, largest finite, +-inf, NaN with payload and negative NaN, signed
+# zero, one, and values whose products land in the fp32 subnormal range.
+SPECIAL_SCALES = np.array([0x0001, 0x0080, 0x007F, 0x7F7F, 0x7F80, 0xFF80, 0x7FC1, 0xFFC0, 0x0000, 0x8000, 0x3F80,
+                           0x0200, 0x1000, 0x2000, 0xBF80], dtype=np.uint16)
+
+
+def _sprinkle(scales, seed, every):
+    s = scales.copy()
+    r = ref.rng(seed)
+    pos = np.arange(0, s.size, every)
+    s.reshape(-1)[pos] = SPECIAL_SCALES[r.integers(0, SPECIAL_SCALES.size, size=pos.size)]
+    return s
+
+
+@pytest.mark.parametrize("kernel", [k for k in shk.default_registry.all() if k.scale.mode is shk.ScaleMode.PER_CHANNEL
+                                    and k.layout is shk.GemmLayout.NN], ids=lambda k: k.kernel_id)
+def test_special_scale_values_store_like_torch(kernel, device):
+    """Per-channel bf16 outputs stay bit-exact (NaN canonical 0x7FC0, subnormals
+    kept, overflow to inf) when the scales hold special values."""
+    bits, layout, sub, epi = _kernel_params(kernel)
+    m, n = 2 * kernel.tile.block_m, 2 * kernel.tile.block_n
+    k = 2 * kernel.tile.block_k
+    seed = stable_seed("special", kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=None,
+                                                 swiglu=epi == "swiglu")
+    sa = _sprinkle(sa, seed, 5)
+    sb = _sprinkle(sb, seed + 1, 7)
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q))
+    with np.errstate(over="ignore", invalid="ignore", under="ignore"):
+        want = ref.reference_gemm_bf16(a_arg, b_arg, bits=bits, layout=layout, a_scale=sa, b_scale=sb,
+                                       subchannel=None, epilogue=epi)
+    nan_want = (want & 0x7FFF) > 0x7F80
+    assert np.array_equal(got[nan_want], want[nan_want]), "NaN results must be the canonical 0x7FC0"
+    if epi == "swiglu":
+        assert max_ulp(got[~nan_want], want[~nan_want]) <= ULP_TOL
+    else:
+        assert np.array_equal(got, want)
