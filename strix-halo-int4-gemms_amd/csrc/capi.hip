@@ -231,6 +231,10 @@ int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintp
   if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
       (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))
     return fail("dense operands must each be smaller than 4 GiB");
+  // Output stores address a tile's rows with 32-bit offsets from its first
+  // element: 256 rows of fp32 (or int32 [up | gate]) must stay below 4 GiB.
+  if ((unsigned long long)b_cols * 4ull * 256ull >= (1ull << 32))
+    return fail("dense output rows are limited to 4194304 bytes");
   if (!p.a_aligned || !p.b_aligned)
     return fail("kernel " + std::to_string(kernel_index) + " needs " + std::to_string(a_need) +
                 "-byte aligned A and " + std::to_string(b_need) + "-byte aligned B data pointers");

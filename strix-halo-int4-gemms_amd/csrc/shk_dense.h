@@ -9,16 +9,62 @@ namespace shk {
 template <class C>
 using DenseEngine = typename std::conditional<(C::PIPE > 0), DmaEngine<C>, FastEngine<C>>::type;
 
+// Writes the scaled values of one tile: `value(i, j, r)` gives the
+// scaled, epilogue-applied fp32 value.  MODE is OUT_BF16 or OUT_F32; NO_NAN
+// promises that no value is NaN, which allows the hardware bf16 conversion.
+template <class C, int MODE, bool NO_NAN, class E, class Value>
+__device__ __forceinline__ void store_values(const E& e, const DenseArgs& p, int m0, int n0, Value value) {
+  // Buffer stores: the tile's first element is the resource base, the lane's
+  // row and column inside a fragment are its offset, the fragment row block
+  // travels in the scalar offset and the fragment column in the immediate,
+  // so a store needs no address arithmetic.  The host keeps 256 output rows
+  // of fp32 below 4 GiB.
+  constexpr uint32_t ESZ = MODE == OUT_BF16 ? 2 : 4;
+  const unsigned long long first = (unsigned long long)m0 * p.N + n0;
+  const rsrc_t r = make_rsrc(static_cast<uint8_t*>(p.out) + first * ESZ,
+                             ((unsigned long long)p.M * p.N - first) * ESZ);
+  const uint32_t voff = ((uint32_t)e.out_row(0) * (uint32_t)p.N + (uint32_t)e.out_col(0)) * ESZ;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+    const uint32_t soff = (uint32_t)(16 * i) * (uint32_t)p.N * ESZ;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = value(i, j, q);
+      const uint32_t off = voff + 16u * j * ESZ;
+      if constexpr (MODE == OUT_BF16) {
+        uint32_t lo, hi;
+        if constexpr (NO_NAN) {
+          lo = pack_bf16x2_nonan(v[0], v[1]);
+          hi = pack_bf16x2_nonan(v[2], v[3]);
+        } else {
+          lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+          hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)lo, (int)hi}, r, off, soff, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(v4i{__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]),
+                                                   __float_as_int(v[3])},
+                                               r, off, soff, 0);
+      }
+      // one fragment at a time: keeps the accumulator reads from being
+      // hoisted ahead of their use, which would need more VGPRs than exist
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 // Writes one tile's results.  `value(i, j, r)` gives the scaled, epilogue-
 // applied fp32 value, `raw(i, j, r)` the int32 written in verification mode.
 // `no_nan` (uniform across the wave) promises that no value is NaN, which
-// allows the hardware bf16 conversion.
+// allows the hardware bf16 conversion.  Each output mode is its own
+// straight-line store sequence.
 template <class C, class E, class Value, class Raw>
 __device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int m0, int n0, Value value, Raw raw,
                                             bool no_nan = false) {
-  const bool swiglu_raw = C::SWIGLU && p.out_mode == OUT_I32;
-  const long ldo = swiglu_raw ? 2L * p.N : (long)p.N;
   if (p.out_mode == OUT_I32) {
+    const long ldo = C::SWIGLU ? 2L * p.N : (long)p.N;
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -28,33 +74,13 @@ __device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int 
         int* o = reinterpret_cast<int*>(p.out) + (long)(m0 + e.out_row(i)) * ldo + col;
         *reinterpret_cast<int4*>(o) = make_int4(raw(i, j, 0), raw(i, j, 1), raw(i, j, 2), raw(i, j, 3));
       }
-    return;
+  } else if (p.out_mode == OUT_F32) {
+    store_values<C, OUT_F32, false>(e, p, m0, n0, value);
+  } else if (no_nan) {
+    store_values<C, OUT_BF16, true>(e, p, m0, n0, value);
+  } else {
+    store_values<C, OUT_BF16, false>(e, p, m0, n0, value);
   }
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const long idx = (long)(m0 + e.out_row(i)) * p.N + n0 + e.out_col(j);
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = value(i, j, r);
-      if (p.out_mode == OUT_BF16) {
-        uint32_t lo, hi;
-        if (no_nan) {
-          lo = pack_bf16x2_nonan(v[0], v[1]);
-          hi = pack_bf16x2_nonan(v[2], v[3]);
-        } else {
-          lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
-          hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
-        }
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + idx) = make_uint2(lo, hi);
-      } else {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + idx) = make_float4(v[0], v[1], v[2], v[3]);
-      }
-      // one fragment at a time: keeps the accumulator reads from being
-      // hoisted ahead of their use, which would need more VGPRs than exist
-      __builtin_amdgcn_sched_barrier(0);
-    }
 }
 
 template <class C>
@@ -126,8 +152,7 @@ __global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
       dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) { return s.f[i][j][r] * C::ACC_UNSCALE; }, raw_of);
     }
   } else {
-    auto nop = [](int) {};
-    e.run(smem, nst, nop);
+    // the scales are loaded before the K loop so their latency is hidden
     float sa[C::FM];
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) sa[i] = load_bf16(p.a_scale + m0 + e.out_row(i));
@@ -137,6 +162,8 @@ __global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
       if (!C::SWIGLU && j >= C::FN) continue;
       load_bf16x4(p.b_scale + (j < C::FN ? 0 : gate) + n0 + e.out_col(j), 4, true, sb[j]);
     }
+    auto nop = [](int) {};
+    e.run(smem, nst, nop);
     // (float(acc) * a_scale) * b_scale on the true accumulator (the shift
     // removes the int4 widening factor exactly).
     auto scaled = [&](int i, int j, int r) {

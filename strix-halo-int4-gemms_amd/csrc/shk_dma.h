@@ -271,6 +271,18 @@ struct DmaEngine {
     else ob.issue_one(rsb, OB::soff(st, ldb), base + A_BYTES, wave, b - OA::BLK);
   }
 
+  // Waits until at most n stages of this wave's DMA loads are outstanding
+  // (n = 0 .. P-1).
+  static __device__ __forceinline__ void wait_stages(int n) {
+    static_assert(P <= 5, "wait_stages covers rings of up to five stages");
+    if (n <= 0) wait_vmcnt<0>();
+    else if (n == 1) wait_vmcnt<DPW>();
+    else if (n == 2) wait_vmcnt<(P > 2 ? 2 : 1) * DPW>();
+    else if (n == 3) wait_vmcnt<(P > 3 ? 3 : 1) * DPW>();
+    else wait_vmcnt<(P > 4 ? 4 : 1) * DPW>();
+  }
+  static __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+
   // Moves the read offsets to the next ring slot.
   __device__ __forceinline__ void advance_reads() {
     const uint32_t delta = slot == P - 1 ? (uint32_t)(-(P - 1) * STAGE) : (uint32_t)STAGE;
@@ -322,14 +334,16 @@ struct DmaEngine {
   template <int S>
   static __device__ __forceinline__ v4i operand(const v4i& f) { return f; }
 
-  // Opens stage k: waits for this wave's DMA of stage k+1, then the barrier
+  // Opens stage k: waits for this wave's DMA of stage k+1 (loads are only
+  // issued for stages that exist, so near the end fewer are outstanding),
+  // then the barrier
   // (stage k+1 complete in LDS; every wave has read all of stage k, whose
   // fragments are in registers), issues the loads of stage k+P into stage
   // k's slot and moves the reads to stage k+1.
   __device__ __forceinline__ void open_stage(uint8_t* smem, int k, int nst) {
-    wait_vmcnt<(P - 2) * DPW>();
+    wait_stages(imin(P - 2, nst - 2 - k));
     __syncthreads();
-    dma_stage(smem, k + P < nst ? k + P : nst - 1, slot);
+    if (k + P < nst) dma_stage(smem, k + P, slot);
     advance_reads();
   }
 
@@ -370,7 +384,9 @@ struct DmaEngine {
   // one wave then co-issues the VALU work with its MFMAs, and a load placed
   // right after an MFMA (before the VALU) costs no MFMA issue slot.  The
   // LDS reads here are invisible to the compiler's wait-count tracking, so
-  // every step starts with an explicit s_waitcnt lgkmcnt(0).
+  // each fragment unit waits explicitly (unit_wait) for the read it widens;
+  // the loop has no other LGKM traffic (no scalar loads) that could make
+  // the in-order count inexact.
   //
   // Widening one packed fragment (dwords x0, x1) takes six VALU in three
   // parts:
@@ -523,12 +539,34 @@ struct DmaEngine {
     }
   }
 
+  // LDS reads issued in step S by units lo..hi (fragments refilled there).
+  template <int S>
+  static constexpr int reads_in(int lo, int hi) {
+    int n = 0;
+    for (int f = lo; f <= hi; ++f) n += refill_kind<S>(f) != 0;
+    return n;
+  }
+  // lgkmcnt that unit F of step S waits for before widening fragment F: the
+  // LDS reads issued after the one that brought fragment F's packed bytes.
+  // Those came one step earlier, except the K-major stage fragments widened
+  // at step 0, whose read was two steps earlier.  The refill of fragment f
+  // is issued by unit f+1 (the tail for the last fragment).
+  template <int S, int F>
+  static constexpr int unit_wait() {
+    constexpr int NF = C::FN2 + C::FM;
+    constexpr bool KM = F < C::FN2 ? C::B_KMAJOR : C::A_KMAJOR;
+    const int after = (KM && S == 0) ? reads_in<1 - S>(0, NF - 1) : reads_in<1 - S>(F + 1, NF - 1);
+    return after + reads_in<S>(0, F - 2);
+  }
+
   // Fragment unit F of an int4 step: MFMAs 3F..3F+2 widen fragment F of the
   // next operand set; the first also refills fragment F-1's packed
   // registers, the second issues DMA block F at the stage's first step.
-  template <int CUR, int S, int F>
+  template <int CUR, int S, bool DMA, int F>
   __device__ __forceinline__ void unit(uint32_t lds0) {
     constexpr int NXT = 1 - CUR;
+    constexpr int WAIT = unit_wait<S, F>();
+    if constexpr (WAIT < 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(WAIT) : "memory");
     const uint2 x = next_packed<S>(F);
     uint32_t t0, t1, lo0, hi0, lo1, hi1;
     constexpr int RK = F > 0 ? refill_kind<S>(F - 1) : 0;
@@ -543,7 +581,7 @@ struct DmaEngine {
     } else {
       mfma_widen<CUR, 0>(3 * F, x.x, x.y, t0, t1);
     }
-    if constexpr (S == 0 && F < DPW) {
+    if constexpr (S == 0 && DMA && F < DPW) {
       const v4i* rs;
       uint32_t voff, soff, m0;
       dma_args(lds0, F, rs, voff, soff, m0);
@@ -556,9 +594,9 @@ struct DmaEngine {
     if constexpr (F < C::FN2) wb[NXT][F] = w;
     else wa[NXT][F - C::FN2] = w;
   }
-  template <int CUR, int S, int... F>
+  template <int CUR, int S, bool DMA, int... F>
   __device__ __forceinline__ void units(uint32_t lds0, std::integer_sequence<int, F...>) {
-    (unit<CUR, S, F>(lds0), ...);
+    (unit<CUR, S, DMA, F>(lds0), ...);
   }
   // MFMAs 3*NF.. of an int4 step; the first refills the last fragment.
   template <int CUR, int S, int... X>
@@ -583,7 +621,7 @@ struct DmaEngine {
   // steps are the fixed asm sequence above: fragment unit f (MFMAs
   // 3f..3f+2) widens fragment f of the next set, B fragments first; the
   // remaining MFMAs carry no VALU.
-  template <int CUR, int S, class OnStep>
+  template <int CUR, int S, class OnStep, bool DMA = true>
   __device__ __forceinline__ void step(const uint8_t* smem, int t, OnStep& on_step) {
     constexpr int NXT = 1 - CUR;
     if constexpr (I4) {
@@ -592,8 +630,7 @@ struct DmaEngine {
       static_assert(3 * NF < NMF, "three MFMAs per prepared fragment and one for the last refill");
       static_assert(DPW <= NF, "one load per prepared fragment");
       const uint32_t lds0 = lds_address(smem);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      units<CUR, S>(lds0, std::make_integer_sequence<int, NF>{});
+      units<CUR, S, DMA>(lds0, std::make_integer_sequence<int, NF>{});
       tail<CUR, S>(lds0, std::make_integer_sequence<int, NMF - 3 * NF - 1>{});
     } else {
       prepare<C::B_KMAJOR, S>(wb[NXT], pb, [&](int j) { return read_b<S>(smem, j); });
@@ -637,26 +674,27 @@ struct DmaEngine {
   template <class OnStep>
   __device__ __forceinline__ void run(uint8_t* smem, int nst, OnStep on_step) {
 #pragma unroll
-    for (int q = 0; q < P; ++q) dma_stage(smem, q < nst ? q : nst - 1, q);
+    for (int q = 0; q < P; ++q)
+      if (q < nst) dma_stage(smem, q, q);
     if constexpr (PING) {
       // Stage k is read only during stage k, so the barrier that opens
       // stage k+1 frees stage k's slot: its loads (stage k+P) are issued
       // then, P-1 stages ahead of use.
-      wait_vmcnt<(P - 1) * DPW>();
+      wait_stages(imin(P - 1, nst - 1));
       __syncthreads();
       stage_ping(smem, 0, on_step);
       for (int k = 1; k < nst; ++k) {
-        wait_vmcnt<(P - 2) * DPW>();
+        wait_stages(imin(P - 2, nst - 1 - k));
         __syncthreads();
         const int prev = k - 1;
-        dma_stage(smem, prev + P < nst ? prev + P : nst - 1, slot);
+        if (prev + P < nst) dma_stage(smem, prev + P, slot);
         advance_reads();
         stage_ping(smem, k, on_step);
       }
       wait_vmcnt<0>();
       return;
     }
-    wait_vmcnt<(P - 1) * DPW>();
+    wait_stages(imin(P - 1, nst - 1));
     __syncthreads();
     if constexpr (I4) {
       // operands of step 0; packed registers: step 1 (MN-major) or stage 0
@@ -679,17 +717,27 @@ struct DmaEngine {
       static_assert(C::FM == 8 && C::FN2 == 8, "the asm step is written for 8x8 accumulator fragments");
       acc_fence<4>(acc);
       static_assert(DPW <= C::FN2 + C::FM, "one load per prepared fragment");
-      for (int k = 0; k < nst; ++k) {
-        // open stage k as open_stage() does, with the loads issued by step 0;
-        // the asm LDS reads of the last step must be complete as well
+      // Stages open as open_stage() does, with the loads issued by step 0
+      // and the asm LDS reads of the last step complete as well.  The last
+      // P stages issue no loads (there is no stage k+P).
+      int k = 0;
+      for (; k + P < nst; ++k) {
         wait_vmcnt<(P - 2) * DPW>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
-        dma_st = k + P < nst ? k + P : nst - 1;
+        dma_st = k + P;
         dma_slot = slot;
         advance_reads();
         step<0, 0>(smem, 2 * k, on_step);
         step<1, 1>(smem, 2 * k + 1, on_step);
+      }
+      for (; k < nst; ++k) {
+        wait_stages(imin(P - 2, nst - 2 - k));
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        advance_reads();
+        step<0, 0, OnStep, false>(smem, 2 * k, on_step);
+        step<1, 1, OnStep, false>(smem, 2 * k + 1, on_step);
       }
       acc_fence<7>(acc);
     } else {
