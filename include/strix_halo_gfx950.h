@@ -63,6 +63,14 @@ extern "C" {
 #define SHK_OUT_F32 1
 #define SHK_OUT_I32 2
 
+/* Operand formats of a dense entry.  PACKED kernels read A and B as given;
+ * BF6 kernels (int4 only) first convert both operands into a caller
+ * workspace of amd_strix_halo_kernels_gemm_workspace_bytes() bytes: every
+ * int4 value -8..7 is exact in the 6-bit float e3m2, whose MFMA runs at
+ * twice the int8 rate; the fp32 accumulation is exact for K <= 262144. */
+#define SHK_OPERANDS_PACKED 0
+#define SHK_OPERANDS_BF6 1
+
 typedef struct shk_kernel_desc {
   int32_t index;
   int32_t family;          /* SHK_FAMILY_* */
@@ -79,6 +87,7 @@ typedef struct shk_kernel_desc {
   int32_t num_stages;      /* LDS stages (double buffered = 2) */
   int32_t lds_bytes;       /* LDS per workgroup */
   int32_t group_size_m;    /* tile-row swizzle width (dense) */
+  int32_t operand_format;  /* SHK_OPERANDS_* */
 } shk_kernel_desc;
 
 /* ---- status (reference dispatch.cpp:206-222) ---------------------------- */
@@ -124,12 +133,32 @@ int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out);
  * b_scale[ceil(k/S), b_cols].  Requires m % block_m == 0, n % block_n == 0,
  * k % block_k == 0 and (subchannel) k % S == 0 (reference
  * template_config.py:22-38).  `gate` of the reference signature is dropped:
- * SwiGLU is fused. */
+ * SwiGLU is fused.  Entries with operand_format SHK_OPERANDS_BF6 need a
+ * workspace and are launched with amd_strix_halo_kernels_launch_gemm_ws;
+ * this function refuses them. */
 int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintptr_t stream,
                                        const void* a, const void* b, const void* a_scale,
                                        const void* b_scale, void* out, int32_t m, int32_t n,
                                        int32_t k, int32_t subchannel, int32_t epilogue,
                                        int32_t out_mode);
+
+/* Workspace bytes a dense entry needs for shape (m, n, k) (0 for PACKED
+ * entries), written to *bytes.  Returns 0, or 1 for a bad index or shape.
+ * No counterpart in the reference, whose gfx1151 kernels read int4 operands
+ * directly. */
+int amd_strix_halo_kernels_gemm_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k,
+                                                uint64_t* bytes);
+
+/* amd_strix_halo_kernels_launch_gemm with a caller workspace (16-byte
+ * aligned, at least amd_strix_halo_kernels_gemm_workspace_bytes() bytes; may
+ * be null for PACKED entries).  The workspace is overwritten by the launch
+ * and may be reused once the launch has completed in stream order.  Same
+ * reference interface as amd_strix_halo_kernels_launch_gemm. */
+int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, uintptr_t stream,
+                                          const void* a, const void* b, const void* a_scale,
+                                          const void* b_scale, void* out, int32_t m, int32_t n,
+                                          int32_t k, int32_t subchannel, int32_t epilogue,
+                                          int32_t out_mode, void* workspace, uint64_t workspace_bytes);
 
 /* ---- ragged task list -------------------------------------------------------
  * Device-side replacement of calculate_group_info (ragged.py:201-323, the

@@ -38,6 +38,13 @@ OUT_BF16 = 0
 OUT_F32 = 1
 OUT_I32 = 2
 
+# Operand formats: PACKED entries read A and B as given; BF6 entries convert
+# both int4 operands into a caller workspace in the bf6 (e3m2) block format
+# first (amd_strix_halo_kernels_gemm_workspace_bytes).
+OPERANDS_PACKED = 0
+OPERANDS_BF6 = 1
+BF6_MAX_K = 262144
+
 
 @dataclass(frozen=True)
 class KernelDesc:
@@ -58,6 +65,18 @@ class KernelDesc:
     num_stages: int
     lds_bytes: int
     group_size_m: int
+    operand_format: int = OPERANDS_PACKED
+
+    @property
+    def needs_workspace(self) -> bool:
+        return self.operand_format == OPERANDS_BF6
+
+    def workspace_bytes(self, m: int, n: int, k: int) -> int:
+        """Bytes of the operand workspace for shape (m, n, k) (0 for PACKED)."""
+        if not self.needs_workspace:
+            return 0
+        b_cols = 2 * n if self.epilogue_kind == EPI_KIND_SWIGLU else n
+        return (m * k * 3) // 4 + (b_cols * k * 3) // 4
 
     def serves_subchannel(self, size: int | None) -> bool:
         if self.scale_mode == SCALE_PER_CHANNEL:
@@ -65,11 +84,17 @@ class KernelDesc:
         return size is not None and self.min_subchannel <= size <= self.max_subchannel
 
 
-def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0):
+def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
+          bf6=False):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
+    # bf6: three stages of 256 A rows + 256 B rows x 128 K in bf6 (96 bytes).
     brows = 2 * bn if swiglu else bn
-    lds = pipe * (bm + brows) * 64 if pipe else 2 * (bm * bk + brows * bk)
+    if bf6:
+        pipe = 3
+        lds = pipe * (bm + 256) * 96
+    else:
+        lds = pipe * (bm + brows) * 64 if pipe else 2 * (bm * bk + brows * bk)
     return KernelDesc(
         index=index,
         family=family,
@@ -86,6 +111,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         num_stages=pipe or 2,
         lds_bytes=lds,
         group_size_m=group_m,
+        operand_format=OPERANDS_BF6 if bf6 else OPERANDS_PACKED,
     )
 
 
@@ -99,6 +125,9 @@ def _build() -> tuple[KernelDesc, ...]:
         big_bk = 128 if bits == 4 else 64
         for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
             d = dict(family=FAMILY_DENSE, bits=bits, layout=layout)
+            if bits == 4:
+                add(**d, bm=256, bn=256, bk=128, wm=2, wn=2, bf6=True)
+                add(**d, bm=256, bn=128, bk=128, wm=2, wn=2, swiglu=True, bf6=True)
             add(**d, bm=256, bn=256, bk=big_bk, wm=2, wn=2, pipe=4)
             add(**d, bm=256, bn=128, bk=big_bk, wm=2, wn=2, swiglu=True, pipe=4)
             add(**d, bm=128, bn=128, bk=64, wm=2, wn=2)

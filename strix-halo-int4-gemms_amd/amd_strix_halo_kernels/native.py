@@ -43,7 +43,7 @@ class _Desc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "index", "family", "dtype_bits", "layout", "scale_mode", "min_subchannel", "max_subchannel",
         "epilogue_kind", "block_m", "block_n", "block_k", "num_waves", "num_stages", "lds_bytes",
-        "group_size_m")]
+        "group_size_m", "operand_format")]
 
 
 def package_root() -> Path:
@@ -75,6 +75,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_kernel_table_entry.restype = I
     lib.amd_strix_halo_kernels_launch_gemm.argtypes = [I, I, U, P, P, P, P, P, I32, I32, I32, I32, I32, I32]
     lib.amd_strix_halo_kernels_launch_gemm.restype = I
+    lib.amd_strix_halo_kernels_gemm_workspace_bytes.argtypes = [I, I32, I32, I32, ctypes.POINTER(ctypes.c_uint64)]
+    lib.amd_strix_halo_kernels_gemm_workspace_bytes.restype = I
+    lib.amd_strix_halo_kernels_launch_gemm_ws.argtypes = [I, I, U, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P,
+                                                          ctypes.c_uint64]
+    lib.amd_strix_halo_kernels_launch_gemm_ws.restype = I
     lib.amd_strix_halo_kernels_ragged_task_capacity.argtypes = [I32, I32, I32, I32]
     lib.amd_strix_halo_kernels_ragged_task_capacity.restype = I32
     lib.amd_strix_halo_kernels_ragged_group_info.argtypes = [I, U, P, I32, I32, I32, I32, P, P, P]
@@ -262,10 +267,25 @@ _EPILOGUE_CODE = {Epilogue.NONE: kt.EPILOGUE_NONE, Epilogue.RELU2: kt.EPILOGUE_R
                   Epilogue.SWIGLU: kt.EPILOGUE_SWIGLU}
 
 
+def gemm_workspace_bytes(kernel: KernelMetadata, m: int, n: int, k: int, *, library_path=None) -> int:
+    """Workspace bytes the kernel's table entry needs for (m, n, k)."""
+    lib = _verified_library(library_path)
+    out = ctypes.c_uint64(0)
+    _check(lib, lib.amd_strix_halo_kernels_gemm_workspace_bytes(_table_index(kernel), m, n, k, ctypes.byref(out)))
+    return int(out.value)
+
+
 def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, library_path, stream) -> None:
     lib = _verified_library(library_path)
     sub = kernel.scale.subchannel_size if kernel.scale.mode is ScaleMode.SUBCHANNEL else 0
-    rc = lib.amd_strix_halo_kernels_launch_gemm(
+    # bf6 entries convert both operands into a workspace first; it comes from
+    # torch's caching allocator on the launch stream, so a later launch on
+    # the same stream may reuse it.
+    ws_bytes = gemm_workspace_bytes(kernel, m, n, k, library_path=library_path)
+    work = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+    if work is not None and stream is not None:
+        work.record_stream(stream)
+    rc = lib.amd_strix_halo_kernels_launch_gemm_ws(
         _table_index(kernel),
         _device_index(a),
         _stream_handle(torch, a, stream),
@@ -280,6 +300,8 @@ def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, li
         sub or 0,
         _EPILOGUE_CODE[kernel.epilogue],
         out_mode,
+        work.data_ptr() if work is not None else None,
+        ws_bytes,
     )
     _check(lib, rc)
 

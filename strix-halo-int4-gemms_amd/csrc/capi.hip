@@ -28,10 +28,13 @@ int fail_hip(const char* what, hipError_t err) {
 const std::vector<Entry>& table() {
   static const std::vector<Entry> t = [] {
     std::vector<Entry> v;
+    shk::append_dense_f6(v, SHK_LAYOUT_NN);
     shk::append_dense_dma_4_0(v);
     shk::append_dense_4_0(v);
+    shk::append_dense_f6(v, SHK_LAYOUT_NT);
     shk::append_dense_dma_4_1(v);
     shk::append_dense_4_1(v);
+    shk::append_dense_f6(v, SHK_LAYOUT_TN);
     shk::append_dense_dma_4_2(v);
     shk::append_dense_4_2(v);
     shk::append_dense_dma_8_0(v);
@@ -107,6 +110,14 @@ int check_out_mode(int out_mode) {
   return 0;
 }
 
+// Workspace of a dense entry: both operands in bf6 block format for BF6
+// entries, nothing otherwise.
+uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k) {
+  if (d.operand_format != SHK_OPERANDS_BF6) return 0;
+  const long b_cols = d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2L * n : (long)n;
+  return shk::f6_operand_bytes(m, k) + shk::f6_operand_bytes(b_cols, k);
+}
+
 // Largest K for which the x16-widened int4 products of one int32 accumulator
 // cannot overflow: 128 * 128 * K < 2^31.
 constexpr int kMaxInt4AccK = 131072;
@@ -160,10 +171,29 @@ int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out) {
   return 0;
 }
 
+int amd_strix_halo_kernels_gemm_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k,
+                                                uint64_t* bytes) {
+  g_last_error.clear();
+  if (bytes == nullptr) return fail("bytes must be non-null");
+  const Entry* e = nullptr;
+  if (lookup(kernel_index, SHK_FAMILY_DENSE, &e)) return 1;
+  if (m < 0 || n < 0 || k < 0) return fail("M, N, and K must be non-negative");
+  *bytes = dense_workspace_bytes(e->d, m, n, k);
+  return 0;
+}
+
 int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintptr_t stream, const void* a,
                                        const void* b, const void* a_scale, const void* b_scale, void* out,
                                        int32_t m, int32_t n, int32_t k, int32_t subchannel, int32_t epilogue,
                                        int32_t out_mode) {
+  return amd_strix_halo_kernels_launch_gemm_ws(kernel_index, device_index, stream, a, b, a_scale, b_scale, out, m,
+                                               n, k, subchannel, epilogue, out_mode, nullptr, 0);
+}
+
+int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, uintptr_t stream, const void* a,
+                                          const void* b, const void* a_scale, const void* b_scale, void* out,
+                                          int32_t m, int32_t n, int32_t k, int32_t subchannel, int32_t epilogue,
+                                          int32_t out_mode, void* workspace, uint64_t workspace_bytes) {
   g_last_error.clear();
   const Entry* e = nullptr;
   if (lookup(kernel_index, SHK_FAMILY_DENSE, &e)) return 1;
@@ -193,9 +223,19 @@ int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintp
   const bool swiglu = d.epilogue_kind == SHK_EPI_KIND_SWIGLU;
   if (swiglu ? epilogue != SHK_EPILOGUE_SWIGLU : (epilogue != SHK_EPILOGUE_NONE && epilogue != SHK_EPILOGUE_RELU2))
     return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
-  if (d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
+  const bool bf6 = d.operand_format == SHK_OPERANDS_BF6;
+  if (bf6 && k > shk::F6_MAX_K)
+    return fail("bf6 kernels support K <= " + std::to_string(shk::F6_MAX_K) + "; got " + std::to_string(k));
+  if (!bf6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
                 std::to_string(k));
+  if (bf6) {
+    const uint64_t need = dense_workspace_bytes(d, m, n, k);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail("kernel " + std::to_string(kernel_index) + " converts its operands into a workspace of " +
+                  std::to_string(need) + " bytes; pass it to amd_strix_halo_kernels_launch_gemm_ws");
+    if (!aligned(workspace, 16)) return fail("the workspace must be 16-byte aligned");
+  }
   if (!aligned(out, 16) || !aligned(b_scale, 8) || !aligned(a_scale, 2))
     return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
 
@@ -221,12 +261,14 @@ int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintp
   p.out_mode = out_mode;
   // 16-byte pieces for K-major operands and for every operand of the
   // direct-to-LDS tiles (more than two stages); 8-byte rows otherwise.
-  const bool dma = d.num_stages > 2;
+  const bool dma = d.num_stages > 2 || bf6;
   const int a_need = (a_km || dma) ? 16 : 8;
   const int b_need = (b_km || dma) ? 16 : 8;
   p.a_aligned = aligned(a, a_need) && p.lda % a_need == 0;
   p.b_aligned = aligned(b, b_need) && p.ldb % b_need == 0;
   p.group_m = d.group_size_m;
+  p.layout = d.layout;
+  p.work = static_cast<uint8_t*>(workspace);
   // Operands are addressed with 32-bit buffer offsets.
   if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
       (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))

@@ -1,0 +1,104 @@
+// Operand conversion of the bf6 GEMM path: packed int4 (either layout) to
+// the block format of shk_f6.h.  Compiled apart from the GEMM, with the
+// default scheduler.
+#include "shk_table.h"
+
+namespace shk {
+namespace {
+
+// 16 packed int4 bytes -> the lane's 24 bf6 bytes.  x ^ 0x8 per nibble is the
+// offset-binary value v + 8; 0x6400 | (v + 8) is the f16 1024 + v + 8, and
+// subtracting 1032 leaves v exactly.  The conversion to bf6 is exact for
+// these values (scale 1).
+__device__ __forceinline__ v6i f6_convert(const uint4& x) {
+  f6_h32 h;
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t u = w[q] ^ 0x88888888u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t d = ((u >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+      const f6_h2 v = __builtin_bit_cast(f6_h2, d) - f6_h2{(_Float16)1032.0f, (_Float16)1032.0f};
+      h[8 * q + 2 * j] = v.x;
+      h[8 * q + 2 * j + 1] = v.y;
+    }
+  }
+  return __builtin_bit_cast(v6i, __builtin_amdgcn_cvt_scalef32_pk32_bf6_f16(h, 1.0f));
+}
+
+__device__ __forceinline__ void f6_store_lane(uint8_t* block, int lane, const v6i& y) {
+  *reinterpret_cast<uint4*>(block + 16 * lane) = make_uint4(y[0], y[1], y[2], y[3]);
+  *reinterpret_cast<uint2*>(block + 1024 + 8 * lane) = make_uint2(y[4], y[5]);
+}
+
+// Source row of packed row r.  For SwiGLU B the packed rows of each 256-row
+// tile (output columns 128t .. 128t+127) are, per 128-row half h (one wave
+// column of the GEMM tile), 64 up columns followed by the same 64 gate
+// columns: 128t + 64h + q (q < 64) and N + 128t + 64h + q - 64.
+__device__ __forceinline__ int f6_src_row(int r, int swiglu_n) {
+  if (swiglu_n == 0) return r;
+  const int t = r >> 8, h = (r >> 7) & 1, q = r & 127;
+  return 128 * t + 64 * h + (q & 63) + (q >= 64 ? swiglu_n : 0);
+}
+
+// K-major source (row r holds its K values contiguously, two per byte): one
+// wave converts one block; a lane loads its 16 source bytes directly.
+__global__ __launch_bounds__(256) void f6_pack_kmajor(const F6PackArgs p) {
+  const int lane = threadIdx.x & 63;
+  const long blk = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int panel = (int)(blk / p.kb);
+  const int kb = (int)(blk - (long)panel * p.kb);
+  const int row = f6_src_row(16 * panel + (lane & 15), p.swiglu_n);
+  const uint4 x = *reinterpret_cast<const uint4*>(p.src + (long)row * p.ld + 64L * kb + 16 * (lane >> 4));
+  f6_store_lane(p.dst + blk * F6_BLOCK, lane, f6_convert(x));
+}
+
+// MN-major source (K row kp holds two K values of every packed row, one per
+// nibble): a workgroup converts the 16 blocks of one 256-row tile and one K
+// block.  The 64 x 256-byte source tile goes through LDS in the MN-major
+// ring layout of the DMA engine, whose transposing reads hand each lane its
+// row's 16 bytes in K order.
+__global__ __launch_bounds__(256) void f6_pack_mnmajor(const F6PackArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[64 * 256];
+  const int t = blockIdx.x / p.kb;
+  const int kb = blockIdx.x - t * p.kb;
+  const int tid = threadIdx.x;
+  const int u = tid & 15;  // 16-row unit of the tile
+  const long col = f6_src_row(F6_TILE * t + 16 * u, p.swiglu_n);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int kp = 16 * q + (tid >> 4);
+    const uint4 x = *reinterpret_cast<const uint4*>(p.src + (64L * kb + kp) * p.ld + col);
+    const int swz = (kp & 7) | ((kp & 16) >> 1);
+    *reinterpret_cast<uint4*>(tile + kp * 256 + 16 * (u ^ swz)) = x;
+  }
+  __syncthreads();
+  const int lane = tid & 63;
+  const int l15 = lane & 15, g = lane >> 4;
+  const int kp = 16 * g + l15 / 2;
+  const int swz = (kp & 7) | ((kp & 16) >> 1);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int unit = 4 * (tid >> 6) + c;
+    const uint8_t* q = tile + kp * 256 + 16 * (unit ^ swz) + 8 * (l15 & 1);
+    const v2i lo = ds_read_tr8(q);
+    const v2i hi = ds_read_tr8(q + 2048);
+    const uint4 x = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    const long blk = (long)(16 * t + unit) * p.kb + kb;
+    f6_store_lane(p.dst + blk * F6_BLOCK, lane, f6_convert(x));
+  }
+}
+
+}  // namespace
+
+hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s) {
+  if (mn_major) {
+    hipLaunchKernelGGL(f6_pack_mnmajor, dim3((a.rows / F6_TILE) * a.kb), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(f6_pack_kmajor, dim3((a.rows / 16) * a.kb / 4), dim3(256), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace shk

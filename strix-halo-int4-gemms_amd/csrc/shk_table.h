@@ -7,7 +7,7 @@
 #include <vector>
 
 #include "../../include/strix_halo_gfx950.h"
-#include "shk_dense.h"
+#include "shk_f6.h"
 
 namespace shk {
 
@@ -25,6 +25,24 @@ struct Entry {
 template <class C>
 hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL(dense_gemm_kernel<C>, grid, dim3(C::NT), 0, s, a);
+  return hipGetLastError();
+}
+// bf6 path: converts A and B into the workspace (layout-dependent), then
+// runs the GEMM on the converted operands.
+template <class C>
+hipError_t launch_f6_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  const bool a_mn = a.layout == SHK_LAYOUT_TN;
+  const bool b_mn = a.layout != SHK_LAYOUT_NT;
+  const unsigned long long a_bytes = f6_operand_bytes(a.M, a.K);
+  const int kb = a.K / 128;
+  hipError_t err = launch_f6_pack(F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0}, a_mn, s);
+  if (err != hipSuccess) return err;
+  err = launch_f6_pack(F6PackArgs{a.b, a.work + a_bytes, a.ldb, a.b_cols, kb, C::SWIGLU ? a.N : 0}, b_mn, s);
+  if (err != hipSuccess) return err;
+  DenseArgs g = a;
+  g.a = a.work;
+  g.b = a.work + a_bytes;
+  hipLaunchKernelGGL(f6_gemm_kernel<C>, grid, dim3(256), 0, s, g);
   return hipGetLastError();
 }
 template <class C>
@@ -56,12 +74,21 @@ constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
       C::NUM_STAGES,
       C::LDS_BYTES,
       group_m,
+      SHK_OPERANDS_PACKED,
   };
 }
 
 template <class C>
 Entry dense_entry(int layout, int group_m) {
   return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_dense_t<C>, nullptr, nullptr};
+}
+template <class C>
+Entry f6_entry(int layout) {
+  shk_kernel_desc d = desc_of<C>(SHK_FAMILY_DENSE, layout, 8);
+  d.num_stages = F6Engine<C>::P;
+  d.lds_bytes = F6Engine<C>::LDS_BYTES;
+  d.operand_format = SHK_OPERANDS_BF6;
+  return Entry{d, &launch_f6_t<C>, nullptr, nullptr};
 }
 template <class C>
 Entry fwd_entry(int layout) {
@@ -73,8 +100,9 @@ Entry bwd_entry(int layout) {
 }
 
 // Each kernel translation unit appends its entries in a fixed order
-// (append_dense_dma_<bits>_<layout>, append_dense_<bits>_<layout>,
-// append_ragged_<layout>).
+// (append_dense_f6(layout), append_dense_dma_<bits>_<layout>,
+// append_dense_<bits>_<layout>, append_ragged_<layout>).
+void append_dense_f6(std::vector<Entry>& t, int layout);
 void append_dense_dma_4_0(std::vector<Entry>& t);
 void append_dense_dma_4_1(std::vector<Entry>& t);
 void append_dense_dma_4_2(std::vector<Entry>& t);

@@ -165,3 +165,50 @@ def test_last_error_is_thread_local(lib):
     t.join()
     assert "non-null" in seen["msg"]
     assert _err(lib) == mine
+
+
+def _ws(lib, index, m, n, k):
+    out = ctypes.c_uint64(0)
+    rc = lib.amd_strix_halo_kernels_gemm_workspace_bytes(index, m, n, k, ctypes.byref(out))
+    return rc, int(out.value)
+
+
+def _gemm_ws(lib, index, m, n, k, *, work, work_bytes, epi=0, mode=0):
+    return lib.amd_strix_halo_kernels_launch_gemm_ws(index, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, m, n, k, 0, epi,
+                                                     mode, work, work_bytes)
+
+
+def test_bf6_entries_report_their_workspace(lib):
+    bf6 = [d for d in kt.entries(kt.FAMILY_DENSE) if d.operand_format == kt.OPERANDS_BF6]
+    assert {(d.layout, d.epilogue_kind) for d in bf6} == {
+        (layout, epi) for layout in (kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN)
+        for epi in (kt.EPI_KIND_PLAIN, kt.EPI_KIND_SWIGLU)}
+    for d in bf6:
+        assert d.dtype_bits == 4 and d.block_m == 256 and d.num_stages == 3 and d.lds_bytes == 147456
+        for m, n, k in ((256, 256, 128), (512, 1024, 4096), (8192, 8192, 8192)):
+            rc, got = _ws(lib, d.index, m, n, k)
+            b_cols = 2 * n if d.epilogue_kind == kt.EPI_KIND_SWIGLU else n
+            # 6 bits per value: 3/4 byte per logical element of A and B
+            assert rc == 0 and got == (m * k + b_cols * k) * 3 // 4 == d.workspace_bytes(m, n, k)
+    packed = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
+    assert _ws(lib, packed, 256, 256, 128) == (0, 0)
+    assert lib.amd_strix_halo_kernels_gemm_workspace_bytes(packed, 1, 1, 1, None) == 1
+    assert "non-null" in _err(lib)
+
+
+def test_bf6_launch_needs_a_workspace(lib):
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_BF6)
+    assert _gemm(lib, idx, 256, 256, 128) == 1
+    assert "workspace of 49152 bytes" in _err(lib)
+    assert _gemm_ws(lib, idx, 256, 256, 128, work=FAKE, work_bytes=49151) == 1
+    assert "workspace of 49152 bytes" in _err(lib)
+    assert _gemm_ws(lib, idx, 256, 256, 128, work=FAKE + 8, work_bytes=49152 + 8) == 1
+    assert "16-byte aligned" in _err(lib)
+
+
+def test_bf6_k_limit_keeps_fp32_sums_exact(lib):
+    # |sum| <= 64 * K must stay <= 2^24 for the fp32 accumulation to be exact
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_BF6)
+    assert kt.BF6_MAX_K * 64 == 1 << 24
+    assert _gemm_ws(lib, idx, 256, 256, kt.BF6_MAX_K + 128, work=FAKE, work_bytes=1 << 40) == 1
+    assert "K <= 262144" in _err(lib)

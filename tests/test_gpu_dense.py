@@ -20,6 +20,7 @@ from tests._util import bf16_bits, dense_case, max_ulp, stable_seed, to_dev
 torch = pytest.importorskip("torch")
 
 import amd_strix_halo_kernels as shk  # noqa: E402
+from amd_strix_halo_kernels import kernel_table as kt  # noqa: E402
 from amd_strix_halo_kernels import native  # noqa: E402
 from amd_strix_halo_kernels.template_config import representative_generation_shape  # noqa: E402
 
@@ -223,3 +224,54 @@ def test_special_scale_values_store_like_torch(kernel, device):
         assert max_ulp(got[~nan_want], want[~nan_want]) <= ULP_TOL
     else:
         assert np.array_equal(got, want)
+
+
+_BF6 = [k for k in shk.default_registry.all()
+        if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_BF6 and k.epilogue is not shk.Epilogue.RELU2]
+
+
+@pytest.mark.parametrize("kernel", _BF6, ids=lambda k: k.kernel_id)
+@pytest.mark.parametrize("k", [128, 256, 384, 640])
+def test_bf6_kernels_every_stage_count(kernel, k, device):
+    """One to five K blocks: the ring prologue, the tail and the main loop."""
+    _, layout, _, epi = _kernel_params(kernel)
+    m, n = 512, 512 if epi != "swiglu" else 256
+    seed = stable_seed(f"{kernel.kernel_id}/{k}")
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=None,
+                                                 swiglu=epi == "swiglu")
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q)), "int32 accumulators differ"
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=4, layout=layout, a_scale=sa, b_scale=sb, epilogue=epi)
+    if epi == "swiglu":
+        assert max_ulp(got, want) <= ULP_TOL
+    else:
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+def test_bf6_exact_at_the_k_bound(layout, device):
+    """K = 262144 with rows of A and columns of B constant: every output is
+    K * c_i * d_j, up to 64 * K = 2^24 for c = d = -8, the largest integer
+    magnitude the fp32 accumulation must still hold exactly."""
+    m = n = 256
+    k = kt.BF6_MAX_K
+    c = np.resize(np.arange(-8, 8, dtype=np.int8), m)
+    d = np.resize(np.arange(7, -9, -1, dtype=np.int8), n)
+    c[:8] = -8
+    d[:8] = -8
+    a_q = np.repeat(c[:, None], k, axis=1)
+    b_q = np.repeat(d[None, :], k, axis=0)
+    a_arg, b_arg = ref.pack_operands(a_q, b_q, bits=4, layout=layout)
+    del a_q, b_q
+    kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL),
+                                         epilogue=shk.Epilogue.NONE, m=m, n=n, k=k, layout=shk.GemmLayout(layout))
+    assert kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_BF6
+    sa = ref.bf16_from_f32(np.ones(m))
+    sb = ref.bf16_from_f32(np.ones(n))
+    print(f"case bf6 k-bound {layout}", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    want = k * c[:, None].astype(np.int64) * d[None, :].astype(np.int64)
+    assert raw[0, 0] == 1 << 24
+    assert np.array_equal(raw, want)
+    assert np.array_equal(got, ref.bf16_round(want.astype(np.float32)))
