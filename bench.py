@@ -12,7 +12,11 @@ K-ragged backward, G=8, M=8192, K=2048, N=1408).
 A step is one API call over operands already resident in HBM; the timed region
 is exactly K steps bracketed by a device synchronisation on both sides.
 Kernel durations come from HIP events recorded around every launch on the
-stream the kernel runs on (torch's current stream).  No cache flush between
+stream the kernel runs on (torch's current stream).  C2 runs on the bf6 path
+(two operand conversions, then the GEMM); the same three launches are also
+made through the split C ABI with an event between each, which gives the GEMM
+kernel's own duration for the roofline (bf6 MFMA peak) beside the whole
+call's throughput (`value`, also reported against the int8 MFMA peak).  No cache flush between
 steps (steady state, the operands of C2 fit the 256 MB MALL); a cold run that
 overwrites a 1 GiB buffer before each launch is reported beside it.  The CPU
 baseline is the repository's C oracle (the same unpack -> int32 matmul ->
@@ -35,9 +39,10 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "int4 GEMM TOPS @8192³ (% gfx950 int8 MFMA peak); fused SwiGLU TOPS"
 INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
+BF6_MFMA_PEAK_TFLOPS = 10100.0  # MI355X dense fp6/fp4 MFMA, published
 HBM_PEAK_GBS = 8000.0
 COPY_BYTES = 256 << 20
-TRAFFIC_FILE = ROOT / "profiles" / "dense_int4_c2_8192_traffic.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "f6_gemm_c2_8192_traffic.txt"
 
 
 def _measured_traffic():
@@ -105,7 +110,46 @@ def _uniform_bf16(torch, shape, lo, hi, gen):
     return (torch.rand(shape, device="cuda", generator=gen) * (hi - lo) + lo).to(torch.bfloat16)
 
 
+def _split_bf6_times(torch, shk, kernel, a, b, sa, sb, m, n, k, steps, warmup):
+    """Per-kernel durations of a bf6 launch: the same three launches as
+    ``mm`` (convert A, convert B, GEMM) made through the split C ABI with a HIP
+    event between each, on torch's current stream.  Returns mean ms of
+    (convert A, convert B, GEMM)."""
+    from amd_strix_halo_kernels import native
+
+    work = native.gemm_workspace(kernel, m, n, k, device=a.device)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+
+    def run(ev=None):
+        if ev is not None:
+            ev[0].record()
+        native.convert_operand(kernel, 0, a, m=m, n=n, k=k, workspace=work)
+        if ev is not None:
+            ev[1].record()
+        native.convert_operand(kernel, 1, b, m=m, n=n, k=k, workspace=work)
+        if ev is not None:
+            ev[2].record()
+        native.launch_converted(kernel, m=m, n=n, k=k, workspace=work, a_scale=sa, b_scale=sb, out=out)
+        if ev is not None:
+            ev[3].record()
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for ev in events:
+        run(ev)
+    torch.cuda.synchronize()
+    sums = [0.0, 0.0, 0.0]
+    for ev in events:
+        for i in range(3):
+            sums[i] += ev[i].elapsed_time(ev[i + 1])
+    return tuple(x / steps for x in sums)
+
+
 def bench_c2(torch, shk, steps, warmup):
+    from amd_strix_halo_kernels import kernel_table as kt
+
     m = n = k = 8192
     gen = torch.Generator(device="cuda").manual_seed(2)
     a = _rand_int4_packed(torch, m, k, gen)                      # [M, K/2]
@@ -122,11 +166,15 @@ def bench_c2(torch, shk, steps, warmup):
     cold = _cold_ms(torch, step)
     ops = 2 * m * n * k
     bytes_alg = m * k // 2 + k * n // 2 + 2 * m + 2 * n + 2 * m * n
-    return {
+    res = {
         "m": m, "n": n, "k": k, "kernel": kernel.kernel_id, "ops": ops, "bytes": bytes_alg,
         "wall_ms": wall, "kernel_ms": kern_mean, "kernel_ms_median": kern_med, "cold_kernel_ms": cold,
-        "host": (a, b, sa, sb),
+        "host": (a, b, sa, sb), "bf6": kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_BF6,
     }
+    if res["bf6"]:
+        res["convert_a_ms"], res["convert_b_ms"], res["gemm_ms"] = _split_bf6_times(
+            torch, shk, kernel, a, b, sa, sb, m, n, k, steps, warmup)
+    return res
 
 
 def bench_c3(torch, shk, steps, warmup):
@@ -323,7 +371,22 @@ def main(argv=None) -> int:
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (C oracle)")
         cpu = cpu_baseline(torch, c2["host"])
-    achieved = tops_kernel
+    if c2["bf6"]:
+        # the dominant kernel is the bf6 GEMM (f6_gemm_kernel); the two
+        # operand conversions are reported beside it
+        achieved = c2["ops"] / (c2["gemm_ms"] * 1e-3) / 1e12
+        peak = BF6_MFMA_PEAK_TFLOPS
+        dtype = "bf6"
+        operands = ("packed int4 converted to bf6 (e3m2, exact for -8..7) blocks in a workspace, "
+                    "bf6 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), fp32 accumulation exact for K <= 262144")
+        note = ("bf6 MFMA tera-ops/s of the GEMM kernel: algorithmic 2*M*N*K over its HIP-event launch duration; "
+                "value counts the whole mm() call including both operand conversions")
+    else:
+        achieved = tops_kernel
+        peak = INT8_MFMA_PEAK_TOPS
+        dtype = "int8"
+        operands = "packed int4 (two nibbles per byte along K), int8 MFMA, int32 accumulation"
+        note = "int8 MFMA tera-ops/s; algorithmic 2*M*N*K per launch over the HIP-event launch duration"
     line = {
         "metric": METRIC,
         "value": tops_wall,
@@ -335,11 +398,11 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": dtype,
         "data": "synthetic",
         "config": {
             "workload": "C2: int4 x int4 per-channel GEMM, epilogue none, M=N=K=8192, bf16 out",
-            "operands": "packed int4 (two nibbles per byte along K), int8 MFMA, int32 accumulation",
+            "operands": operands,
             "kernel": c2["kernel"],
             "parallelism": "single GPU",
         },
@@ -350,12 +413,14 @@ def main(argv=None) -> int:
         "roofline": {
             "bound": "mfma",
             "achieved": achieved,
-            "peak": INT8_MFMA_PEAK_TOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": achieved / INT8_MFMA_PEAK_TOPS,
-            "traffic": _measured_traffic(),
-            "note": "int8 MFMA tera-ops/s; algorithmic 2*M*N*K per launch over the HIP-event launch duration",
+            "frac": achieved / peak,
+            "traffic": _measured_traffic() if c2["bf6"] else None,
+            "note": note,
         },
+        "bf6_launch_ms": ({"convert_a": c2["convert_a_ms"], "convert_b": c2["convert_b_ms"], "gemm": c2["gemm_ms"]}
+                          if c2["bf6"] else None),
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

@@ -160,6 +160,22 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
                                           int32_t k, int32_t subchannel, int32_t epilogue,
                                           int32_t out_mode, void* workspace, uint64_t workspace_bytes);
 
+/* The two halves of a bf6 launch, for callers that convert an operand once
+ * and multiply it many times (a weight matrix), and for timing the GEMM
+ * kernel on its own.  amd_strix_halo_kernels_gemm_convert converts operand 0
+ * (A, laid out as for launch_gemm) or operand 1 (B) of shape (m, n, k) into
+ * its part of the workspace; amd_strix_halo_kernels_launch_gemm_converted
+ * runs the GEMM on the converted operands in the workspace.  A launch_gemm_ws
+ * call is exactly convert(A), convert(B), launch_gemm_converted on one stream.
+ * Both refuse PACKED entries.  No counterpart in the reference. */
+int amd_strix_halo_kernels_gemm_convert(int kernel_index, int device_index, uintptr_t stream, int32_t operand,
+                                        const void* src, int32_t m, int32_t n, int32_t k, void* workspace,
+                                        uint64_t workspace_bytes);
+int amd_strix_halo_kernels_launch_gemm_converted(int kernel_index, int device_index, uintptr_t stream,
+                                                 const void* a_scale, const void* b_scale, void* out, int32_t m,
+                                                 int32_t n, int32_t k, int32_t epilogue, int32_t out_mode,
+                                                 const void* workspace, uint64_t workspace_bytes);
+
 /* ---- ragged task list -------------------------------------------------------
  * Device-side replacement of calculate_group_info (ragged.py:201-323, the
  * Triton kernel ragged.py:127-185).  From int32 group_sizes[groups] builds,

@@ -80,6 +80,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_launch_gemm_ws.argtypes = [I, I, U, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P,
                                                           ctypes.c_uint64]
     lib.amd_strix_halo_kernels_launch_gemm_ws.restype = I
+    lib.amd_strix_halo_kernels_gemm_convert.argtypes = [I, I, U, I32, P, I32, I32, I32, P, ctypes.c_uint64]
+    lib.amd_strix_halo_kernels_gemm_convert.restype = I
+    lib.amd_strix_halo_kernels_launch_gemm_converted.argtypes = [I, I, U, P, P, P, I32, I32, I32, I32, I32, P,
+                                                                 ctypes.c_uint64]
+    lib.amd_strix_halo_kernels_launch_gemm_converted.restype = I
     lib.amd_strix_halo_kernels_ragged_task_capacity.argtypes = [I32, I32, I32, I32]
     lib.amd_strix_halo_kernels_ragged_task_capacity.restype = I32
     lib.amd_strix_halo_kernels_ragged_group_info.argtypes = [I, U, P, I32, I32, I32, I32, P, P, P]
@@ -304,6 +309,42 @@ def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, li
         ws_bytes,
     )
     _check(lib, rc)
+
+
+def gemm_workspace(kernel: KernelMetadata, m: int, n: int, k: int, *, device: Any, library_path=None) -> Any:
+    """A uint8 workspace tensor for a bf6 kernel's converted operands."""
+    torch = _torch()
+    return torch.empty(gemm_workspace_bytes(kernel, m, n, k, library_path=library_path), dtype=torch.uint8,
+                       device=device)
+
+
+def convert_operand(kernel: KernelMetadata, operand: int, src: Any, *, m: int, n: int, k: int, workspace: Any,
+                    library_path=None, stream: Any | None = None) -> None:
+    """Converts A (operand 0) or B (operand 1) of a bf6 kernel into its part
+    of `workspace` (amd_strix_halo_kernels_gemm_convert)."""
+    torch = _torch()
+    lib = _verified_library(library_path)
+    src = _require_contiguous("src", src)
+    _require_device(torch, {"src": src, "workspace": workspace})
+    rc = lib.amd_strix_halo_kernels_gemm_convert(_table_index(kernel), _device_index(src),
+                                                 _stream_handle(torch, src, stream), operand, src.data_ptr(), m, n,
+                                                 k, workspace.data_ptr(), workspace.numel())
+    _check(lib, rc)
+
+
+def launch_converted(kernel: KernelMetadata, *, m: int, n: int, k: int, workspace: Any, a_scale: Any, b_scale: Any,
+                     out: Any, out_mode: int = kt.OUT_BF16, library_path=None, stream: Any | None = None) -> Any:
+    """GEMM of a bf6 kernel on operands already converted into `workspace`
+    (amd_strix_halo_kernels_launch_gemm_converted)."""
+    torch = _torch()
+    lib = _verified_library(library_path)
+    _require_device(torch, {"workspace": workspace, "a_scale": a_scale, "b_scale": b_scale, "out": out})
+    rc = lib.amd_strix_halo_kernels_launch_gemm_converted(
+        _table_index(kernel), _device_index(out), _stream_handle(torch, out, stream), a_scale.data_ptr(),
+        b_scale.data_ptr(), out.data_ptr(), m, n, k, _EPILOGUE_CODE[kernel.epilogue], out_mode,
+        workspace.data_ptr(), workspace.numel())
+    _check(lib, rc)
+    return out
 
 
 def _prepare_dense(torch, a, b, kernel, a_scale, b_scale, gate):

@@ -122,6 +122,123 @@ uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, i
 // cannot overflow: 128 * 128 * K < 2^31.
 constexpr int kMaxInt4AccK = 131072;
 
+// A validated dense call.  PHASE_ALL is a whole launch; the other phases are
+// the separately launched parts of a bf6 entry: converting A, converting B,
+// and the GEMM on converted operands.  Each phase checks the arguments it
+// uses; all of them check the shape and the workspace.
+enum Phase { PHASE_ALL, PHASE_CONVERT_A, PHASE_CONVERT_B, PHASE_GEMM };
+
+struct DenseCall {
+  const Entry* e = nullptr;
+  shk::DenseArgs p{};
+  long tiles = 0;
+};
+
+int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, const void* b, const void* a_scale,
+                  const void* b_scale, void* out, int32_t m, int32_t n, int32_t k, int32_t subchannel,
+                  int32_t epilogue, int32_t out_mode, void* workspace, uint64_t workspace_bytes) {
+  if (lookup(kernel_index, SHK_FAMILY_DENSE, &c.e)) return 1;
+  const shk_kernel_desc& d = c.e->d;
+  const bool bf6 = d.operand_format == SHK_OPERANDS_BF6;
+  const bool uses_a = phase == PHASE_ALL || phase == PHASE_CONVERT_A;
+  const bool uses_b = phase == PHASE_ALL || phase == PHASE_CONVERT_B;
+  const bool gemm = phase == PHASE_ALL || phase == PHASE_GEMM;
+  if (phase != PHASE_ALL && !bf6)
+    return fail("kernel " + std::to_string(kernel_index) +
+                " reads its operands directly; only bf6 entries convert them separately");
+  if ((uses_a && a == nullptr) || (uses_b && b == nullptr) ||
+      (gemm && (a_scale == nullptr || b_scale == nullptr || out == nullptr))) {
+    if (phase == PHASE_ALL) return fail("a, b, a_scale, b_scale, and out pointers must be non-null");
+    if (phase == PHASE_GEMM) return fail("a_scale, b_scale, and out pointers must be non-null");
+    return fail("the operand pointer must be non-null");
+  }
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail("M, N, and K must be positive; got (" + std::to_string(m) + ", " + std::to_string(n) + ", " +
+                std::to_string(k) + ")");
+  std::string why;
+  if (m % d.block_m) why += "M=" + std::to_string(m) + " is not divisible by BLOCK_M=" + std::to_string(d.block_m);
+  if (n % d.block_n) {
+    if (!why.empty()) why += "; ";
+    why += "N=" + std::to_string(n) + " is not divisible by BLOCK_N=" + std::to_string(d.block_n);
+  }
+  if (k % d.block_k) {
+    if (!why.empty()) why += "; ";
+    why += "K=" + std::to_string(k) + " is not divisible by BLOCK_K*SPLIT_K=" + std::to_string(d.block_k);
+  }
+  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && k % subchannel) {
+    if (!why.empty()) why += "; ";
+    why += "K=" + std::to_string(k) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
+  }
+  if (!why.empty()) return fail("kernel " + std::to_string(kernel_index) + " requires tile-multiple shape: " + why);
+  const bool swiglu = d.epilogue_kind == SHK_EPI_KIND_SWIGLU;
+  if (gemm) {
+    if (check_subchannel(d, subchannel)) return 1;
+    if (check_out_mode(out_mode)) return 1;
+    if (swiglu ? epilogue != SHK_EPILOGUE_SWIGLU : (epilogue != SHK_EPILOGUE_NONE && epilogue != SHK_EPILOGUE_RELU2))
+      return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
+  }
+  if (bf6 && k > shk::F6_MAX_K)
+    return fail("bf6 kernels support K <= " + std::to_string(shk::F6_MAX_K) + "; got " + std::to_string(k));
+  if (!bf6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
+    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
+                std::to_string(k));
+  if (bf6) {
+    const uint64_t need = dense_workspace_bytes(d, m, n, k);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail("kernel " + std::to_string(kernel_index) + " converts its operands into a workspace of " +
+                  std::to_string(need) + " bytes (amd_strix_halo_kernels_gemm_workspace_bytes)");
+    if (!aligned(workspace, 16)) return fail("the workspace must be 16-byte aligned");
+  }
+  if (gemm && (!aligned(out, 16) || !aligned(b_scale, 8) || !aligned(a_scale, 2)))
+    return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
+
+  const long kbytes = (long)k * d.dtype_bits / 8;
+  const int b_cols = swiglu ? 2 * n : n;
+  shk::DenseArgs& p = c.p;
+  p.a = static_cast<const uint8_t*>(a);
+  p.b = static_cast<const uint8_t*>(b);
+  p.a_scale = static_cast<const uint16_t*>(a_scale);
+  p.b_scale = static_cast<const uint16_t*>(b_scale);
+  p.out = out;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  const bool a_km = d.layout != SHK_LAYOUT_TN;
+  const bool b_km = d.layout == SHK_LAYOUT_NT;
+  p.lda = a_km ? kbytes : m;
+  p.ldb = b_km ? kbytes : b_cols;
+  p.b_cols = b_cols;
+  p.subchannel = subchannel;
+  p.scale_cols = subchannel > 0 ? (k + subchannel - 1) / subchannel : 1;
+  p.epilogue = epilogue == SHK_EPILOGUE_RELU2 ? shk::EPI_RELU2 : shk::EPI_NONE;
+  p.out_mode = out_mode;
+  // 16-byte pieces for K-major operands and for every operand of the
+  // direct-to-LDS and bf6 tiles; 8-byte rows otherwise.
+  const bool dma = d.num_stages > 2 || bf6;
+  const int a_need = (a_km || dma) ? 16 : 8;
+  const int b_need = (b_km || dma) ? 16 : 8;
+  p.a_aligned = !uses_a || (aligned(a, a_need) && p.lda % a_need == 0);
+  p.b_aligned = !uses_b || (aligned(b, b_need) && p.ldb % b_need == 0);
+  p.group_m = d.group_size_m;
+  p.layout = d.layout;
+  p.work = static_cast<uint8_t*>(workspace);
+  // Operands are addressed with 32-bit buffer offsets.
+  if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
+      (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))
+    return fail("dense operands must each be smaller than 4 GiB");
+  // Output stores address a tile's rows with 32-bit offsets from its first
+  // element: 256 rows of fp32 (or int32 [up | gate]) must stay below 4 GiB.
+  if ((unsigned long long)b_cols * 4ull * 256ull >= (1ull << 32))
+    return fail("dense output rows are limited to 4194304 bytes");
+  if (!p.a_aligned || !p.b_aligned)
+    return fail("kernel " + std::to_string(kernel_index) + " needs " + std::to_string(a_need) +
+                "-byte aligned A and " + std::to_string(b_need) + "-byte aligned B data pointers");
+  c.tiles = (long)(m / d.block_m) * (n / d.block_n);
+  if (c.tiles > 0x7FFFFFFFL) return fail("too many output tiles");
+  return 0;
+}
+
+
 }  // namespace
 
 extern "C" {
@@ -195,97 +312,47 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
                                           int32_t m, int32_t n, int32_t k, int32_t subchannel, int32_t epilogue,
                                           int32_t out_mode, void* workspace, uint64_t workspace_bytes) {
   g_last_error.clear();
-  const Entry* e = nullptr;
-  if (lookup(kernel_index, SHK_FAMILY_DENSE, &e)) return 1;
-  const shk_kernel_desc& d = e->d;
-  if (a == nullptr || b == nullptr || a_scale == nullptr || b_scale == nullptr || out == nullptr)
-    return fail("a, b, a_scale, b_scale, and out pointers must be non-null");
-  if (m <= 0 || n <= 0 || k <= 0)
-    return fail("M, N, and K must be positive; got (" + std::to_string(m) + ", " + std::to_string(n) + ", " +
-                std::to_string(k) + ")");
-  std::string why;
-  if (m % d.block_m) why += "M=" + std::to_string(m) + " is not divisible by BLOCK_M=" + std::to_string(d.block_m);
-  if (n % d.block_n) {
-    if (!why.empty()) why += "; ";
-    why += "N=" + std::to_string(n) + " is not divisible by BLOCK_N=" + std::to_string(d.block_n);
-  }
-  if (k % d.block_k) {
-    if (!why.empty()) why += "; ";
-    why += "K=" + std::to_string(k) + " is not divisible by BLOCK_K*SPLIT_K=" + std::to_string(d.block_k);
-  }
-  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && k % subchannel) {
-    if (!why.empty()) why += "; ";
-    why += "K=" + std::to_string(k) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
-  }
-  if (!why.empty()) return fail("kernel " + std::to_string(kernel_index) + " requires tile-multiple shape: " + why);
-  if (check_subchannel(d, subchannel)) return 1;
-  if (check_out_mode(out_mode)) return 1;
-  const bool swiglu = d.epilogue_kind == SHK_EPI_KIND_SWIGLU;
-  if (swiglu ? epilogue != SHK_EPILOGUE_SWIGLU : (epilogue != SHK_EPILOGUE_NONE && epilogue != SHK_EPILOGUE_RELU2))
-    return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
-  const bool bf6 = d.operand_format == SHK_OPERANDS_BF6;
-  if (bf6 && k > shk::F6_MAX_K)
-    return fail("bf6 kernels support K <= " + std::to_string(shk::F6_MAX_K) + "; got " + std::to_string(k));
-  if (!bf6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
-    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
-                std::to_string(k));
-  if (bf6) {
-    const uint64_t need = dense_workspace_bytes(d, m, n, k);
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail("kernel " + std::to_string(kernel_index) + " converts its operands into a workspace of " +
-                  std::to_string(need) + " bytes; pass it to amd_strix_halo_kernels_launch_gemm_ws");
-    if (!aligned(workspace, 16)) return fail("the workspace must be 16-byte aligned");
-  }
-  if (!aligned(out, 16) || !aligned(b_scale, 8) || !aligned(a_scale, 2))
-    return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
-
-  const long kbytes = (long)k * d.dtype_bits / 8;
-  const int b_cols = swiglu ? 2 * n : n;
-  shk::DenseArgs p{};
-  p.a = static_cast<const uint8_t*>(a);
-  p.b = static_cast<const uint8_t*>(b);
-  p.a_scale = static_cast<const uint16_t*>(a_scale);
-  p.b_scale = static_cast<const uint16_t*>(b_scale);
-  p.out = out;
-  p.M = m;
-  p.N = n;
-  p.K = k;
-  const bool a_km = d.layout != SHK_LAYOUT_TN;
-  const bool b_km = d.layout == SHK_LAYOUT_NT;
-  p.lda = a_km ? kbytes : m;
-  p.ldb = b_km ? kbytes : b_cols;
-  p.b_cols = b_cols;
-  p.subchannel = subchannel;
-  p.scale_cols = subchannel > 0 ? (k + subchannel - 1) / subchannel : 1;
-  p.epilogue = epilogue == SHK_EPILOGUE_RELU2 ? shk::EPI_RELU2 : shk::EPI_NONE;
-  p.out_mode = out_mode;
-  // 16-byte pieces for K-major operands and for every operand of the
-  // direct-to-LDS tiles (more than two stages); 8-byte rows otherwise.
-  const bool dma = d.num_stages > 2 || bf6;
-  const int a_need = (a_km || dma) ? 16 : 8;
-  const int b_need = (b_km || dma) ? 16 : 8;
-  p.a_aligned = aligned(a, a_need) && p.lda % a_need == 0;
-  p.b_aligned = aligned(b, b_need) && p.ldb % b_need == 0;
-  p.group_m = d.group_size_m;
-  p.layout = d.layout;
-  p.work = static_cast<uint8_t*>(workspace);
-  // Operands are addressed with 32-bit buffer offsets.
-  if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
-      (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))
-    return fail("dense operands must each be smaller than 4 GiB");
-  // Output stores address a tile's rows with 32-bit offsets from its first
-  // element: 256 rows of fp32 (or int32 [up | gate]) must stay below 4 GiB.
-  if ((unsigned long long)b_cols * 4ull * 256ull >= (1ull << 32))
-    return fail("dense output rows are limited to 4194304 bytes");
-  if (!p.a_aligned || !p.b_aligned)
-    return fail("kernel " + std::to_string(kernel_index) + " needs " + std::to_string(a_need) +
-                "-byte aligned A and " + std::to_string(b_need) + "-byte aligned B data pointers");
-  const long tiles = (long)(m / d.block_m) * (n / d.block_n);
-  if (tiles > 0x7FFFFFFFL) return fail("too many output tiles");
-
+  DenseCall c;
+  if (prepare_dense(c, kernel_index, PHASE_ALL, a, b, a_scale, b_scale, out, m, n, k, subchannel, epilogue,
+                    out_mode, workspace, workspace_bytes))
+    return 1;
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
-  const hipError_t err = e->dense(p, dim3((unsigned)tiles), reinterpret_cast<hipStream_t>(stream));
+  const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles), reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail_hip("kernel launch", err);
+  return 0;
+}
+
+int amd_strix_halo_kernels_gemm_convert(int kernel_index, int device_index, uintptr_t stream, int32_t operand,
+                                        const void* src, int32_t m, int32_t n, int32_t k, void* workspace,
+                                        uint64_t workspace_bytes) {
+  g_last_error.clear();
+  if (operand != 0 && operand != 1) return fail("operand must be 0 (A) or 1 (B)");
+  DenseCall c;
+  if (prepare_dense(c, kernel_index, operand == 0 ? PHASE_CONVERT_A : PHASE_CONVERT_B, operand == 0 ? src : nullptr,
+                    operand == 1 ? src : nullptr, nullptr, nullptr, nullptr, m, n, k, 0, 0, SHK_OUT_BF16, workspace,
+                    workspace_bytes))
+    return 1;
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const hipError_t err = shk::f6_convert_operand(c.p, operand, c.e->d.epilogue_kind == SHK_EPI_KIND_SWIGLU,
+                                                 reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail_hip("kernel launch", err);
+  return 0;
+}
+
+int amd_strix_halo_kernels_launch_gemm_converted(int kernel_index, int device_index, uintptr_t stream,
+                                                 const void* a_scale, const void* b_scale, void* out, int32_t m,
+                                                 int32_t n, int32_t k, int32_t epilogue, int32_t out_mode,
+                                                 const void* workspace, uint64_t workspace_bytes) {
+  g_last_error.clear();
+  DenseCall c;
+  if (prepare_dense(c, kernel_index, PHASE_GEMM, nullptr, nullptr, a_scale, b_scale, out, m, n, k, 0, epilogue,
+                    out_mode, const_cast<void*>(workspace), workspace_bytes))
+    return 1;
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const hipError_t err = c.e->converted(c.p, dim3((unsigned)c.tiles), reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail_hip("kernel launch", err);
   return 0;
 }

@@ -20,6 +20,7 @@ struct Entry {
   DenseLaunchFn dense;
   RaggedFwdLaunchFn fwd;
   RaggedBwdLaunchFn bwd;
+  DenseLaunchFn converted;  // bf6 entries: the GEMM alone, on converted operands
 };
 
 template <class C>
@@ -27,23 +28,30 @@ hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL(dense_gemm_kernel<C>, grid, dim3(C::NT), 0, s, a);
   return hipGetLastError();
 }
-// bf6 path: converts A and B into the workspace (layout-dependent), then
-// runs the GEMM on the converted operands.
-template <class C>
-hipError_t launch_f6_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
-  const bool a_mn = a.layout == SHK_LAYOUT_TN;
-  const bool b_mn = a.layout != SHK_LAYOUT_NT;
-  const unsigned long long a_bytes = f6_operand_bytes(a.M, a.K);
+// bf6 path.  f6_convert_operand converts A (operand 0) or B (operand 1) of
+// a dense call into its part of the workspace (A first, then B); the GEMM
+// then reads both parts.
+inline hipError_t f6_convert_operand(const DenseArgs& a, int operand, bool swiglu, hipStream_t s) {
   const int kb = a.K / 128;
-  hipError_t err = launch_f6_pack(F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0}, a_mn, s);
-  if (err != hipSuccess) return err;
-  err = launch_f6_pack(F6PackArgs{a.b, a.work + a_bytes, a.ldb, a.b_cols, kb, C::SWIGLU ? a.N : 0}, b_mn, s);
-  if (err != hipSuccess) return err;
+  if (operand == 0)
+    return launch_f6_pack(F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0}, a.layout == SHK_LAYOUT_TN, s);
+  return launch_f6_pack(F6PackArgs{a.b, a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0},
+                        a.layout != SHK_LAYOUT_NT, s);
+}
+template <class C>
+hipError_t launch_f6_gemm_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   DenseArgs g = a;
   g.a = a.work;
-  g.b = a.work + a_bytes;
+  g.b = a.work + f6_operand_bytes(a.M, a.K);
   hipLaunchKernelGGL(f6_gemm_kernel<C>, grid, dim3(256), 0, s, g);
   return hipGetLastError();
+}
+template <class C>
+hipError_t launch_f6_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  hipError_t err = f6_convert_operand(a, 0, C::SWIGLU, s);
+  if (err == hipSuccess) err = f6_convert_operand(a, 1, C::SWIGLU, s);
+  if (err == hipSuccess) err = launch_f6_gemm_t<C>(a, grid, s);
+  return err;
 }
 template <class C>
 hipError_t launch_fwd_t(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
@@ -80,7 +88,7 @@ constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
 
 template <class C>
 Entry dense_entry(int layout, int group_m) {
-  return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_dense_t<C>, nullptr, nullptr};
+  return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_dense_t<C>, nullptr, nullptr, nullptr};
 }
 template <class C>
 Entry f6_entry(int layout) {
@@ -88,15 +96,15 @@ Entry f6_entry(int layout) {
   d.num_stages = F6Engine<C>::P;
   d.lds_bytes = F6Engine<C>::LDS_BYTES;
   d.operand_format = SHK_OPERANDS_BF6;
-  return Entry{d, &launch_f6_t<C>, nullptr, nullptr};
+  return Entry{d, &launch_f6_t<C>, nullptr, nullptr, &launch_f6_gemm_t<C>};
 }
 template <class C>
 Entry fwd_entry(int layout) {
-  return Entry{desc_of<C>(SHK_FAMILY_RAGGED_FWD, layout, 1), nullptr, &launch_fwd_t<C>, nullptr};
+  return Entry{desc_of<C>(SHK_FAMILY_RAGGED_FWD, layout, 1), nullptr, &launch_fwd_t<C>, nullptr, nullptr};
 }
 template <class C>
 Entry bwd_entry(int layout) {
-  return Entry{desc_of<C>(SHK_FAMILY_RAGGED_BWD, layout, 1), nullptr, nullptr, &launch_bwd_t<C>};
+  return Entry{desc_of<C>(SHK_FAMILY_RAGGED_BWD, layout, 1), nullptr, nullptr, &launch_bwd_t<C>, nullptr};
 }
 
 // Each kernel translation unit appends its entries in a fixed order

@@ -212,3 +212,26 @@ def test_bf6_k_limit_keeps_fp32_sums_exact(lib):
     assert kt.BF6_MAX_K * 64 == 1 << 24
     assert _gemm_ws(lib, idx, 256, 256, kt.BF6_MAX_K + 128, work=FAKE, work_bytes=1 << 40) == 1
     assert "K <= 262144" in _err(lib)
+
+
+def test_split_bf6_phases_validate_their_arguments(lib):
+    bf6 = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_BF6)
+    packed = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
+    conv = lib.amd_strix_halo_kernels_gemm_convert
+    gemm = lib.amd_strix_halo_kernels_launch_gemm_converted
+    assert conv(packed, 0, 0, 0, FAKE, 256, 256, 128, FAKE, 1 << 20) == 1
+    assert "only bf6 entries" in _err(lib)
+    assert conv(bf6, 0, 0, 2, FAKE, 256, 256, 128, FAKE, 1 << 20) == 1
+    assert "operand must be 0 (A) or 1 (B)" in _err(lib)
+    assert conv(bf6, 0, 0, 1, None, 256, 256, 128, FAKE, 1 << 20) == 1
+    assert "non-null" in _err(lib)
+    assert conv(bf6, 0, 0, 0, FAKE, 256, 256, 128, FAKE, 100) == 1
+    assert "workspace of 49152 bytes" in _err(lib)
+    assert conv(bf6, 0, 0, 0, FAKE, 250, 256, 128, FAKE, 1 << 20) == 1
+    assert "M=250 is not divisible by BLOCK_M=256" in _err(lib)
+    assert gemm(packed, 0, 0, FAKE, FAKE, FAKE, 64, 64, 64, 0, 0, FAKE, 1 << 20) == 1
+    assert "only bf6 entries" in _err(lib)
+    assert gemm(bf6, 0, 0, FAKE, FAKE, FAKE, 256, 256, 128, kt.EPILOGUE_SWIGLU, 0, FAKE, 1 << 20) == 1
+    assert "does not match the kernel's epilogue kind" in _err(lib)
+    assert gemm(bf6, 0, 0, FAKE, FAKE, None, 256, 256, 128, 0, 0, FAKE, 1 << 20) == 1
+    assert "a_scale, b_scale, and out pointers must be non-null" in _err(lib)

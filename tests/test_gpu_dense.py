@@ -275,3 +275,32 @@ def test_bf6_exact_at_the_k_bound(layout, device):
     assert raw[0, 0] == 1 << 24
     assert np.array_equal(raw, want)
     assert np.array_equal(got, ref.bf16_round(want.astype(np.float32)))
+
+
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+@pytest.mark.parametrize("epilogue", ["none", "swiglu"])
+def test_bf6_converted_operands_are_reusable(layout, epilogue, device):
+    """convert(B) once, then convert(A) + GEMM for two different A: each
+    result equals the one-call launch bit for bit."""
+    m, n, k = 512, 256, 384
+    swiglu = epilogue == "swiglu"
+    spec = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL)
+    kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=spec, epilogue=shk.Epilogue(epilogue),
+                                         m=m, n=n, k=k, layout=shk.GemmLayout(layout))
+    assert kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_BF6
+    _, _, _, b_arg, _, sb = dense_case(11, bits=4, layout=layout, m=m, n=n, k=k, subchannel=None, swiglu=swiglu)
+    b = to_dev(torch, b_arg, device)
+    tb = to_dev(torch, sb, device)
+    work = native.gemm_workspace(kernel, m, n, k, device=device)
+    print(f"case bf6 reuse {layout} {epilogue}", flush=True)
+    native.convert_operand(kernel, 1, b, m=m, n=n, k=k, workspace=work)
+    for seed in (12, 13):
+        _, _, a_arg, _, sa, _ = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=None, swiglu=swiglu)
+        a = to_dev(torch, a_arg, device)
+        ta = to_dev(torch, sa, device)
+        native.convert_operand(kernel, 0, a, m=m, n=n, k=k, workspace=work)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+        native.launch_converted(kernel, m=m, n=n, k=k, workspace=work, a_scale=ta, b_scale=tb, out=out)
+        direct = shk.explicit_mm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16_bits(torch, out), bf16_bits(torch, direct))
