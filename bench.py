@@ -12,10 +12,10 @@ K-ragged backward, G=8, M=8192, K=2048, N=1408).
 A step is one API call over operands already resident in HBM; the timed region
 is exactly K steps bracketed by a device synchronisation on both sides.
 Kernel durations come from HIP events recorded around every launch on the
-stream the kernel runs on (torch's current stream).  C2 runs on the bf6 path
+stream the kernel runs on (torch's current stream).  C2 runs on the fp6 path
 (two operand conversions, then the GEMM); the same three launches are also
 made through the split C ABI with an event between each, which gives the GEMM
-kernel's own duration for the roofline (bf6 MFMA peak) beside the whole
+kernel's own duration for the roofline (fp6 MFMA peak) beside the whole
 call's throughput (`value`, also reported against the int8 MFMA peak).  No cache flush between
 steps (steady state, the operands of C2 fit the 256 MB MALL); a cold run that
 overwrites a 1 GiB buffer before each launch is reported beside it.  The CPU
@@ -39,7 +39,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "int4 GEMM TOPS @8192³ (% gfx950 int8 MFMA peak); fused SwiGLU TOPS"
 INT8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, published
-BF6_MFMA_PEAK_TFLOPS = 10100.0  # MI355X dense fp6/fp4 MFMA, published
+FP6_MFMA_PEAK_TFLOPS = 10100.0  # MI355X dense fp6/fp4 MFMA, published
 HBM_PEAK_GBS = 8000.0
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = ROOT / "profiles" / "f6_gemm_c2_8192_traffic.txt"
@@ -110,8 +110,8 @@ def _uniform_bf16(torch, shape, lo, hi, gen):
     return (torch.rand(shape, device="cuda", generator=gen) * (hi - lo) + lo).to(torch.bfloat16)
 
 
-def _split_bf6_times(torch, shk, kernel, a, b, sa, sb, m, n, k, steps, warmup):
-    """Per-kernel durations of a bf6 launch: the same three launches as
+def _split_fp6_times(torch, shk, kernel, a, b, sa, sb, m, n, k, steps, warmup):
+    """Per-kernel durations of a fp6 launch: the same three launches as
     ``mm`` (convert A, convert B, GEMM) made through the split C ABI with a HIP
     event between each, on torch's current stream.  Returns mean ms of
     (convert A, convert B, GEMM)."""
@@ -169,10 +169,10 @@ def bench_c2(torch, shk, steps, warmup):
     res = {
         "m": m, "n": n, "k": k, "kernel": kernel.kernel_id, "ops": ops, "bytes": bytes_alg,
         "wall_ms": wall, "kernel_ms": kern_mean, "kernel_ms_median": kern_med, "cold_kernel_ms": cold,
-        "host": (a, b, sa, sb), "bf6": kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_BF6,
+        "host": (a, b, sa, sb), "fp6": kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_FP6,
     }
-    if res["bf6"]:
-        res["convert_a_ms"], res["convert_b_ms"], res["gemm_ms"] = _split_bf6_times(
+    if res["fp6"]:
+        res["convert_a_ms"], res["convert_b_ms"], res["gemm_ms"] = _split_fp6_times(
             torch, shk, kernel, a, b, sa, sb, m, n, k, steps, warmup)
     return res
 
@@ -371,15 +371,15 @@ def main(argv=None) -> int:
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (C oracle)")
         cpu = cpu_baseline(torch, c2["host"])
-    if c2["bf6"]:
-        # the dominant kernel is the bf6 GEMM (f6_gemm_kernel); the two
+    if c2["fp6"]:
+        # the dominant kernel is the fp6 GEMM (f6_gemm_kernel); the two
         # operand conversions are reported beside it
         achieved = c2["ops"] / (c2["gemm_ms"] * 1e-3) / 1e12
-        peak = BF6_MFMA_PEAK_TFLOPS
-        dtype = "bf6"
-        operands = ("packed int4 converted to bf6 (e3m2, exact for -8..7) blocks in a workspace, "
-                    "bf6 MFMA (v_mfma_scale_f32_16x16x128_f8f6f4), fp32 accumulation exact for K <= 262144")
-        note = ("bf6 MFMA tera-ops/s of the GEMM kernel: algorithmic 2*M*N*K over its HIP-event launch duration; "
+        peak = FP6_MFMA_PEAK_TFLOPS
+        dtype = "fp6"
+        operands = ("packed int4 converted to fp6 blocks in a workspace (e2m3 holding v/8, exact for -8..7), "
+                    "fp6 MFMA (v_mfma_f32_32x32x64_f8f6f4), fp32 accumulation exact for K <= 262144")
+        note = ("fp6 MFMA tera-ops/s of the GEMM kernel: algorithmic 2*M*N*K over its HIP-event launch duration; "
                 "value counts the whole mm() call including both operand conversions")
     else:
         achieved = tops_kernel
@@ -416,11 +416,11 @@ def main(argv=None) -> int:
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": achieved / peak,
-            "traffic": _measured_traffic() if c2["bf6"] else None,
+            "traffic": _measured_traffic() if c2["fp6"] else None,
             "note": note,
         },
-        "bf6_launch_ms": ({"convert_a": c2["convert_a_ms"], "convert_b": c2["convert_b_ms"], "gemm": c2["gemm_ms"]}
-                          if c2["bf6"] else None),
+        "fp6_launch_ms": ({"convert_a": c2["convert_a_ms"], "convert_b": c2["convert_b_ms"], "gemm": c2["gemm_ms"]}
+                          if c2["fp6"] else None),
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

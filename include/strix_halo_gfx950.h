@@ -64,12 +64,12 @@ extern "C" {
 #define SHK_OUT_I32 2
 
 /* Operand formats of a dense entry.  PACKED kernels read A and B as given;
- * BF6 kernels (int4 only) first convert both operands into a caller
+ * FP6 kernels (int4 only) first convert both operands into a caller
  * workspace of amd_strix_halo_kernels_gemm_workspace_bytes() bytes: every
- * int4 value -8..7 is exact in the 6-bit float e3m2, whose MFMA runs at
+ * int4 value v is exact as v/8 in the 6-bit float e2m3, whose MFMA runs at
  * twice the int8 rate; the fp32 accumulation is exact for K <= 262144. */
 #define SHK_OPERANDS_PACKED 0
-#define SHK_OPERANDS_BF6 1
+#define SHK_OPERANDS_FP6 1
 
 typedef struct shk_kernel_desc {
   int32_t index;
@@ -133,7 +133,7 @@ int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out);
  * b_scale[ceil(k/S), b_cols].  Requires m % block_m == 0, n % block_n == 0,
  * k % block_k == 0 and (subchannel) k % S == 0 (reference
  * template_config.py:22-38).  `gate` of the reference signature is dropped:
- * SwiGLU is fused.  Entries with operand_format SHK_OPERANDS_BF6 need a
+ * SwiGLU is fused.  Entries with operand_format SHK_OPERANDS_FP6 need a
  * workspace and are launched with amd_strix_halo_kernels_launch_gemm_ws;
  * this function refuses them. */
 int amd_strix_halo_kernels_launch_gemm(int kernel_index, int device_index, uintptr_t stream,
@@ -160,7 +160,7 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
                                           int32_t k, int32_t subchannel, int32_t epilogue,
                                           int32_t out_mode, void* workspace, uint64_t workspace_bytes);
 
-/* The two halves of a bf6 launch, for callers that convert an operand once
+/* The two halves of a fp6 launch, for callers that convert an operand once
  * and multiply it many times (a weight matrix), and for timing the GEMM
  * kernel on its own.  amd_strix_halo_kernels_gemm_convert converts operand 0
  * (A, laid out as for launch_gemm) or operand 1 (B) of shape (m, n, k) into

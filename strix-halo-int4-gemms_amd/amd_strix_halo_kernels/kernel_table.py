@@ -38,12 +38,12 @@ OUT_BF16 = 0
 OUT_F32 = 1
 OUT_I32 = 2
 
-# Operand formats: PACKED entries read A and B as given; BF6 entries convert
-# both int4 operands into a caller workspace in the bf6 (e3m2) block format
+# Operand formats: PACKED entries read A and B as given; FP6 entries convert
+# both int4 operands into a caller workspace in the fp6 (e2m3, v/8) block format
 # first (amd_strix_halo_kernels_gemm_workspace_bytes).
 OPERANDS_PACKED = 0
-OPERANDS_BF6 = 1
-BF6_MAX_K = 262144
+OPERANDS_FP6 = 1
+FP6_MAX_K = 262144
 
 
 @dataclass(frozen=True)
@@ -69,7 +69,7 @@ class KernelDesc:
 
     @property
     def needs_workspace(self) -> bool:
-        return self.operand_format == OPERANDS_BF6
+        return self.operand_format == OPERANDS_FP6
 
     def workspace_bytes(self, m: int, n: int, k: int) -> int:
         """Bytes of the operand workspace for shape (m, n, k) (0 for PACKED)."""
@@ -85,12 +85,12 @@ class KernelDesc:
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
-          bf6=False):
+          fp6=False):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
-    # bf6: three stages of 256 A rows + 256 B rows x 128 K in bf6 (96 bytes).
+    # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
     brows = 2 * bn if swiglu else bn
-    if bf6:
+    if fp6:
         pipe = 3
         lds = pipe * (bm + 256) * 96
     else:
@@ -111,7 +111,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         num_stages=pipe or 2,
         lds_bytes=lds,
         group_size_m=group_m,
-        operand_format=OPERANDS_BF6 if bf6 else OPERANDS_PACKED,
+        operand_format=OPERANDS_FP6 if fp6 else OPERANDS_PACKED,
     )
 
 
@@ -126,8 +126,8 @@ def _build() -> tuple[KernelDesc, ...]:
         for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
             d = dict(family=FAMILY_DENSE, bits=bits, layout=layout)
             if bits == 4:
-                add(**d, bm=256, bn=256, bk=128, wm=2, wn=2, bf6=True)
-                add(**d, bm=256, bn=128, bk=128, wm=2, wn=2, swiglu=True, bf6=True)
+                add(**d, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
+                add(**d, bm=256, bn=128, bk=128, wm=2, wn=2, swiglu=True, fp6=True)
             add(**d, bm=256, bn=256, bk=big_bk, wm=2, wn=2, pipe=4)
             add(**d, bm=256, bn=128, bk=big_bk, wm=2, wn=2, swiglu=True, pipe=4)
             add(**d, bm=128, bn=128, bk=64, wm=2, wn=2)

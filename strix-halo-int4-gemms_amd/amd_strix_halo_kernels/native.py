@@ -283,7 +283,7 @@ def gemm_workspace_bytes(kernel: KernelMetadata, m: int, n: int, k: int, *, libr
 def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, library_path, stream) -> None:
     lib = _verified_library(library_path)
     sub = kernel.scale.subchannel_size if kernel.scale.mode is ScaleMode.SUBCHANNEL else 0
-    # bf6 entries convert both operands into a workspace first; it comes from
+    # fp6 entries convert both operands into a workspace first; it comes from
     # torch's caching allocator on the launch stream, so a later launch on
     # the same stream may reuse it.
     ws_bytes = gemm_workspace_bytes(kernel, m, n, k, library_path=library_path)
@@ -312,7 +312,7 @@ def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, li
 
 
 def gemm_workspace(kernel: KernelMetadata, m: int, n: int, k: int, *, device: Any, library_path=None) -> Any:
-    """A uint8 workspace tensor for a bf6 kernel's converted operands."""
+    """A uint8 workspace tensor for a fp6 kernel's converted operands."""
     torch = _torch()
     return torch.empty(gemm_workspace_bytes(kernel, m, n, k, library_path=library_path), dtype=torch.uint8,
                        device=device)
@@ -320,7 +320,7 @@ def gemm_workspace(kernel: KernelMetadata, m: int, n: int, k: int, *, device: An
 
 def convert_operand(kernel: KernelMetadata, operand: int, src: Any, *, m: int, n: int, k: int, workspace: Any,
                     library_path=None, stream: Any | None = None) -> None:
-    """Converts A (operand 0) or B (operand 1) of a bf6 kernel into its part
+    """Converts A (operand 0) or B (operand 1) of a fp6 kernel into its part
     of `workspace` (amd_strix_halo_kernels_gemm_convert)."""
     torch = _torch()
     lib = _verified_library(library_path)
@@ -334,7 +334,7 @@ def convert_operand(kernel: KernelMetadata, operand: int, src: Any, *, m: int, n
 
 def launch_converted(kernel: KernelMetadata, *, m: int, n: int, k: int, workspace: Any, a_scale: Any, b_scale: Any,
                      out: Any, out_mode: int = kt.OUT_BF16, library_path=None, stream: Any | None = None) -> Any:
-    """GEMM of a bf6 kernel on operands already converted into `workspace`
+    """GEMM of a fp6 kernel on operands already converted into `workspace`
     (amd_strix_halo_kernels_launch_gemm_converted)."""
     torch = _torch()
     lib = _verified_library(library_path)

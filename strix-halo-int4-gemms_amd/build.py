@@ -61,7 +61,7 @@ def translation_units() -> list[tuple[str, Path, list[str]]]:
             defs = [f"-DSHK_BITS={bits}", f"-DSHK_LAYOUT={layout}"]
             units.append((f"dense_dma_{bits}_{layout}", CSRC / "k_dense.hip", [*defs, "-DSHK_DENSE_DMA=1", *DMA_FLAGS]))
             units.append((f"dense_{bits}_{layout}", CSRC / "k_dense.hip", [*defs, "-DSHK_DENSE_DMA=0"]))
-    # bf6 path: the GEMM keeps 256 accumulators like the DMA objects; the
+    # fp6 path: the GEMM keeps 256 accumulators like the DMA objects; the
     # operand conversion is compiled with the default scheduler.
     units.append(("dense_f6", CSRC / "k_f6.hip", list(DMA_FLAGS)))
     units.append(("f6pack", CSRC / "k_f6pack.hip", []))

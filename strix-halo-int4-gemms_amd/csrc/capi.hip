@@ -110,10 +110,10 @@ int check_out_mode(int out_mode) {
   return 0;
 }
 
-// Workspace of a dense entry: both operands in bf6 block format for BF6
+// Workspace of a dense entry: both operands in fp6 block format for FP6
 // entries, nothing otherwise.
 uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k) {
-  if (d.operand_format != SHK_OPERANDS_BF6) return 0;
+  if (d.operand_format != SHK_OPERANDS_FP6) return 0;
   const long b_cols = d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2L * n : (long)n;
   return shk::f6_operand_bytes(m, k) + shk::f6_operand_bytes(b_cols, k);
 }
@@ -123,7 +123,7 @@ uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, i
 constexpr int kMaxInt4AccK = 131072;
 
 // A validated dense call.  PHASE_ALL is a whole launch; the other phases are
-// the separately launched parts of a bf6 entry: converting A, converting B,
+// the separately launched parts of a fp6 entry: converting A, converting B,
 // and the GEMM on converted operands.  Each phase checks the arguments it
 // uses; all of them check the shape and the workspace.
 enum Phase { PHASE_ALL, PHASE_CONVERT_A, PHASE_CONVERT_B, PHASE_GEMM };
@@ -139,13 +139,13 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
                   int32_t epilogue, int32_t out_mode, void* workspace, uint64_t workspace_bytes) {
   if (lookup(kernel_index, SHK_FAMILY_DENSE, &c.e)) return 1;
   const shk_kernel_desc& d = c.e->d;
-  const bool bf6 = d.operand_format == SHK_OPERANDS_BF6;
+  const bool fp6 = d.operand_format == SHK_OPERANDS_FP6;
   const bool uses_a = phase == PHASE_ALL || phase == PHASE_CONVERT_A;
   const bool uses_b = phase == PHASE_ALL || phase == PHASE_CONVERT_B;
   const bool gemm = phase == PHASE_ALL || phase == PHASE_GEMM;
-  if (phase != PHASE_ALL && !bf6)
+  if (phase != PHASE_ALL && !fp6)
     return fail("kernel " + std::to_string(kernel_index) +
-                " reads its operands directly; only bf6 entries convert them separately");
+                " reads its operands directly; only fp6 entries convert them separately");
   if ((uses_a && a == nullptr) || (uses_b && b == nullptr) ||
       (gemm && (a_scale == nullptr || b_scale == nullptr || out == nullptr))) {
     if (phase == PHASE_ALL) return fail("a, b, a_scale, b_scale, and out pointers must be non-null");
@@ -177,12 +177,12 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
     if (swiglu ? epilogue != SHK_EPILOGUE_SWIGLU : (epilogue != SHK_EPILOGUE_NONE && epilogue != SHK_EPILOGUE_RELU2))
       return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
   }
-  if (bf6 && k > shk::F6_MAX_K)
-    return fail("bf6 kernels support K <= " + std::to_string(shk::F6_MAX_K) + "; got " + std::to_string(k));
-  if (!bf6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
+  if (fp6 && k > shk::F6_MAX_K)
+    return fail("fp6 kernels support K <= " + std::to_string(shk::F6_MAX_K) + "; got " + std::to_string(k));
+  if (!fp6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
                 std::to_string(k));
-  if (bf6) {
+  if (fp6) {
     const uint64_t need = dense_workspace_bytes(d, m, n, k);
     if (workspace == nullptr || workspace_bytes < need)
       return fail("kernel " + std::to_string(kernel_index) + " converts its operands into a workspace of " +
@@ -213,8 +213,8 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
   p.epilogue = epilogue == SHK_EPILOGUE_RELU2 ? shk::EPI_RELU2 : shk::EPI_NONE;
   p.out_mode = out_mode;
   // 16-byte pieces for K-major operands and for every operand of the
-  // direct-to-LDS and bf6 tiles; 8-byte rows otherwise.
-  const bool dma = d.num_stages > 2 || bf6;
+  // direct-to-LDS and fp6 tiles; 8-byte rows otherwise.
+  const bool dma = d.num_stages > 2 || fp6;
   const int a_need = (a_km || dma) ? 16 : 8;
   const int b_need = (b_km || dma) ? 16 : 8;
   p.a_aligned = !uses_a || (aligned(a, a_need) && p.lda % a_need == 0);

@@ -1,4 +1,4 @@
-// GEMM kernels of the bf6 path (shk_f6.h): the 256x256 per-channel tile and
+// GEMM kernels of the fp6 path (shk_f6.h): the 256x256 per-channel tile and
 // the 256x128 SwiGLU tile.  They read operands already converted to the
 // block format, so one instantiation serves every layout; the table holds
 // one entry per layout (NN, NT, TN), which differ in how the operands are

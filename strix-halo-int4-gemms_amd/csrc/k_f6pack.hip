@@ -1,4 +1,4 @@
-// Operand conversion of the bf6 GEMM path: packed int4 (either layout) to
+// Operand conversion of the fp6 GEMM path: packed int4 (either layout) to
 // the block format of shk_f6.h.  Compiled apart from the GEMM, with the
 // default scheduler.
 #include "shk_table.h"
@@ -6,10 +6,10 @@
 namespace shk {
 namespace {
 
-// 16 packed int4 bytes -> the lane's 24 bf6 bytes.  x ^ 0x8 per nibble is the
-// offset-binary value v + 8; 0x6400 | (v + 8) is the f16 1024 + v + 8, and
-// subtracting 1032 leaves v exactly.  The conversion to bf6 is exact for
-// these values (scale 1).
+// 16 packed int4 bytes -> the lane's 24 fp6 bytes.  x ^ 0x8 per nibble is
+// the offset-binary value v + 8; 0x6400 | (v + 8) is the f16 1024 + v + 8;
+// subtracting 1032 and scaling by 1/8 gives v/8 exactly (f16 holds both
+// steps exactly), and v/8 is exact in e2m3.
 __device__ __forceinline__ v6i f6_convert(const uint4& x) {
   f6_h32 h;
   const uint32_t w[4] = {x.x, x.y, x.z, x.w};
@@ -19,12 +19,13 @@ __device__ __forceinline__ v6i f6_convert(const uint4& x) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t d = ((u >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
-      const f6_h2 v = __builtin_bit_cast(f6_h2, d) - f6_h2{(_Float16)1032.0f, (_Float16)1032.0f};
+      f6_h2 v = __builtin_bit_cast(f6_h2, d) - f6_h2{(_Float16)1032.0f, (_Float16)1032.0f};
+      v = v * f6_h2{(_Float16)0.125f, (_Float16)0.125f};
       h[8 * q + 2 * j] = v.x;
       h[8 * q + 2 * j + 1] = v.y;
     }
   }
-  return __builtin_bit_cast(v6i, __builtin_amdgcn_cvt_scalef32_pk32_bf6_f16(h, 1.0f));
+  return __builtin_bit_cast(v6i, __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(h, 1.0f));
 }
 
 __device__ __forceinline__ void f6_store_lane(uint8_t* block, int lane, const v6i& y) {
@@ -49,43 +50,48 @@ __global__ __launch_bounds__(256) void f6_pack_kmajor(const F6PackArgs p) {
   const long blk = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int panel = (int)(blk / p.kb);
   const int kb = (int)(blk - (long)panel * p.kb);
-  const int row = f6_src_row(16 * panel + (lane & 15), p.swiglu_n);
-  const uint4 x = *reinterpret_cast<const uint4*>(p.src + (long)row * p.ld + 64L * kb + 16 * (lane >> 4));
+  const int row = f6_src_row(32 * panel + (lane & 31), p.swiglu_n);
+  const uint4 x = *reinterpret_cast<const uint4*>(p.src + (long)row * p.ld + 32L * kb + 16 * (lane >> 5));
   f6_store_lane(p.dst + blk * F6_BLOCK, lane, f6_convert(x));
 }
 
 // MN-major source (K row kp holds two K values of every packed row, one per
-// nibble): a workgroup converts the 16 blocks of one 256-row tile and one K
-// block.  The 64 x 256-byte source tile goes through LDS in the MN-major
-// ring layout of the DMA engine, whose transposing reads hand each lane its
-// row's 16 bytes in K order.
+// nibble): a workgroup converts the 8 blocks of one 256-row tile and one
+// 64-K block.  The 32 x 256-byte source tile goes through LDS in the
+// MN-major ring layout of the DMA engine, whose transposing reads hand each
+// lane its row's bytes in K order: within a 16-lane group, lane i addresses
+// source row kp + i/2 at byte 8*(i%2) of a 16-row unit and receives the 8
+// bytes of those 8 rows in column i.
 __global__ __launch_bounds__(256) void f6_pack_mnmajor(const F6PackArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[64 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * 256];
   const int t = blockIdx.x / p.kb;
   const int kb = blockIdx.x - t * p.kb;
   const int tid = threadIdx.x;
   const int u = tid & 15;  // 16-row unit of the tile
   const long col = f6_src_row(F6_TILE * t + 16 * u, p.swiglu_n);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < 2; ++q) {
     const int kp = 16 * q + (tid >> 4);
-    const uint4 x = *reinterpret_cast<const uint4*>(p.src + (64L * kb + kp) * p.ld + col);
+    const uint4 x = *reinterpret_cast<const uint4*>(p.src + (32L * kb + kp) * p.ld + col);
     const int swz = (kp & 7) | ((kp & 16) >> 1);
     *reinterpret_cast<uint4*>(tile + kp * 256 + 16 * (u ^ swz)) = x;
   }
   __syncthreads();
+  // lane l of a block: packed row 32b + l % 32 (unit 2b + (l/16) % 2, column
+  // l % 16 of it), K rows 16*(l/32) + [0, 16)
   const int lane = tid & 63;
-  const int l15 = lane & 15, g = lane >> 4;
-  const int kp = 16 * g + l15 / 2;
+  const int i = lane & 15;
+  const int kp = 16 * (lane >> 5) + i / 2;
   const int swz = (kp & 7) | ((kp & 16) >> 1);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int unit = 4 * (tid >> 6) + c;
-    const uint8_t* q = tile + kp * 256 + 16 * (unit ^ swz) + 8 * (l15 & 1);
+  for (int c = 0; c < 2; ++c) {
+    const int b = 2 * (tid >> 6) + c;
+    const int unit = 2 * b + ((lane >> 4) & 1);
+    const uint8_t* q = tile + kp * 256 + 16 * (unit ^ swz) + 8 * (i & 1);
     const v2i lo = ds_read_tr8(q);
     const v2i hi = ds_read_tr8(q + 2048);
     const uint4 x = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    const long blk = (long)(16 * t + unit) * p.kb + kb;
+    const long blk = (long)(8 * t + b) * p.kb + kb;
     f6_store_lane(p.dst + blk * F6_BLOCK, lane, f6_convert(x));
   }
 }
@@ -96,7 +102,7 @@ hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s) {
   if (mn_major) {
     hipLaunchKernelGGL(f6_pack_mnmajor, dim3((a.rows / F6_TILE) * a.kb), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL(f6_pack_kmajor, dim3((a.rows / 16) * a.kb / 4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(f6_pack_kmajor, dim3((a.rows / 32) * a.kb / 4), dim3(256), 0, s, a);
   }
   return hipGetLastError();
 }

@@ -1,29 +1,33 @@
-// int4 x int4 dense GEMM on the bf6 (e3m2) MFMA.
+// int4 x int4 dense GEMM on the fp6 MFMA.
 //
-// gfx950 has no int4 MFMA, but every int4 value -8..7 is exact in the 6-bit
-// float format e3m2 ("bf6": sign, 3 exponent bits with bias 3, 2 mantissa
-// bits: 1, 2, 3 = 1.5*2, 4, 5 = 1.25*4, 6, 7 = 1.75*4 and 8 are all
-// representable), and v_mfma_scale_f32_16x16x128_f8f6f4 multiplies bf6
-// operands at twice the int8 MFMA rate.  Products of two such values are
-// integers of magnitude <= 64 and the MFMA accumulates in fp32, which holds
-// every integer below 2^24 exactly, so for K <= 2^18 every partial sum, and
-// the result, is the exact int32 sum (|sum| <= 64 * K <= 2^24).  The epilogue
-// therefore sees the same integer as the int8 engines and produces the same
-// bits.
+// gfx950 has no int4 MFMA, and -8..7 does not fit fp4 e2m1.  Every int4 value
+// v is, however, exact as v/8 in the 6-bit float e2m3 ("fp6": sign, 2
+// exponent bits with bias 1, 3 mantissa bits): |v| <= 7 are the subnormals
+// |v|/8 and 8 is 2^0, so the code is simply sign << 5 | |v|.  The f8f6f4 MFMA
+// multiplies fp6 operands at twice the int8 MFMA rate.  A product of two such
+// operands is an integer / 64 of magnitude <= 1, and the MFMA accumulates in
+// fp32, which holds every multiple of 1/64 below 2^18 exactly, so for
+// K <= 2^18 every partial sum is exact and 64 * acc is the exact int32 sum
+// (|sum| <= 64 * K <= 2^24).  The epilogue therefore sees the same integer as
+// the int8 engines and produces the same bits.  e2m3 rather than bf6 (e3m2,
+// where -8..7 are exact too) because the same MFMA then draws less power,
+// which is the limit on this chip with full-rate MFMAs on random data.  The
+// GEMM issues v_mfma_f32_32x32x64_f8f6f4 (cbsz = blgp = 2: both operands
+// e2m3).
 //
 // The path runs in two launches:
 //  1. f6_pack_* converts each operand, in whichever layout it arrives, into
-//     the "block" format in a caller workspace: a 16-row x 128-K block is
-//     1536 bytes, 24 per MFMA lane (lane l: row l % 16, K values
-//     32*(l/16) + [0, 32) of the block) split into a 1024-byte part (the
+//     the "block" format in a caller workspace: a 32-row x 64-K block is
+//     1536 bytes, 24 per MFMA lane (lane l: row l % 32, K values
+//     32*(l/32) + [0, 32) of the block) split into a 1024-byte part (the
 //     lane's first 16 bytes at 16*l) and a 512-byte part (its last 8 bytes at
 //     1024 + 8*l).  Blocks are stored panel-major: block (p, kb) of the
-//     16-row panel p and K block kb sits at (p * KB + kb) * 1536.
-//  2. f6_gemm_kernel streams 256 x 128 blocks of both operands with LDS-DMA
-//     into a three-slot ring (48 KiB per stage) and reads each fragment with
-//     one ds_read_b128 and one ds_read_b64 of consecutive lane addresses,
-//     which is free of bank conflicts without a swizzle.  The K loop has no
-//     VALU work: DMA, LDS reads and MFMAs only.
+//     32-row panel p and 64-K block kb sits at (p * K/64 + kb) * 1536.
+//  2. f6_gemm_kernel streams the 256-row x 128-K stages of both operands
+//     with LDS-DMA into a three-slot ring (48 KiB per stage) and reads each
+//     fragment with one ds_read_b128 and one ds_read_b64 of consecutive lane
+//     addresses, which is free of bank conflicts without a swizzle.  The K
+//     loop has no VALU work: DMA, LDS reads and MFMAs only.
 //
 // K order inside a lane's 32 values.  The conversion turns the lane's 16
 // packed bytes (byte b holds K values 2b, 2b+1, low nibble first) into f16
@@ -40,12 +44,16 @@
 namespace shk {
 
 typedef int v6i __attribute__((ext_vector_type(6)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 f6_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f6_h32 __attribute__((ext_vector_type(32)));
 
-constexpr int F6_BLOCK = 1536;     // bytes of a 16-row x 128-K bf6 block
+constexpr int F6_BLOCK = 1536;     // bytes of a 32-row x 64-K fp6 block
 constexpr int F6_MAX_K = 262144;   // 64 * K <= 2^24: fp32 partial sums stay exact
 constexpr int F6_TILE = 256;       // packed rows per GEMM tile (A rows, B columns)
+// Each operand holds v/8, so the accumulator is sum / 64; multiplying by 64
+// is exact.
+constexpr float F6_UNSCALE = 64.0f;
 
 // Bytes of one operand with `rows` rows (a multiple of 256) and K (a
 // multiple of 128) in block format.
@@ -58,7 +66,7 @@ struct F6PackArgs {
   uint8_t* dst;
   long ld;       // bytes between consecutive source rows
   int rows;      // packed rows (a multiple of 256)
-  int kb;        // K / 128
+  int kb;        // K / 64: blocks per panel
   int swiglu_n;  // > 0: SwiGLU B with N output columns (rows interleave up and gate)
 };
 
@@ -67,42 +75,47 @@ struct F6PackArgs {
 hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s);
 
 // ---------------------------------------------------------------------------
-// GEMM engine.  Four waves in 2 x 2, each owning 128 x 128 of the 256-row
-// tile (SwiGLU: 128 rows x 64 output columns, up and gate).  Accumulator
-// [i][j] is the 16 x 16 block of A fragment i and B fragment j; the B
-// fragment is the MFMA's first operand, so lane l holds row l % 16 and the
-// four columns 4*(l/16) + [0, 4) of the block.
+// GEMM engine.  Four waves in 2 x 2, each owning 128 rows x 128 packed B
+// rows of the 256 x 256 tile: 4 x 4 accumulators of 32 x 32 (SwiGLU: the
+// packed B rows of a wave are 64 up columns then the same 64 gate columns,
+// so fragments j = 2, 3 are the gate of j = 0, 1).  The B fragment is the
+// MFMA's first operand, so lane l holds output row 32*i + l % 32 and, in
+// registers 4q .. 4q+3, the four consecutive columns 32*j + 8q + 4*(l/32).
 //
-// Schedule of stage k (one 128-K block, slot k % 3 of the ring):
+// Schedule of stage k (128 K = two 64-K steps, slot k % 3 of the ring):
 //  * top: wait for this wave's DMA of stage k+1 and its own LDS reads of
 //    stage k, then the barrier: stage k+1 is complete in LDS and no wave
 //    still reads slot k % 3;
-//  * 64 MFMAs on the fragments of stage k (register set k % 2); after each
-//    of the first 32 one LDS read of stage k+1 into the other set, after
-//    each odd one of the next 24 one DMA load of stage k+3 into slot k % 3.
+//  * 32 MFMAs (2 steps x 4 x 4) on the fragments of stage k (register set
+//    k % 2); after each, one LDS read of stage k+1 into the other set; the
+//    odd MFMAs 1 .. 23 each carry one DMA load of stage k+3 into slot k % 3.
 // The DMA of a stage is thus issued two stages before its data is read.
+// A stage in LDS holds, per operand, eight 32-row panels of two blocks.
 template <class C>
 struct F6Engine {
+  static constexpr bool SWIGLU = C::SWIGLU;
   static constexpr int P = 3;
   static constexpr int NW = 4;
-  static constexpr int OPB = 16 * F6_BLOCK;      // one operand's stage: 24 KiB
+  static constexpr int PANEL = 2 * F6_BLOCK;     // 32 rows x 128 K: 3 KiB
+  static constexpr int OPB = 8 * PANEL;          // one operand's stage: 24 KiB
   static constexpr int STAGE = 2 * OPB;          // 48 KiB
   static constexpr int LDS_BYTES = P * STAGE;    // 144 KiB
   static constexpr int DPW = STAGE / 1024 / NW;  // 12 DMA loads per wave per stage
-  static_assert(C::BM == 256 && C::WM == 2 && C::WN == 2 && C::FM == 8 && C::FN2 == 8, "256-row tiles, 2x2 waves");
-  static_assert(C::BROWS == 256, "256 packed B rows per tile");
+  static constexpr int TN = SWIGLU ? 64 : 128;   // output columns per wave
+  static constexpr int FN = SWIGLU ? 2 : 4;      // output column fragments per wave
+  static_assert(C::BM == 256 && C::WM == 2 && C::WN == 2 && C::BROWS == 256, "256-row tiles, 2x2 waves");
 
-  v4i acc[8][8];
-  v6i fa[2][8];
-  v6i fb[2][8];
+  v16f acc[4][4];
+  v6i fa[2][2][4];  // [set][step][i]
+  v6i fb[2][2][4];  // [set][step][j]
   uint32_t voff[DPW];
-  v4i rs;        // this wave's DMA operand (waves 0-1: A, 2-3: B)
-  uint32_t lds0; // LDS address of slot 0
+  v4i rs;         // this wave's DMA operand (waves 0-1: A, 2-3: B)
+  uint32_t lds0;  // LDS address of slot 0
   int lane, wave, wm, wn;
-  int one;       // E8M0 scale 2^0
 
   // LDS read addresses of this lane in one slot: 16- and 8-byte parts of
-  // the wave's A fragment 0 and B fragment 0 (fragment f adds 1536 * f).
+  // the wave's A panel 0 and B panel 0, step 0 (panel f adds PANEL * f,
+  // step 1 adds one block).
   struct Reads {
     uint32_t a16, a8, b16, b8;
     __device__ __forceinline__ void add(uint32_t d) {
@@ -113,204 +126,387 @@ struct F6Engine {
     }
   };
 
-  __device__ __forceinline__ int out_row(int i) const { return wm * C::TM + 16 * i + (lane & 15); }
-  __device__ __forceinline__ int out_col(int j) const {
-    return wn * C::TN + 16 * (j < C::FN ? j : j - C::FN) + 4 * (lane >> 4);
-  }
+  __device__ __forceinline__ int out_row(int i) const { return wm * 128 + 32 * i + (lane & 31); }
+  // first of the four columns of fragment j (< FN), register group q
+  __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
 
-  // a6 / b6: block-format operands; the tile's first panels are m0 / 16 and
-  // 16 * bt (bt: B tile index).
+  // a6 / b6: block-format operands; the tile's first panels are m0 / 32 and
+  // 8 * bt (bt: B tile index).
   __device__ __forceinline__ void setup(uint8_t* smem, const uint8_t* a6, const uint8_t* b6, int m0, int bt, int kb,
                                         unsigned long long a_bytes, unsigned long long b_bytes) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     wm = wave % 2;
     wn = wave / 2;
-    one = 127;
     lds0 = lds_address(smem);
     const unsigned long long panel_bytes = (unsigned long long)kb * F6_BLOCK;
     const bool is_a = wave < 2;
     const unsigned long long first =
-        (is_a ? (unsigned long long)(m0 / 16) : (unsigned long long)bt * 16) * panel_bytes;
+        (is_a ? (unsigned long long)(m0 / 32) : (unsigned long long)bt * 8) * panel_bytes;
     rs = buffer_words((is_a ? a6 : b6) + first, (is_a ? a_bytes : b_bytes) - first);
-    // DMA load c of this wave fills stage bytes [1024 * (DPW*wave + c), +1024)
+    // DMA load c of this wave fills stage bytes [1024 * (DPW*wave + c), +1024):
+    // panel o / PANEL of the operand, byte o % PANEL of its two blocks
 #pragma unroll
     for (int c = 0; c < DPW; ++c) {
       const uint32_t o = 1024u * (DPW * wave + c) + 16u * lane - (is_a ? 0u : (uint32_t)OPB);
-      const uint32_t blk = o / F6_BLOCK, r = o % F6_BLOCK;
-      voff[c] = blk * (uint32_t)panel_bytes + r;
+      voff[c] = (o / PANEL) * (uint32_t)panel_bytes + o % PANEL;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   }
 
   __device__ __forceinline__ Reads reads_of_slot(int slot) const {
     const uint32_t s = lds0 + (uint32_t)slot * STAGE;
-    return Reads{s + 8u * wm * F6_BLOCK + 16u * lane, s + 8u * wm * F6_BLOCK + 1024u + 8u * lane,
-                 s + OPB + 8u * wn * F6_BLOCK + 16u * lane, s + OPB + 8u * wn * F6_BLOCK + 1024u + 8u * lane};
+    const uint32_t a = s + 4u * wm * PANEL, b = s + OPB + 4u * wn * PANEL;
+    return Reads{a + 16u * lane, a + 1024u + 8u * lane, b + 16u * lane, b + 1024u + 8u * lane};
   }
 
-  __device__ __forceinline__ void dma(int st, int slot, int c) const {
-    lds_dma16(rs, voff[c], (uint32_t)st * F6_BLOCK, lds0 + (uint32_t)slot * STAGE + 1024u * (DPW * wave + c));
-  }
-
-  // LDS read Q (0..31) of a stage into set S: fragments in the order A0,
-  // B0..B7, A1..A7 (the order of their first use), each as its 16-byte then
+  // LDS read Q (0..31) of a stage into set S: per step, the fragments in the
+  // order of their first use (A0, B0..B3, A1..A3), each as its 16-byte then
   // its 8-byte part.
   template <int S, int Q>
   __device__ __forceinline__ void read(const Reads& r) {
-    constexpr int F = Q / 2;
-    constexpr bool IS_A = F == 0 || F >= 9;
-    constexpr int IDX = F == 0 ? 0 : (F >= 9 ? F - 8 : F - 1);
-    v6i& dst = IS_A ? fa[S][IDX] : fb[S][IDX];
+    constexpr int ST = Q / 16;
+    constexpr int F = (Q % 16) / 2;
+    constexpr bool IS_A = F == 0 || F >= 5;
+    constexpr int IDX = F == 0 ? 0 : (F >= 5 ? F - 4 : F - 1);
+    constexpr int OFF = IDX * PANEL + ST * F6_BLOCK;
+    v6i& dst = IS_A ? fa[S][ST][IDX] : fb[S][ST][IDX];
     if constexpr (Q % 2 == 0) {
       v4i x;
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(IS_A ? r.a16 : r.b16), "i"(IDX * F6_BLOCK));
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(IS_A ? r.a16 : r.b16), "i"(OFF));
       dst.s0 = x.x;
       dst.s1 = x.y;
       dst.s2 = x.z;
       dst.s3 = x.w;
     } else {
       v2i y;
-      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(y) : "v"(IS_A ? r.a8 : r.b8), "i"(IDX * F6_BLOCK));
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(y) : "v"(IS_A ? r.a8 : r.b8), "i"(OFF));
       dst.s4 = y.x;
       dst.s5 = y.y;
     }
   }
 
-  template <int S>
-  __device__ __forceinline__ void mfma(int i, int j) {
-    asm volatile("v_mfma_scale_f32_16x16x128_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:3 blgp:3"
-                 : "+a"(acc[i][j])
-                 : "v"(fb[S][j]), "v"(fa[S][i]), "v"(one));
-  }
-
-  // MFMA T (0..63) of a stage on set S, followed by LDS read T of the next
-  // stage (T < 32) or DMA load (T - 33) / 2 of the stage `dma_st` (odd T from
-  // 33 on).
+  // MFMA T (0..31) of a stage on set S (step T/16, A fragment (T%16)/4, B
+  // fragment T%4), fused with DMA load (T-1)/2 of the stage for odd T < 24,
+  // followed by LDS read T of the next stage.  Every stage runs the same
+  // sequence with no branch: a branch around an asm MFMA or LDS read would
+  // let the register allocator copy an accumulator or fragment between the
+  // asm statements, and the copy would read a value the hardware has not
+  // written yet (the compiler cannot see the MFMA or the load in the asm).
   template <int S, int T>
-  __device__ __forceinline__ void tick(bool rd, const Reads& r, int dma_st, int dma_slot) {
-    mfma<S>(T / 8, T % 8);
-    if constexpr (T < 32) {
-      if (rd) read<1 - S, T>(r);
-    } else if constexpr (T % 2 == 1 && (T - 33) / 2 < DPW) {
-      if (dma_st >= 0) dma(dma_st, dma_slot, (T - 33) / 2);
+  __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0) {
+    constexpr int ST = T / 16, I = (T % 16) / 4, J = T % 4;
+    if constexpr (T % 2 == 1 && T < 2 * DPW) {
+      constexpr int c = T / 2;
+      // the compiler writes M0 before the statement; the MFMA is the wait
+      // state the LDS-DMA load needs after that write
+      asm volatile(
+          "v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0 cbsz:2 blgp:2\n\t"
+          "buffer_load_dwordx4 %3, %4, %5 offen lds"
+          : "+a"(acc[I][J])
+          : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(voff[c]), "s"(rs_st), "s"(so), "{m0}"(m0 + 1024u * c)
+          : "memory");
+    } else {
+      asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0 cbsz:2 blgp:2"
+                   : "+a"(acc[I][J])
+                   : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]));
     }
+    read<1 - S, T>(r);
   }
   template <int S, int... T>
-  __device__ __forceinline__ void ticks(bool rd, const Reads& r, int dma_st, int dma_slot,
+  __device__ __forceinline__ void ticks(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0,
                                         std::integer_sequence<int, T...>) {
-    (tick<S, T>(rd, r, dma_st, dma_slot), ...);
+    (tick<S, T>(r, rs_st, so, m0), ...);
   }
   template <int S, int... Q>
   __device__ __forceinline__ void reads(const Reads& r, std::integer_sequence<int, Q...>) {
     (read<S, Q>(r), ...);
   }
 
-  // Top of a stage: this wave's DMA of the next stage has landed (the
-  // stage after it may stay outstanding), its LDS reads are done, then the
-  // barrier.
-  static __device__ __forceinline__ void open(bool one_pending) {
-    if (one_pending) wait_vmcnt<DPW>();
-    else wait_vmcnt<0>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // Wait states between accumulator writes and reads outside the asm
+  // MFMAs; every accumulator is an operand, so no access crosses it.
+  template <int N>
+  __device__ __forceinline__ void fence() {
+    static_assert(N == 4 || N == 7, "wait states");
+#define SHK_F6_ACC(i) "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3])
+    if constexpr (N == 4)
+      asm volatile("s_nop 4" : SHK_F6_ACC(0), SHK_F6_ACC(1), SHK_F6_ACC(2), SHK_F6_ACC(3));
+    else
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                   : SHK_F6_ACC(0), SHK_F6_ACC(1), SHK_F6_ACC(2), SHK_F6_ACC(3));
+#undef SHK_F6_ACC
   }
 
-  // Stage k on set S: reads stage k+1 through `r` if `rd`, loads stage
-  // `dma_st` (k + 3, or -1) into slot `dma_slot` (k's).
+  // Stage k on set S.  Top: this wave's DMA of stage k+1 has landed (that
+  // of k+2 may be outstanding), its LDS reads are done, then the barrier.
+  // Then the MFMAs of stage k, the reads of stage k+1 (slot `r`) and the DMA
+  // of stage k+3 into slot `slot` (k's).  Past the last stage, the reads
+  // fetch a stale slot into the unused set and the DMA loads go through
+  // `rs_end`, a resource of zero records: they return zeros without touching
+  // memory, into a slot that holds no live data.
   template <int S>
-  __device__ __forceinline__ void stage(bool one_pending, bool rd, const Reads& r, int dma_st, int dma_slot) {
-    open(one_pending);
-    ticks<S>(rd, r, dma_st, dma_slot, std::make_integer_sequence<int, 64>{});
+  __device__ __forceinline__ void stage(const Reads& r, int k, int nst, int slot, const v4i& rs_end) {
+    wait_vmcnt<DPW>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const bool live = k + 3 < nst;
+    const v4i rs_st = live ? rs : rs_end;
+    const uint32_t so = live ? (uint32_t)(k + 3) * PANEL : 0u;
+    ticks<S>(r, rs_st, so, lds0 + (uint32_t)slot * STAGE + 1024u * DPW * wave,
+             std::make_integer_sequence<int, 32>{});
+  }
+  // Moves the read slot one ahead (wrapping after slot 2) and the stage slot.
+  static __device__ __forceinline__ void advance(Reads& r, int& slot) {
+    r.add(slot == 1 ? (uint32_t)(-2 * STAGE) : (uint32_t)STAGE);
+    slot = slot == 2 ? 0 : slot + 1;
   }
 
+  // nst: 128-K stages.
   __device__ __forceinline__ void run(int nst) {
-    for (int s = 0; s < 3 && s < nst; ++s)
+    const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
+    // stages 0..2 (zeros past the last stage), then stage 0 into set 0
 #pragma unroll
-      for (int c = 0; c < DPW; ++c) dma(s, s, c);
-    if (nst >= 3) wait_vmcnt<2 * DPW>();
-    else if (nst == 2) wait_vmcnt<DPW>();
-    else wait_vmcnt<0>();
+    for (int st = 0; st < 3; ++st)
+#pragma unroll
+      for (int c = 0; c < DPW; ++c)
+        lds_dma16(st < nst ? rs : rs_end, voff[c], st < nst ? (uint32_t)st * PANEL : 0u,
+                  lds0 + (uint32_t)st * STAGE + 1024u * (DPW * wave + c));
+    wait_vmcnt<2 * DPW>();
     asm volatile("s_barrier" ::: "memory");
     reads<0>(reads_of_slot(0), std::make_integer_sequence<int, 32>{});
-    acc_fence<4>(acc);
+    fence<4>();
     // r: read slot of stage k+1; slot: slot of stage k
     Reads r = reads_of_slot(1);
     int slot = 0;
-    const uint32_t step = (uint32_t)STAGE;
-    auto advance = [&]() {
-      r.add(slot == 1 ? (uint32_t)(-2 * (int)step) : step);
-      slot = slot == 2 ? 0 : slot + 1;
-    };
     int k = 0;
-    for (; k + 4 < nst; k += 2) {
-      stage<0>(true, true, r, k + 3, slot);
-      advance();
-      stage<1>(true, true, r, k + 4, slot);
-      advance();
+    for (; k + 2 <= nst; k += 2) {
+      stage<0>(r, k, nst, slot, rs_end);
+      advance(r, slot);
+      stage<1>(r, k + 1, nst, slot, rs_end);
+      advance(r, slot);
     }
-    // at most four stages remain; stage k uses set 0
-    while (k < nst) {
-      stage<0>(k + 2 < nst, k + 1 < nst, r, k + 3 < nst ? k + 3 : -1, slot);
-      advance();
-      if (++k >= nst) break;
-      stage<1>(k + 2 < nst, k + 1 < nst, r, k + 3 < nst ? k + 3 : -1, slot);
-      advance();
-      ++k;
+    // Wait states after the last MFMA wherever paths merge, so that a copy
+    // the register allocator places on a merge reads finished accumulators.
+    fence<7>();
+    if (k < nst) {
+      stage<0>(r, k, nst, slot, rs_end);
+      fence<7>();
     }
-    // wait states between the last MFMA and the first accumulator read
-    acc_fence<7>(acc);
-    acc_fence<7>(acc);
+    fence<7>();
+    // the loads past the last stage land before the workgroup's LDS is freed
+    wait_vmcnt<0>();
   }
 };
 
-template <class C>
+// bf16 pair halves as fp32
+__device__ __forceinline__ float f6_bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float f6_bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ float f6_bf16_at(const uint2& w, int t) {
+  return t == 0 ? f6_bf16_lo(w.x) : t == 1 ? f6_bf16_hi(w.x) : t == 2 ? f6_bf16_lo(w.y) : f6_bf16_hi(w.y);
+}
+
+// Writes a wave's results: lane l writes output row out_row(i) and, per
+// register group q, the four columns out_col(j, q) + [0, 4) (for SwiGLU from
+// accumulator j and its gate partner j + 2).
+//  * OUT_I32: the exact integers ([M, 2N] for SwiGLU: up, then gate at +N);
+//  * otherwise (float(acc) * a_scale) * b_scale, then ReLU^2 or SwiGLU, as
+//    fp32 or bf16 (NO_NAN: no value is NaN, so the hardware conversion,
+//    which does not canonicalize NaN, may be used).
+// sb[j][q]: the four bf16 B scales of those columns (j >= FN: the gate's).
+template <class C, int MODE, int EPI, bool NO_NAN, class E>
+__device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int m0, int n0, const float (&sa)[4],
+                                            const uint2 (&sb)[4][4]) {
+  constexpr uint32_t ESZ = MODE == OUT_BF16 ? 2 : 4;
+  const uint32_t ldo = (MODE == OUT_I32 && C::SWIGLU) ? 2u * (uint32_t)p.N : (uint32_t)p.N;
+  const unsigned long long first = (unsigned long long)m0 * ldo + n0;
+  const rsrc_t r = make_rsrc(static_cast<uint8_t*>(p.out) + first * ESZ,
+                             ((unsigned long long)p.M * ldo - first) * ESZ);
+  const uint32_t voff = ((uint32_t)e.out_row(0) * ldo + (uint32_t)e.out_col(0, 0)) * ESZ;
+  // column group (j, q) outer, rows i inner: each group's four B scales are
+  // unpacked once and die after the group
+#pragma unroll
+  for (int j = 0; j < E::FN; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t off = voff + (uint32_t)(32 * j + 8 * q) * ESZ;
+      float su[4], sg[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        su[t] = f6_bf16_at(sb[j][q], t);
+        sg[t] = C::SWIGLU ? f6_bf16_at(sb[j + 2 < 4 ? j + 2 : j][q], t) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t soff = (uint32_t)(32 * i) * ldo * ESZ;
+        if constexpr (MODE == OUT_I32) {
+          const v16f& u = e.acc[i][j];
+          __builtin_amdgcn_raw_buffer_store_b128(
+              v4i{(int)(u[4 * q] * F6_UNSCALE), (int)(u[4 * q + 1] * F6_UNSCALE), (int)(u[4 * q + 2] * F6_UNSCALE),
+                  (int)(u[4 * q + 3] * F6_UNSCALE)},
+              r, off, soff, 0);
+          if constexpr (C::SWIGLU) {
+            const v16f& g = e.acc[i][j + 2];
+            __builtin_amdgcn_raw_buffer_store_b128(
+                v4i{(int)(g[4 * q] * F6_UNSCALE), (int)(g[4 * q + 1] * F6_UNSCALE),
+                    (int)(g[4 * q + 2] * F6_UNSCALE), (int)(g[4 * q + 3] * F6_UNSCALE)},
+                r, off + (uint32_t)p.N * ESZ, soff, 0);
+          }
+        } else {
+          float v[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float x = (e.acc[i][j][4 * q + t] * F6_UNSCALE) * sa[i];
+            x = x * su[t];
+            if constexpr (C::SWIGLU) {
+              float g = (e.acc[i][j + 2][4 * q + t] * F6_UNSCALE) * sa[i];
+              g = g * sg[t];
+              x = swiglu(x, g);
+            } else if constexpr (EPI == EPI_RELU2) {
+              x = apply_epi(x, EPI_RELU2);
+            }
+            v[t] = x;
+          }
+          if constexpr (MODE == OUT_BF16) {
+            uint32_t lo, hi;
+            if constexpr (NO_NAN) {
+              lo = pack_bf16x2_nonan(v[0], v[1]);
+              hi = pack_bf16x2_nonan(v[2], v[3]);
+            } else {
+              lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+              hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+            }
+            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)lo, (int)hi}, r, off, soff, 0);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                v4i{__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]), __float_as_int(v[3])}, r,
+                off, soff, 0);
+          }
+        }
+      }
+      // one column group at a time: keeps accumulator reads and scale
+      // unpacking from being hoisted ahead of their use
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// bf16 epilogue through LDS (plain tiles).  Each wave writes its 128 x 128
+// bf16 results into its own 32 KiB region of the (now idle) ring, row r at
+// r * 256 with 16-byte unit u (columns 8u .. 8u+7) at 16 * (u ^ (r % 16)),
+// then reads the region back four rows per instruction (16 lanes per row)
+// and writes them with 16-byte stores: each store instruction covers four
+// whole 256-byte row segments instead of 32 rows x 16 bytes.  The swizzle
+// makes both directions free of bank conflicts: a write puts lanes 0-15
+// (rows r .. r+15) in 16 distinct units; a read puts the 16 lanes of a row in
+// 16 distinct units.
+template <class C, int EPI, bool NO_NAN, class E>
+__device__ __forceinline__ void f6_epilogue_lds(const E& e, const DenseArgs& p, uint8_t* smem, int m0, int n0,
+                                                const float (&sa)[4], const uint2 (&sb)[4][4]) {
+  static_assert(!C::SWIGLU, "plain tiles");
+  // every wave has finished reading the ring
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  uint8_t* region = smem + (size_t)e.wave * 32768;
+  const int lane = e.lane;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float su[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) su[t] = f6_bf16_at(sb[j][q], t);
+      const int u = 4 * j + q;          // 16-byte unit: columns 32j + 8q .. +7
+      const int half = 8 * (lane >> 5);  // columns +4 .. +7 of the unit
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float x = (e.acc[i][j][4 * q + t] * F6_UNSCALE) * sa[i];
+          x = x * su[t];
+          if constexpr (EPI == EPI_RELU2) x = apply_epi(x, EPI_RELU2);
+          v[t] = x;
+        }
+        uint32_t lo, hi;
+        if constexpr (NO_NAN) {
+          lo = pack_bf16x2_nonan(v[0], v[1]);
+          hi = pack_bf16x2_nonan(v[2], v[3]);
+        } else {
+          lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+          hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+        }
+        const int r = 32 * i + (lane & 31);
+        *reinterpret_cast<uint2*>(region + r * 256 + 16 * (u ^ (r & 15)) + half) = make_uint2(lo, hi);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // read back four rows per instruction and store whole row segments
+  const unsigned long long first = (unsigned long long)m0 * p.N + n0;
+  const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(p.out) + first * 2, ((unsigned long long)p.M * p.N - first) * 2);
+  const int rr = lane >> 4, u = lane & 15;
+  const uint32_t voff = ((uint32_t)(e.wm * 128 + rr) * (uint32_t)p.N + (uint32_t)(e.wn * 128 + 8 * u)) * 2u;
+#pragma unroll
+  for (int t = 0; t < 32; ++t) {
+    const int r = 4 * t + rr;
+    const uint4 x = *reinterpret_cast<const uint4*>(region + r * 256 + 16 * (u ^ (r & 15)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(4 * t) * (uint32_t)p.N * 2u,
+                                           0);
+  }
+}
+
+// One kernel per output mode and epilogue (chosen by the host), so that
+// each holds a single straight-line epilogue.
+template <class C, int MODE, int EPI>
 __global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[F6Engine<C>::LDS_BYTES];
+  using E = F6Engine<C>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
   dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
-  const int kb = p.K / 128;
-  F6Engine<C> e;
-  e.setup(smem, p.a, p.b, m0, tn, kb, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.b_cols, p.K));
-  float sa[C::FM];
+  E e;
+  e.setup(smem, p.a, p.b, m0, tn, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.b_cols, p.K));
+  float sa[4];
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i) sa[i] = load_bf16(p.a_scale + m0 + e.out_row(i));
-  float sb[C::FN2][4];
+  for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
+  e.run(p.K / 128);
+  // B scales (bf16, four per load), loaded once the loop has freed the
+  // fragment registers; fragments j >= FN read the gate's scales
   const int gate = C::SWIGLU ? p.N : 0;
+  uint2 sb[4][4];
 #pragma unroll
-  for (int j = 0; j < C::FN2; ++j) {
-    if (!C::SWIGLU && j >= C::FN) continue;
-    load_bf16x4(p.b_scale + (j < C::FN ? 0 : gate) + n0 + e.out_col(j), 4, true, sb[j]);
-  }
-  e.run(kb);
-  // The accumulator is the exact integer sum as an fp32 value.
-  auto scaled = [&](int i, int j, int r) {
-    float x = __int_as_float(e.acc[i][j][r]) * sa[i];
-    return x * sb[j][r];
-  };
-  bool finite = true;
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i) finite = finite && (__float_as_uint(sa[i]) & 0x7F800000u) != 0x7F800000u;
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) finite = finite && (__float_as_uint(sb[j][r]) & 0x7F800000u) != 0x7F800000u;
-  const bool no_nan = __all(finite);
-  auto raw_of = [&](int i, int j, int r) { return (int)__int_as_float(e.acc[i][j][r]); };
-  if (C::SWIGLU) {
-    dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) { return swiglu(scaled(i, j, r), scaled(i, j + C::FN, r)); },
-                   raw_of);
-  } else if (p.epilogue == EPI_RELU2) {
-    dense_store<C>(e, p, m0, n0, [&](int i, int j, int r) { return apply_epi(scaled(i, j, r), EPI_RELU2); }, raw_of,
-                   no_nan);
+    for (int q = 0; q < 4; ++q) {
+      const int jj = j < E::FN ? j : j - E::FN;
+      sb[j][q] = MODE == OUT_I32 ? uint2{0, 0}
+                                 : *reinterpret_cast<const uint2*>(p.b_scale + (j < E::FN ? 0 : gate) + n0 +
+                                                                   e.out_col(jj, q));
+    }
+  if constexpr (MODE != OUT_BF16 || C::SWIGLU) {
+    f6_epilogue<C, MODE, EPI, false>(e, p, m0, n0, sa, sb);
   } else {
-    dense_store<C>(e, p, m0, n0, scaled, raw_of, no_nan);
+    // Finite scales times a finite integer give no NaN (at most +-inf), and
+    // neither does ReLU^2 of such a value.
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) finite = finite && (__float_as_uint(sa[i]) & 0x7F800000u) != 0x7F800000u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint2 w = sb[j][q];
+        finite = finite && (w.x & 0x7F80u) != 0x7F80u && (w.x & 0x7F800000u) != 0x7F800000u &&
+                 (w.y & 0x7F80u) != 0x7F80u && (w.y & 0x7F800000u) != 0x7F800000u;
+      }
+    if (__all(finite)) f6_epilogue_lds<C, EPI, true>(e, p, smem, m0, n0, sa, sb);
+    else f6_epilogue_lds<C, EPI, false>(e, p, smem, m0, n0, sa, sb);
   }
 }
 

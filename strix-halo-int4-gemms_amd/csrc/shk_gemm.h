@@ -353,8 +353,8 @@ struct DenseArgs {
   int a_aligned;     // operand base/stride alignment allows vector loads
   int b_aligned;
   int group_m;       // tile-row swizzle width
-  int layout;        // SHK_LAYOUT_* (read by the bf6 path's operand conversion)
-  uint8_t* work;     // bf6 path: caller workspace for the converted operands
+  int layout;        // SHK_LAYOUT_* (read by the fp6 path's operand conversion)
+  uint8_t* work;     // fp6 path: caller workspace for the converted operands
 };
 
 // Tile order: workgroups are dispatched round-robin over the 8 XCDs, so the

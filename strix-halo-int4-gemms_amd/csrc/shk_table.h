@@ -20,7 +20,7 @@ struct Entry {
   DenseLaunchFn dense;
   RaggedFwdLaunchFn fwd;
   RaggedBwdLaunchFn bwd;
-  DenseLaunchFn converted;  // bf6 entries: the GEMM alone, on converted operands
+  DenseLaunchFn converted;  // fp6 entries: the GEMM alone, on converted operands
 };
 
 template <class C>
@@ -28,11 +28,11 @@ hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   hipLaunchKernelGGL(dense_gemm_kernel<C>, grid, dim3(C::NT), 0, s, a);
   return hipGetLastError();
 }
-// bf6 path.  f6_convert_operand converts A (operand 0) or B (operand 1) of
+// fp6 path.  f6_convert_operand converts A (operand 0) or B (operand 1) of
 // a dense call into its part of the workspace (A first, then B); the GEMM
 // then reads both parts.
 inline hipError_t f6_convert_operand(const DenseArgs& a, int operand, bool swiglu, hipStream_t s) {
-  const int kb = a.K / 128;
+  const int kb = a.K / 64;
   if (operand == 0)
     return launch_f6_pack(F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0}, a.layout == SHK_LAYOUT_TN, s);
   return launch_f6_pack(F6PackArgs{a.b, a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0},
@@ -43,7 +43,18 @@ hipError_t launch_f6_gemm_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   DenseArgs g = a;
   g.a = a.work;
   g.b = a.work + f6_operand_bytes(a.M, a.K);
-  hipLaunchKernelGGL(f6_gemm_kernel<C>, grid, dim3(256), 0, s, g);
+  if (a.out_mode == OUT_I32) {
+    hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_I32, EPI_NONE>), grid, dim3(256), 0, s, g);
+  } else if (a.out_mode == OUT_F32) {
+    if (!C::SWIGLU && a.epilogue == EPI_RELU2)
+      hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_F32, EPI_RELU2>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_F32, EPI_NONE>), grid, dim3(256), 0, s, g);
+  } else if (!C::SWIGLU && a.epilogue == EPI_RELU2) {
+    hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_BF16, EPI_RELU2>), grid, dim3(256), 0, s, g);
+  } else {
+    hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_BF16, EPI_NONE>), grid, dim3(256), 0, s, g);
+  }
   return hipGetLastError();
 }
 template <class C>
@@ -95,7 +106,7 @@ Entry f6_entry(int layout) {
   shk_kernel_desc d = desc_of<C>(SHK_FAMILY_DENSE, layout, 8);
   d.num_stages = F6Engine<C>::P;
   d.lds_bytes = F6Engine<C>::LDS_BYTES;
-  d.operand_format = SHK_OPERANDS_BF6;
+  d.operand_format = SHK_OPERANDS_FP6;
   return Entry{d, &launch_f6_t<C>, nullptr, nullptr, &launch_f6_gemm_t<C>};
 }
 template <class C>

@@ -178,12 +178,12 @@ def _gemm_ws(lib, index, m, n, k, *, work, work_bytes, epi=0, mode=0):
                                                      mode, work, work_bytes)
 
 
-def test_bf6_entries_report_their_workspace(lib):
-    bf6 = [d for d in kt.entries(kt.FAMILY_DENSE) if d.operand_format == kt.OPERANDS_BF6]
-    assert {(d.layout, d.epilogue_kind) for d in bf6} == {
+def test_fp6_entries_report_their_workspace(lib):
+    fp6 = [d for d in kt.entries(kt.FAMILY_DENSE) if d.operand_format == kt.OPERANDS_FP6]
+    assert {(d.layout, d.epilogue_kind) for d in fp6} == {
         (layout, epi) for layout in (kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN)
         for epi in (kt.EPI_KIND_PLAIN, kt.EPI_KIND_SWIGLU)}
-    for d in bf6:
+    for d in fp6:
         assert d.dtype_bits == 4 and d.block_m == 256 and d.num_stages == 3 and d.lds_bytes == 147456
         for m, n, k in ((256, 256, 128), (512, 1024, 4096), (8192, 8192, 8192)):
             rc, got = _ws(lib, d.index, m, n, k)
@@ -196,8 +196,8 @@ def test_bf6_entries_report_their_workspace(lib):
     assert "non-null" in _err(lib)
 
 
-def test_bf6_launch_needs_a_workspace(lib):
-    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_BF6)
+def test_fp6_launch_needs_a_workspace(lib):
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_FP6)
     assert _gemm(lib, idx, 256, 256, 128) == 1
     assert "workspace of 49152 bytes" in _err(lib)
     assert _gemm_ws(lib, idx, 256, 256, 128, work=FAKE, work_bytes=49151) == 1
@@ -206,32 +206,32 @@ def test_bf6_launch_needs_a_workspace(lib):
     assert "16-byte aligned" in _err(lib)
 
 
-def test_bf6_k_limit_keeps_fp32_sums_exact(lib):
+def test_fp6_k_limit_keeps_fp32_sums_exact(lib):
     # |sum| <= 64 * K must stay <= 2^24 for the fp32 accumulation to be exact
-    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_BF6)
-    assert kt.BF6_MAX_K * 64 == 1 << 24
-    assert _gemm_ws(lib, idx, 256, 256, kt.BF6_MAX_K + 128, work=FAKE, work_bytes=1 << 40) == 1
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_FP6)
+    assert kt.FP6_MAX_K * 64 == 1 << 24
+    assert _gemm_ws(lib, idx, 256, 256, kt.FP6_MAX_K + 128, work=FAKE, work_bytes=1 << 40) == 1
     assert "K <= 262144" in _err(lib)
 
 
-def test_split_bf6_phases_validate_their_arguments(lib):
-    bf6 = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_BF6)
+def test_split_fp6_phases_validate_their_arguments(lib):
+    fp6 = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_FP6)
     packed = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
     conv = lib.amd_strix_halo_kernels_gemm_convert
     gemm = lib.amd_strix_halo_kernels_launch_gemm_converted
     assert conv(packed, 0, 0, 0, FAKE, 256, 256, 128, FAKE, 1 << 20) == 1
-    assert "only bf6 entries" in _err(lib)
-    assert conv(bf6, 0, 0, 2, FAKE, 256, 256, 128, FAKE, 1 << 20) == 1
+    assert "only fp6 entries" in _err(lib)
+    assert conv(fp6, 0, 0, 2, FAKE, 256, 256, 128, FAKE, 1 << 20) == 1
     assert "operand must be 0 (A) or 1 (B)" in _err(lib)
-    assert conv(bf6, 0, 0, 1, None, 256, 256, 128, FAKE, 1 << 20) == 1
+    assert conv(fp6, 0, 0, 1, None, 256, 256, 128, FAKE, 1 << 20) == 1
     assert "non-null" in _err(lib)
-    assert conv(bf6, 0, 0, 0, FAKE, 256, 256, 128, FAKE, 100) == 1
+    assert conv(fp6, 0, 0, 0, FAKE, 256, 256, 128, FAKE, 100) == 1
     assert "workspace of 49152 bytes" in _err(lib)
-    assert conv(bf6, 0, 0, 0, FAKE, 250, 256, 128, FAKE, 1 << 20) == 1
+    assert conv(fp6, 0, 0, 0, FAKE, 250, 256, 128, FAKE, 1 << 20) == 1
     assert "M=250 is not divisible by BLOCK_M=256" in _err(lib)
     assert gemm(packed, 0, 0, FAKE, FAKE, FAKE, 64, 64, 64, 0, 0, FAKE, 1 << 20) == 1
-    assert "only bf6 entries" in _err(lib)
-    assert gemm(bf6, 0, 0, FAKE, FAKE, FAKE, 256, 256, 128, kt.EPILOGUE_SWIGLU, 0, FAKE, 1 << 20) == 1
+    assert "only fp6 entries" in _err(lib)
+    assert gemm(fp6, 0, 0, FAKE, FAKE, FAKE, 256, 256, 128, kt.EPILOGUE_SWIGLU, 0, FAKE, 1 << 20) == 1
     assert "does not match the kernel's epilogue kind" in _err(lib)
-    assert gemm(bf6, 0, 0, FAKE, FAKE, None, 256, 256, 128, 0, 0, FAKE, 1 << 20) == 1
+    assert gemm(fp6, 0, 0, FAKE, FAKE, None, 256, 256, 128, 0, 0, FAKE, 1 << 20) == 1
     assert "a_scale, b_scale, and out pointers must be non-null" in _err(lib)

@@ -226,13 +226,13 @@ def test_special_scale_values_store_like_torch(kernel, device):
         assert np.array_equal(got, want)
 
 
-_BF6 = [k for k in shk.default_registry.all()
-        if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_BF6 and k.epilogue is not shk.Epilogue.RELU2]
+_FP6 = [k for k in shk.default_registry.all()
+        if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.epilogue is not shk.Epilogue.RELU2]
 
 
-@pytest.mark.parametrize("kernel", _BF6, ids=lambda k: k.kernel_id)
+@pytest.mark.parametrize("kernel", _FP6, ids=lambda k: k.kernel_id)
 @pytest.mark.parametrize("k", [128, 256, 384, 640])
-def test_bf6_kernels_every_stage_count(kernel, k, device):
+def test_fp6_kernels_every_stage_count(kernel, k, device):
     """One to five K blocks: the ring prologue, the tail and the main loop."""
     _, layout, _, epi = _kernel_params(kernel)
     m, n = 512, 512 if epi != "swiglu" else 256
@@ -250,12 +250,12 @@ def test_bf6_kernels_every_stage_count(kernel, k, device):
 
 
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
-def test_bf6_exact_at_the_k_bound(layout, device):
+def test_fp6_exact_at_the_k_bound(layout, device):
     """K = 262144 with rows of A and columns of B constant: every output is
     K * c_i * d_j, up to 64 * K = 2^24 for c = d = -8, the largest integer
     magnitude the fp32 accumulation must still hold exactly."""
     m = n = 256
-    k = kt.BF6_MAX_K
+    k = kt.FP6_MAX_K
     c = np.resize(np.arange(-8, 8, dtype=np.int8), m)
     d = np.resize(np.arange(7, -9, -1, dtype=np.int8), n)
     c[:8] = -8
@@ -266,10 +266,10 @@ def test_bf6_exact_at_the_k_bound(layout, device):
     del a_q, b_q
     kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL),
                                          epilogue=shk.Epilogue.NONE, m=m, n=n, k=k, layout=shk.GemmLayout(layout))
-    assert kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_BF6
+    assert kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_FP6
     sa = ref.bf16_from_f32(np.ones(m))
     sb = ref.bf16_from_f32(np.ones(n))
-    print(f"case bf6 k-bound {layout}", flush=True)
+    print(f"case fp6 k-bound {layout}", flush=True)
     got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
     want = k * c[:, None].astype(np.int64) * d[None, :].astype(np.int64)
     assert raw[0, 0] == 1 << 24
@@ -279,7 +279,7 @@ def test_bf6_exact_at_the_k_bound(layout, device):
 
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
 @pytest.mark.parametrize("epilogue", ["none", "swiglu"])
-def test_bf6_converted_operands_are_reusable(layout, epilogue, device):
+def test_fp6_converted_operands_are_reusable(layout, epilogue, device):
     """convert(B) once, then convert(A) + GEMM for two different A: each
     result equals the one-call launch bit for bit."""
     m, n, k = 512, 256, 384
@@ -287,12 +287,12 @@ def test_bf6_converted_operands_are_reusable(layout, epilogue, device):
     spec = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL)
     kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=spec, epilogue=shk.Epilogue(epilogue),
                                          m=m, n=n, k=k, layout=shk.GemmLayout(layout))
-    assert kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_BF6
+    assert kt.TABLE[kernel.table_index].operand_format == kt.OPERANDS_FP6
     _, _, _, b_arg, _, sb = dense_case(11, bits=4, layout=layout, m=m, n=n, k=k, subchannel=None, swiglu=swiglu)
     b = to_dev(torch, b_arg, device)
     tb = to_dev(torch, sb, device)
     work = native.gemm_workspace(kernel, m, n, k, device=device)
-    print(f"case bf6 reuse {layout} {epilogue}", flush=True)
+    print(f"case fp6 reuse {layout} {epilogue}", flush=True)
     native.convert_operand(kernel, 1, b, m=m, n=n, k=k, workspace=work)
     for seed in (12, 13):
         _, _, a_arg, _, sa, _ = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=None, swiglu=swiglu)
