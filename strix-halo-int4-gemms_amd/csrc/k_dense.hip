@@ -46,9 +46,16 @@ using C = Cfg<kBits, kAKmajor, kBKmajor, BM, BN, BK, WM, WN, SWIGLU, SUBCH, MK, 
 constexpr int kBigBK = kBits == 4 ? 128 : 64;
 
 #if SHK_DENSE_DMA
+// int8 large tiles run on the 32x32 int8 engine (shk_i8.h), int4 ones on the
+// direct-to-LDS engine with widening (the fp6 entries precede them).
 void append_all(std::vector<Entry>& t) {
-  t.push_back(dense_entry<C<256, 256, kBigBK, 2, 2, false, false, 64, 4>>(kLayout, 8));
-  t.push_back(dense_entry<C<256, 128, kBigBK, 2, 2, true, false, 64, 4>>(kLayout, 8));
+  if constexpr (kBits == 8) {
+    t.push_back(i8_entry<C<256, 256, kBigBK, 2, 2, false, false, 64, 4>>(kLayout, 8));
+    t.push_back(i8_entry<C<256, 128, kBigBK, 2, 2, true, false, 64, 4>>(kLayout, 8));
+  } else {
+    t.push_back(dense_entry<C<256, 256, kBigBK, 2, 2, false, false, 64, 4>>(kLayout, 8));
+    t.push_back(dense_entry<C<256, 128, kBigBK, 2, 2, true, false, 64, 4>>(kLayout, 8));
+  }
 }
 #else
 void append_all(std::vector<Entry>& t) {

@@ -45,9 +45,9 @@ __device__ __forceinline__ int f6_src_row(int r, int swiglu_n) {
 
 // K-major source (row r holds its K values contiguously, two per byte): one
 // wave converts one block; a lane loads its 16 source bytes directly.
-__global__ __launch_bounds__(256) void f6_pack_kmajor(const F6PackArgs p) {
+__device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
   const int lane = threadIdx.x & 63;
-  const long blk = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long blk = (long)wg * 4 + (threadIdx.x >> 6);
   const int panel = (int)(blk / p.kb);
   const int kb = (int)(blk - (long)panel * p.kb);
   const int row = f6_src_row(32 * panel + (lane & 31), p.swiglu_n);
@@ -62,10 +62,9 @@ __global__ __launch_bounds__(256) void f6_pack_kmajor(const F6PackArgs p) {
 // lane its row's bytes in K order: within a 16-lane group, lane i addresses
 // source row kp + i/2 at byte 8*(i%2) of a 16-row unit and receives the 8
 // bytes of those 8 rows in column i.
-__global__ __launch_bounds__(256) void f6_pack_mnmajor(const F6PackArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * 256];
-  const int t = blockIdx.x / p.kb;
-  const int kb = blockIdx.x - t * p.kb;
+__device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_t* tile) {
+  const int t = wg / p.kb;
+  const int kb = wg - t * p.kb;
   const int tid = threadIdx.x;
   const int u = tid & 15;  // 16-row unit of the tile
   const long col = f6_src_row(F6_TILE * t + 16 * u, p.swiglu_n);
@@ -96,14 +95,43 @@ __global__ __launch_bounds__(256) void f6_pack_mnmajor(const F6PackArgs p) {
   }
 }
 
+// Workgroups of one operand: one per 8 blocks (MN-major: a 256-row tile
+// and a 64-K block) or per 4 blocks (K-major: one per wave).
+int pack_groups(const F6PackArgs& a, bool mn_major) {
+  return mn_major ? (a.rows / F6_TILE) * a.kb : (a.rows / 32) * a.kb / 4;
+}
+
+__global__ __launch_bounds__(256) void f6_pack_one(const F6PackArgs p, int mn_major) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * 256];
+  if (mn_major) pack_mnmajor(p, blockIdx.x, tile);
+  else pack_kmajor(p, blockIdx.x);
+}
+
+// Both operands of a call in one launch: workgroups [0, a_groups) convert
+// A, the rest B.
+__global__ __launch_bounds__(256) void f6_pack_two(const F6PackArgs a, const F6PackArgs b, int a_mn, int b_mn,
+                                                   int a_groups) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * 256];
+  const int wg = blockIdx.x;
+  if (wg < a_groups) {
+    if (a_mn) pack_mnmajor(a, wg, tile);
+    else pack_kmajor(a, wg);
+  } else {
+    if (b_mn) pack_mnmajor(b, wg - a_groups, tile);
+    else pack_kmajor(b, wg - a_groups);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s) {
-  if (mn_major) {
-    hipLaunchKernelGGL(f6_pack_mnmajor, dim3((a.rows / F6_TILE) * a.kb), dim3(256), 0, s, a);
-  } else {
-    hipLaunchKernelGGL(f6_pack_kmajor, dim3((a.rows / 32) * a.kb / 4), dim3(256), 0, s, a);
-  }
+  hipLaunchKernelGGL(f6_pack_one, dim3(pack_groups(a, mn_major)), dim3(256), 0, s, a, (int)mn_major);
+  return hipGetLastError();
+}
+
+hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s) {
+  const int ga = pack_groups(a, a_mn), gb = pack_groups(b, b_mn);
+  hipLaunchKernelGGL(f6_pack_two, dim3(ga + gb), dim3(256), 0, s, a, b, (int)a_mn, (int)b_mn, ga);
   return hipGetLastError();
 }
 

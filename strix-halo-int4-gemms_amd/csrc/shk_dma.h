@@ -745,11 +745,18 @@ struct DmaEngine {
       for (int j = 0; j < C::FN2; ++j) wb[0][j] = read_b<0>(smem, j);
 #pragma unroll
       for (int i = 0; i < C::FM; ++i) wa[0][i] = read_a<0>(smem, i);
-      for (int k = 0; k < nst; k += 2) {
+      // stage pairs alternate the operand sets; an odd count ends with one
+      // more stage on set 0
+      int k = 0;
+      for (; k + 2 <= nst; k += 2) {
         open_stage(smem, k, nst);
         step<0, 0>(smem, k, on_step);
         open_stage(smem, k + 1, nst);
         step<1, 0>(smem, k + 1, on_step);
+      }
+      if (k < nst) {
+        open_stage(smem, k, nst);
+        step<0, 0>(smem, k, on_step);
       }
     }
     wait_vmcnt<0>();

@@ -73,6 +73,8 @@ struct F6PackArgs {
 // Converts one operand into block format (k_f6pack.hip).  mn_major: the
 // source is stored K-row by K-row (two K values per byte of every row).
 hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s);
+// Both operands in one launch.
+hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // GEMM engine.  Four waves in 2 x 2, each owning 128 rows x 128 packed B
@@ -129,6 +131,9 @@ struct F6Engine {
   __device__ __forceinline__ int out_row(int i) const { return wm * 128 + 32 * i + (lane & 31); }
   // first of the four columns of fragment j (< FN), register group q
   __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
+  // the exact integer sum of accumulator register x of [i][j], as fp32 / int32
+  __device__ __forceinline__ float acc_value(int i, int j, int x) const { return acc[i][j][x] * F6_UNSCALE; }
+  __device__ __forceinline__ int acc_int(int i, int j, int x) const { return (int)(acc[i][j][x] * F6_UNSCALE); }
 
   // a6 / b6: block-format operands; the tile's first panels are m0 / 32 and
   // 8 * bt (bt: B tile index).
@@ -343,26 +348,24 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int 
       for (int i = 0; i < 4; ++i) {
         const uint32_t soff = (uint32_t)(32 * i) * ldo * ESZ;
         if constexpr (MODE == OUT_I32) {
-          const v16f& u = e.acc[i][j];
           __builtin_amdgcn_raw_buffer_store_b128(
-              v4i{(int)(u[4 * q] * F6_UNSCALE), (int)(u[4 * q + 1] * F6_UNSCALE), (int)(u[4 * q + 2] * F6_UNSCALE),
-                  (int)(u[4 * q + 3] * F6_UNSCALE)},
+              v4i{e.acc_int(i, j, 4 * q), e.acc_int(i, j, 4 * q + 1), e.acc_int(i, j, 4 * q + 2),
+                  e.acc_int(i, j, 4 * q + 3)},
               r, off, soff, 0);
           if constexpr (C::SWIGLU) {
-            const v16f& g = e.acc[i][j + 2];
             __builtin_amdgcn_raw_buffer_store_b128(
-                v4i{(int)(g[4 * q] * F6_UNSCALE), (int)(g[4 * q + 1] * F6_UNSCALE),
-                    (int)(g[4 * q + 2] * F6_UNSCALE), (int)(g[4 * q + 3] * F6_UNSCALE)},
+                v4i{e.acc_int(i, j + 2, 4 * q), e.acc_int(i, j + 2, 4 * q + 1), e.acc_int(i, j + 2, 4 * q + 2),
+                    e.acc_int(i, j + 2, 4 * q + 3)},
                 r, off + (uint32_t)p.N * ESZ, soff, 0);
           }
         } else {
           float v[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            float x = (e.acc[i][j][4 * q + t] * F6_UNSCALE) * sa[i];
+            float x = e.acc_value(i, j, 4 * q + t) * sa[i];
             x = x * su[t];
             if constexpr (C::SWIGLU) {
-              float g = (e.acc[i][j + 2][4 * q + t] * F6_UNSCALE) * sa[i];
+              float g = e.acc_value(i, j + 2, 4 * q + t) * sa[i];
               g = g * sg[t];
               x = swiglu(x, g);
             } else if constexpr (EPI == EPI_RELU2) {
@@ -394,40 +397,51 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int 
   }
 }
 
-// bf16 epilogue through LDS (plain tiles).  Each wave writes its 128 x 128
-// bf16 results into its own 32 KiB region of the (now idle) ring, row r at
-// r * 256 with 16-byte unit u (columns 8u .. 8u+7) at 16 * (u ^ (r % 16)),
-// then reads the region back four rows per instruction (16 lanes per row)
-// and writes them with 16-byte stores: each store instruction covers four
-// whole 256-byte row segments instead of 32 rows x 16 bytes.  The swizzle
-// makes both directions free of bank conflicts: a write puts lanes 0-15
-// (rows r .. r+15) in 16 distinct units; a read puts the 16 lanes of a row in
-// 16 distinct units.
+// bf16 epilogue through LDS.  Each wave writes its 128-row bf16 results
+// into its own region of the (now idle) ring, then reads the region back
+// row-contiguously and writes whole row segments with 16-byte stores,
+// instead of 32 rows x 16 bytes per store instruction.  16-byte unit u
+// (columns 8u .. 8u+7) of row r sits at r * PITCH + 16 * (u ^ swz(r)):
+//  * 128 columns (PITCH 256, 16 units): swz(r) = r % 16;
+//  * 64 columns, SwiGLU (PITCH 128, 8 units): swz(r) = (r / 2) % 8.
+// Both keep the writes (lanes 0-15 hold rows r .. r+15 of one unit) and the
+// reads (16 lanes hold one or two whole rows) free of bank conflicts.
 template <class C, int EPI, bool NO_NAN, class E>
-__device__ __forceinline__ void f6_epilogue_lds(const E& e, const DenseArgs& p, uint8_t* smem, int m0, int n0,
-                                                const float (&sa)[4], const uint2 (&sb)[4][4]) {
-  static_assert(!C::SWIGLU, "plain tiles");
+__device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const DenseArgs& p, uint8_t* smem, int m0, int n0,
+                                                    const float (&sa)[4], const uint2 (&sb)[4][4]) {
+  constexpr int UNITS = E::TN / 8;
+  constexpr int PITCH = 16 * UNITS;
+  auto swz = [](int r) { return UNITS == 16 ? (r & 15) : ((r >> 1) & 7); };
   // every wave has finished reading the ring
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  uint8_t* region = smem + (size_t)e.wave * 32768;
+  uint8_t* region = smem + (size_t)e.wave * 128 * PITCH;
   const int lane = e.lane;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < E::FN; ++j) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      float su[4];
+      float su[4], sg[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) su[t] = f6_bf16_at(sb[j][q], t);
-      const int u = 4 * j + q;          // 16-byte unit: columns 32j + 8q .. +7
+      for (int t = 0; t < 4; ++t) {
+        su[t] = f6_bf16_at(sb[j][q], t);
+        sg[t] = C::SWIGLU ? f6_bf16_at(sb[j + 2 < 4 ? j + 2 : j][q], t) : 0.0f;
+      }
+      const int u = 4 * j + q;           // columns 32j + 8q .. +7
       const int half = 8 * (lane >> 5);  // columns +4 .. +7 of the unit
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          float x = (e.acc[i][j][4 * q + t] * F6_UNSCALE) * sa[i];
+          float x = e.acc_value(i, j, 4 * q + t) * sa[i];
           x = x * su[t];
-          if constexpr (EPI == EPI_RELU2) x = apply_epi(x, EPI_RELU2);
+          if constexpr (C::SWIGLU) {
+            float g = e.acc_value(i, j + 2, 4 * q + t) * sa[i];
+            g = g * sg[t];
+            x = swiglu(x, g);
+          } else if constexpr (EPI == EPI_RELU2) {
+            x = apply_epi(x, EPI_RELU2);
+          }
           v[t] = x;
         }
         uint32_t lo, hi;
@@ -439,22 +453,73 @@ __device__ __forceinline__ void f6_epilogue_lds(const E& e, const DenseArgs& p, 
           hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
         }
         const int r = 32 * i + (lane & 31);
-        *reinterpret_cast<uint2*>(region + r * 256 + 16 * (u ^ (r & 15)) + half) = make_uint2(lo, hi);
+        *reinterpret_cast<uint2*>(region + r * PITCH + 16 * (u ^ swz(r)) + half) = make_uint2(lo, hi);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // read back four rows per instruction and store whole row segments
+  // read back 64 / UNITS rows per instruction and store whole row segments
   const unsigned long long first = (unsigned long long)m0 * p.N + n0;
   const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(p.out) + first * 2, ((unsigned long long)p.M * p.N - first) * 2);
-  const int rr = lane >> 4, u = lane & 15;
-  const uint32_t voff = ((uint32_t)(e.wm * 128 + rr) * (uint32_t)p.N + (uint32_t)(e.wn * 128 + 8 * u)) * 2u;
+  constexpr int ROWS = 64 / UNITS;
+  const int rr = lane / UNITS, u = lane % UNITS;
+  const uint32_t voff = ((uint32_t)(e.wm * 128 + rr) * (uint32_t)p.N + (uint32_t)(e.wn * E::TN + 8 * u)) * 2u;
 #pragma unroll
-  for (int t = 0; t < 32; ++t) {
-    const int r = 4 * t + rr;
-    const uint4 x = *reinterpret_cast<const uint4*>(region + r * 256 + 16 * (u ^ (r & 15)));
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(4 * t) * (uint32_t)p.N * 2u,
-                                           0);
+  for (int t = 0; t < 128 / ROWS; ++t) {
+    const int r = ROWS * t + rr;
+    const uint4 x = *reinterpret_cast<const uint4*>(region + r * PITCH + 16 * (u ^ swz(r)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff,
+                                           (uint32_t)(ROWS * t) * (uint32_t)p.N * 2u, 0);
+  }
+}
+
+// B scales of the wave's columns (bf16, four per load): [j][q] for
+// fragment j, register group q; fragments j >= FN read the gate's scales.
+template <class C, class E>
+__device__ __forceinline__ void mfma32_load_b_scales(const E& e, const DenseArgs& p, int n0, uint2 (&sb)[4][4]) {
+  const int gate = C::SWIGLU ? p.N : 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int jj = j < E::FN ? j : j - E::FN;
+      sb[j][q] = *reinterpret_cast<const uint2*>(p.b_scale + (j < E::FN ? 0 : gate) + n0 + e.out_col(jj, q));
+    }
+}
+
+// Epilogue of the 32x32 engines after the K loop: OUT_I32 and OUT_F32 store
+// directly; bf16 goes through LDS, with the hardware conversion when no
+// value can be NaN (finite scales times a finite integer give at most
+// +-inf, and ReLU^2 of that is no NaN either; SwiGLU always rounds in
+// software).
+template <class C, int MODE, int EPI, class E>
+__device__ __forceinline__ void mfma32_finish(const E& e, const DenseArgs& p, uint8_t* smem, int m0, int n0,
+                                              const float (&sa)[4]) {
+  if constexpr (MODE == OUT_I32) {
+    const uint2 none[4][4] = {};
+    f6_epilogue<C, OUT_I32, EPI_NONE, false>(e, p, m0, n0, sa, none);
+    return;
+  }
+  uint2 sb[4][4];
+  mfma32_load_b_scales<C>(e, p, n0, sb);
+  if constexpr (MODE == OUT_F32) {
+    f6_epilogue<C, OUT_F32, EPI, false>(e, p, m0, n0, sa, sb);
+  } else if constexpr (C::SWIGLU) {
+    mfma32_epilogue_lds<C, EPI_NONE, false>(e, p, smem, m0, n0, sa, sb);
+  } else {
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) finite = finite && (__float_as_uint(sa[i]) & 0x7F800000u) != 0x7F800000u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint2 w = sb[j][q];
+        finite = finite && (w.x & 0x7F80u) != 0x7F80u && (w.x & 0x7F800000u) != 0x7F800000u &&
+                 (w.y & 0x7F80u) != 0x7F80u && (w.y & 0x7F800000u) != 0x7F800000u;
+      }
+    if (__all(finite)) mfma32_epilogue_lds<C, EPI, true>(e, p, smem, m0, n0, sa, sb);
+    else mfma32_epilogue_lds<C, EPI, false>(e, p, smem, m0, n0, sa, sb);
   }
 }
 
@@ -476,38 +541,7 @@ __global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
   e.run(p.K / 128);
-  // B scales (bf16, four per load), loaded once the loop has freed the
-  // fragment registers; fragments j >= FN read the gate's scales
-  const int gate = C::SWIGLU ? p.N : 0;
-  uint2 sb[4][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int jj = j < E::FN ? j : j - E::FN;
-      sb[j][q] = MODE == OUT_I32 ? uint2{0, 0}
-                                 : *reinterpret_cast<const uint2*>(p.b_scale + (j < E::FN ? 0 : gate) + n0 +
-                                                                   e.out_col(jj, q));
-    }
-  if constexpr (MODE != OUT_BF16 || C::SWIGLU) {
-    f6_epilogue<C, MODE, EPI, false>(e, p, m0, n0, sa, sb);
-  } else {
-    // Finite scales times a finite integer give no NaN (at most +-inf), and
-    // neither does ReLU^2 of such a value.
-    bool finite = true;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) finite = finite && (__float_as_uint(sa[i]) & 0x7F800000u) != 0x7F800000u;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint2 w = sb[j][q];
-        finite = finite && (w.x & 0x7F80u) != 0x7F80u && (w.x & 0x7F800000u) != 0x7F800000u &&
-                 (w.y & 0x7F80u) != 0x7F80u && (w.y & 0x7F800000u) != 0x7F800000u;
-      }
-    if (__all(finite)) f6_epilogue_lds<C, EPI, true>(e, p, smem, m0, n0, sa, sb);
-    else f6_epilogue_lds<C, EPI, false>(e, p, smem, m0, n0, sa, sb);
-  }
+  mfma32_finish<C, MODE, EPI>(e, p, smem, m0, n0, sa);
 }
 
 }  // namespace shk

@@ -7,7 +7,7 @@
 #include <vector>
 
 #include "../../include/strix_halo_gfx950.h"
-#include "shk_f6.h"
+#include "shk_i8.h"
 
 namespace shk {
 
@@ -31,12 +31,16 @@ hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
 // fp6 path.  f6_convert_operand converts A (operand 0) or B (operand 1) of
 // a dense call into its part of the workspace (A first, then B); the GEMM
 // then reads both parts.
-inline hipError_t f6_convert_operand(const DenseArgs& a, int operand, bool swiglu, hipStream_t s) {
+inline F6PackArgs f6_pack_args(const DenseArgs& a, int operand, bool swiglu) {
   const int kb = a.K / 64;
-  if (operand == 0)
-    return launch_f6_pack(F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0}, a.layout == SHK_LAYOUT_TN, s);
-  return launch_f6_pack(F6PackArgs{a.b, a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0},
-                        a.layout != SHK_LAYOUT_NT, s);
+  if (operand == 0) return F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0};
+  return F6PackArgs{a.b, a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0};
+}
+inline bool f6_mn_major(const DenseArgs& a, int operand) {
+  return operand == 0 ? a.layout == SHK_LAYOUT_TN : a.layout != SHK_LAYOUT_NT;
+}
+inline hipError_t f6_convert_operand(const DenseArgs& a, int operand, bool swiglu, hipStream_t s) {
+  return launch_f6_pack(f6_pack_args(a, operand, swiglu), f6_mn_major(a, operand), s);
 }
 template <class C>
 hipError_t launch_f6_gemm_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
@@ -59,10 +63,27 @@ hipError_t launch_f6_gemm_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
 }
 template <class C>
 hipError_t launch_f6_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
-  hipError_t err = f6_convert_operand(a, 0, C::SWIGLU, s);
-  if (err == hipSuccess) err = f6_convert_operand(a, 1, C::SWIGLU, s);
+  hipError_t err = launch_f6_pack2(f6_pack_args(a, 0, C::SWIGLU), f6_mn_major(a, 0), f6_pack_args(a, 1, C::SWIGLU),
+                                   f6_mn_major(a, 1), s);
   if (err == hipSuccess) err = launch_f6_gemm_t<C>(a, grid, s);
   return err;
+}
+// int8 32x32 engine: one kernel per output mode and epilogue.
+template <class C>
+hipError_t launch_i8_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  if (a.out_mode == OUT_I32) {
+    hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_I32, EPI_NONE>), grid, dim3(256), 0, s, a);
+  } else if (a.out_mode == OUT_F32) {
+    if (!C::SWIGLU && a.epilogue == EPI_RELU2)
+      hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_F32, EPI_RELU2>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_F32, EPI_NONE>), grid, dim3(256), 0, s, a);
+  } else if (!C::SWIGLU && a.epilogue == EPI_RELU2) {
+    hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_BF16, EPI_RELU2>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_BF16, EPI_NONE>), grid, dim3(256), 0, s, a);
+  }
+  return hipGetLastError();
 }
 template <class C>
 hipError_t launch_fwd_t(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
@@ -100,6 +121,11 @@ constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
 template <class C>
 Entry dense_entry(int layout, int group_m) {
   return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_dense_t<C>, nullptr, nullptr, nullptr};
+}
+template <class C>
+Entry i8_entry(int layout, int group_m) {
+  static_assert(C::LDS_BYTES == I8Engine<C>::LDS_BYTES && C::NUM_STAGES == I8Engine<C>::P, "table geometry");
+  return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_i8_t<C>, nullptr, nullptr, nullptr};
 }
 template <class C>
 Entry f6_entry(int layout) {

@@ -11,6 +11,7 @@ size, checked on sampled rows.
 
 from __future__ import annotations
 
+import math
 import numpy as np
 import pytest
 
@@ -55,6 +56,38 @@ def test_every_registry_kernel_matches_oracle(kernel, device):
         k = -(-k // sub) * sub
     m, n = 2 * shape.m, 2 * shape.n  # several tiles
     seed = stable_seed(kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=epi == "swiglu")
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q)), "int32 accumulators differ"
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=bits, layout=layout, a_scale=sa, b_scale=sb,
+                                   subchannel=sub, epilogue=epi)
+    if epi == "swiglu":
+        assert max_ulp(got, want) <= ULP_TOL
+    else:
+        assert np.array_equal(got, want)
+
+
+def _odd_stage_k(kernel):
+    """Three K periods of the kernel (block_k, or the least common multiple
+    with the sub-channel group), when that is an odd number of K blocks."""
+    bk = kernel.tile.block_k * kernel.tile.split_k
+    sub = kernel.scale.subchannel_size if kernel.scale.mode is shk.ScaleMode.SUBCHANNEL else None
+    unit = math.lcm(bk, sub) if sub else bk
+    return 3 * unit if (3 * unit // bk) % 2 == 1 else None
+
+
+@pytest.mark.parametrize("kernel", [k for k in shk.default_registry.all() if _odd_stage_k(k)],
+                         ids=lambda k: k.kernel_id)
+def test_every_registry_kernel_odd_stage_count(kernel, device):
+    """Pipelined kernels run K blocks in pairs; an odd count ends on a single
+    block, which must not multiply a stale ring slot."""
+    bits, layout, sub, epi = _kernel_params(kernel)
+    shape = representative_generation_shape(kernel)
+    k = _odd_stage_k(kernel)
+    m, n = 2 * shape.m, 2 * shape.n
+    seed = stable_seed(kernel.kernel_id, "odd")
     a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=sub,
                                                  swiglu=epi == "swiglu")
     print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
