@@ -245,9 +245,12 @@ def bench_c5(torch, shk, steps, warmup):
     def fwd():
         # The device work of one ragged_dot_int4 call (task list + grouped
         # kernel); the API's host-side group-size validation is not timed.
+        # (the fp6 entry, as ragged_dot_int4 picks for this shape: both
+        # operand conversions are inside the timed call)
         return native.launch_ragged_fwd(lhs, rhs, gs, a_scale=sa, b_scale=sb, out=out_f,
-                                        layout=shk.GemmLayout.NN, subchannel=None, block_m=64, align_tile=8,
-                                        rows=rows, cols=n, k_packed=k // 2, out_mode=kt.OUT_BF16)
+                                        layout=shk.GemmLayout.NN, subchannel=None, block_m=kt.RAGGED_FP6_BLOCK_M,
+                                        align_tile=kt.RAGGED_FP6_ALIGN, rows=rows, cols=n, k_packed=k // 2,
+                                        out_mode=kt.OUT_BF16)
 
     ref_out = shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb)
     fwd()
@@ -268,7 +271,7 @@ def bench_c5(torch, shk, steps, warmup):
 
     def bwd():
         return native.launch_ragged_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, out=out_b, layout=shk.GemmLayout.NN,
-                                        subchannel=None, split_k=1, rows=2048, cols=n, k_packed=cap // 2)
+                                        subchannel=None, split_k=1, rows=2048, cols=n, k_packed=cap // 2, fp6=True)
 
     api_b = shk.ragged_dot_int4_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b)
     bwd()

@@ -209,13 +209,38 @@ int32_t amd_strix_halo_kernels_ragged_task_capacity(int32_t rows, int32_t groups
  * Layouts: NN lhs[m, k'], rhs[G, k', n]; NT rhs[G, n, k']; TN lhs[k', m];
  * TT both.  Scales bf16: per-channel a_scale[m], b_scale[G, n]; subchannel S
  * a_scale[m, ceil(k/S)], b_scale[G, ceil(k/S), n].  out_mode BF16 or F32
- * (or I32 raw) [m, n].  The entry's block_m must equal the task tile. */
+ * (or I32 raw) [m, n].  The entry's block_m must equal the task tile.
+ * FP6 entries (operand_format) need a workspace: they fail here and run
+ * through amd_strix_halo_kernels_launch_ragged_fwd_ws. */
 int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index, uintptr_t stream,
                                              const void* lhs, const void* rhs, const void* a_scale,
                                              const void* b_scale, const int32_t* tasks_i32,
                                              const int32_t* num_tasks_i32, int32_t capacity,
                                              void* out, int32_t m, int32_t n, int32_t k_packed,
                                              int32_t groups, int32_t subchannel, int32_t out_mode);
+
+/* ---- fp6 ragged entries -----------------------------------------------------
+ * No counterpart in the reference (its ragged kernels read the packed
+ * operands directly).  FP6 ragged entries convert both int4 operands into
+ * the fp6 block format in a caller workspace of
+ * amd_strix_halo_kernels_ragged_workspace_bytes bytes (0 for PACKED
+ * entries; sizes as passed to the launch), 16-byte aligned, then run the
+ * 256 x 256 fp6 GEMM.  They are per-channel, need 16-byte aligned lhs and
+ * rhs, M and N multiples of 16, out 16-byte and b_scale 8-byte aligned.
+ * Forward: K a multiple of 128, task list built with tile 256 and an
+ * align_tile that is a multiple of 32.  Backward: K capacity a multiple of
+ * 32; split_k has no effect (each output is computed whole and written, the
+ * result of split_k = 1).  Otherwise the _ws calls equal the calls above,
+ * which they replace for every entry. */
+int amd_strix_halo_kernels_ragged_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k_packed,
+                                                  int32_t groups, uint64_t* bytes);
+int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_index, uintptr_t stream,
+                                                const void* lhs, const void* rhs, const void* a_scale,
+                                                const void* b_scale, const int32_t* tasks_i32,
+                                                const int32_t* num_tasks_i32, int32_t capacity,
+                                                void* out, int32_t m, int32_t n, int32_t k_packed,
+                                                int32_t groups, int32_t subchannel, int32_t out_mode,
+                                                void* workspace, uint64_t workspace_bytes);
 
 /* ---- ragged backward --------------------------------------------------------
  * Replaces amd_strix_halo_kernels_launch_ragged_bwd_hsaco (dispatch.cpp:391-457)
@@ -237,6 +262,13 @@ int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index,
                                              void* out, int32_t m, int32_t n, int32_t k_packed,
                                              int32_t groups, int32_t subchannel, int32_t split_k,
                                              int32_t out_mode);
+/* The backward with a workspace (fp6 ragged entries above). */
+int amd_strix_halo_kernels_launch_ragged_bwd_ws(int kernel_index, int device_index, uintptr_t stream,
+                                                const void* lhs, const void* rhs, const void* a_scale,
+                                                const void* b_scale, const int32_t* group_sizes,
+                                                void* out, int32_t m, int32_t n, int32_t k_packed,
+                                                int32_t groups, int32_t subchannel, int32_t split_k,
+                                                int32_t out_mode, void* workspace, uint64_t workspace_bytes);
 
 #ifdef __cplusplus
 }

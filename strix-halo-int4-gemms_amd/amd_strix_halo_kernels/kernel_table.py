@@ -12,6 +12,7 @@ This table replaces the reference's tuned gfx1151 tile seeds
 
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass
 
 FAMILY_DENSE = 0
@@ -78,6 +79,19 @@ class KernelDesc:
         b_cols = 2 * n if self.epilogue_kind == EPI_KIND_SWIGLU else n
         return (m * k * 3) // 4 + (b_cols * k * 3) // 4
 
+    def ragged_workspace_bytes(self, m: int, n: int, k_packed: int, groups: int) -> int:
+        """Bytes of the operand workspace of a ragged call (0 for PACKED):
+        with K rounded up to 128, the forward holds A (round32(m) rows) and
+        per group B (round32(n) rows); the backward per group A, then per
+        group B (k_f6ragged.hip)."""
+        if not self.needs_workspace or m == 0 or n == 0 or groups == 0:
+            return 0
+        kw = -(-2 * k_packed // 128) * 128
+        m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
+        if self.family == FAMILY_RAGGED_FWD:
+            return (m32 * kw * 3) // 4 + groups * ((n32 * kw * 3) // 4)
+        return groups * ((m32 * kw * 3) // 4 + (n32 * kw * 3) // 4)
+
     def serves_subchannel(self, size: int | None) -> bool:
         if self.scale_mode == SCALE_PER_CHANNEL:
             return size is None
@@ -140,12 +154,15 @@ def _build() -> tuple[KernelDesc, ...]:
             add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True, mk=32)
             add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, swiglu=True, subch=True, mk=32)
     for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN, LAYOUT_TT):
+        # fp6 entries lead each family (k_ragged.hip)
+        add(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, group_m=1, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             f = dict(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1)
             add(**f, bm=16, bn=128, bk=128, wm=1, wn=4)
             add(**f, bm=32, bn=128, bk=128, wm=2, wn=2)
             add(**f, bm=64, bn=128, bk=128, wm=2, wn=2)
             add(**f, bm=128, bn=128, bk=128, wm=2, wn=2)
+        add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, group_m=1, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1, bm=128, bn=128,
                 bk=128, wm=2, wn=2)
@@ -159,17 +176,36 @@ def entries(family: int) -> tuple[KernelDesc, ...]:
     return tuple(d for d in TABLE if d.family == family)
 
 
-def find_ragged(family: int, *, layout: int, subchannel: int | None, block_m: int | None = None) -> KernelDesc:
-    """Ragged kernel for a layout and scale mode (and task rows for the forward)."""
+@functools.lru_cache(maxsize=None)
+def find_ragged(family: int, *, layout: int, subchannel: int | None, block_m: int | None = None,
+                fp6: bool = False) -> KernelDesc:
+    """Ragged kernel for a layout and scale mode (and task rows for the
+    forward): an FP6 entry if `fp6`, else one that reads the packed operands."""
+    fmt = OPERANDS_FP6 if fp6 else OPERANDS_PACKED
     for d in TABLE:
         if d.family != family or d.layout != layout or not d.serves_subchannel(subchannel):
+            continue
+        if d.operand_format != fmt:
             continue
         if block_m is not None and d.block_m != block_m:
             continue
         return d
     raise LookupError(
-        f"no gfx950 ragged kernel for family={family}, layout={layout}, subchannel={subchannel}, block_m={block_m}"
+        f"no gfx950 ragged kernel for family={family}, layout={layout}, subchannel={subchannel}, block_m={block_m}, "
+        f"fp6={fp6}"
     )
 
 
-RAGGED_FWD_BLOCK_M = tuple(sorted({d.block_m for d in entries(FAMILY_RAGGED_FWD)}))
+def ragged_fp6_eligible(family: int, *, subchannel: int | None, m: int, n: int, k_packed: int) -> bool:
+    """Whether a ragged call's sizes suit the fp6 entries (k_f6ragged.hip):
+    per-channel, N a multiple of 8 (whole 16-byte output units) and K at
+    most FP6_MAX_K.  The same for the forward and the backward (`family`)."""
+    del family, m
+    return subchannel is None and n % 8 == 0 and 2 * k_packed <= FP6_MAX_K
+
+
+# Task rows of the forward kernels that read packed operands, and of the fp6
+# forward (whose task list is built with align_tile 32).
+RAGGED_FWD_BLOCK_M = tuple(sorted({d.block_m for d in entries(FAMILY_RAGGED_FWD) if not d.needs_workspace}))
+RAGGED_FP6_BLOCK_M = 256
+RAGGED_FP6_ALIGN = 32

@@ -18,6 +18,7 @@ raises otherwise.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from dataclasses import dataclass
 from pathlib import Path
@@ -46,6 +47,7 @@ class _Desc(ctypes.Structure):
         "group_size_m", "operand_format")]
 
 
+@functools.lru_cache(maxsize=None)
 def package_root() -> Path:
     return Path(__file__).resolve().parent
 
@@ -95,6 +97,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_launch_ragged_bwd.argtypes = [I, I, U, P, P, P, P, P, P, I32, I32, I32, I32, I32,
                                                              I32, I32]
     lib.amd_strix_halo_kernels_launch_ragged_bwd.restype = I
+    lib.amd_strix_halo_kernels_ragged_workspace_bytes.argtypes = [I, I32, I32, I32, I32,
+                                                                  ctypes.POINTER(ctypes.c_uint64)]
+    lib.amd_strix_halo_kernels_ragged_workspace_bytes.restype = I
+    lib.amd_strix_halo_kernels_launch_ragged_fwd_ws.argtypes = [I, I, U, P, P, P, P, P, P, I32, P, I32, I32, I32,
+                                                                I32, I32, I32, P, ctypes.c_uint64]
+    lib.amd_strix_halo_kernels_launch_ragged_fwd_ws.restype = I
+    lib.amd_strix_halo_kernels_launch_ragged_bwd_ws.argtypes = [I, I, U, P, P, P, P, P, P, I32, I32, I32, I32, I32,
+                                                                I32, I32, P, ctypes.c_uint64]
+    lib.amd_strix_halo_kernels_launch_ragged_bwd_ws.restype = I
 
 
 def load_dispatch_library(path: str | Path | None = None) -> ctypes.CDLL:
@@ -123,7 +134,12 @@ def library_kernel_table(lib: ctypes.CDLL) -> tuple[kt.KernelDesc, ...]:
     return tuple(out)
 
 
+_DEFAULT_LIBRARY: list[ctypes.CDLL] = []  # the verified default library, once loaded
+
+
 def _verified_library(path: str | Path | None = None) -> ctypes.CDLL:
+    if path is None and _DEFAULT_LIBRARY:
+        return _DEFAULT_LIBRARY[0]
     lib = load_dispatch_library(path)
     key = str(Path(path) if path is not None else native_library_path())
     if key not in _VERIFIED:
@@ -132,6 +148,8 @@ def _verified_library(path: str | Path | None = None) -> ctypes.CDLL:
                 f"the kernel table of {key} does not match amd_strix_halo_kernels.kernel_table; rebuild the library"
             )
         _VERIFIED.add(key)
+    if path is None:
+        _DEFAULT_LIBRARY[:] = [lib]
     return lib
 
 
@@ -286,7 +304,8 @@ def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, li
     # fp6 entries convert both operands into a workspace first; it comes from
     # torch's caching allocator on the launch stream, so a later launch on
     # the same stream may reuse it.
-    ws_bytes = gemm_workspace_bytes(kernel, m, n, k, library_path=library_path)
+    # (the table mirror's size, which gemm_workspace_bytes matches)
+    ws_bytes = kt.TABLE[_table_index(kernel)].workspace_bytes(m, n, k)
     work = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
     if work is not None and stream is not None:
         work.record_stream(stream)
@@ -464,6 +483,29 @@ def ragged_group_info_device(
     return tasks, num, info
 
 
+def ragged_workspace_bytes(desc: kt.KernelDesc, m: int, n: int, k_packed: int, groups: int, *,
+                           library_path=None) -> int:
+    """Workspace bytes a ragged table entry needs (0 unless FP6)."""
+    lib = _verified_library(library_path)
+    out = ctypes.c_uint64(0)
+    _check(lib, lib.amd_strix_halo_kernels_ragged_workspace_bytes(desc.index, m, n, k_packed, groups,
+                                                                   ctypes.byref(out)))
+    return int(out.value)
+
+
+def _ragged_workspace(torch, desc, like, m, n, k_packed, groups, stream, head: int = 0):
+    """One uint8 buffer of `head` bytes followed by the entry's operand
+    workspace (sized by the table mirror, which the library's
+    amd_strix_halo_kernels_ragged_workspace_bytes matches), from torch's
+    caching allocator on the launch stream (see _gemm_call)."""
+    nbytes = desc.ragged_workspace_bytes(m, n, k_packed, groups)
+    total = head + nbytes
+    buf = torch.empty(total, dtype=torch.uint8, device=like.device) if total else None
+    if buf is not None and stream is not None:
+        buf.record_stream(stream)
+    return buf, nbytes
+
+
 def launch_ragged_fwd(
     lhs: Any,
     rhs: Any,
@@ -484,26 +526,39 @@ def launch_ragged_fwd(
     stream: Any | None = None,
 ) -> Any:
     """Device task list + grouped forward (replaces launch_ragged_fwd_kernel,
-    native.py:533-600).  No host synchronisation."""
+    native.py:533-600).  No host synchronisation.  block_m 256
+    (kt.RAGGED_FP6_BLOCK_M) selects the fp6 entry, whose operands are
+    converted into a workspace and whose tasks need align_tile a multiple
+    of 32.  The task list, its count and the workspace share one
+    allocation."""
     torch = _torch()
     lib = _verified_library(library_path)
+    fp6 = block_m == kt.RAGGED_FP6_BLOCK_M
     desc = kt.find_ragged(kt.FAMILY_RAGGED_FWD, layout=kt.LAYOUT_CODES[layout.value], subchannel=subchannel,
-                          block_m=block_m)
+                          block_m=block_m, fp6=fp6)
+    if fp6 and align_tile % 32:
+        raise ValueError(f"the fp6 ragged forward needs align_tile a multiple of 32; got {align_tile}")
     groups = int(group_sizes_i32.shape[0])
     capacity = int(lib.amd_strix_halo_kernels_ragged_task_capacity(rows, groups, block_m, align_tile))
-    tasks, num, _ = ragged_group_info_device(group_sizes_i32, tile=block_m, align_tile=align_tile,
-                                             capacity=capacity, with_info=False, library_path=library_path,
-                                             stream=stream)
-    rc = lib.amd_strix_halo_kernels_launch_ragged_fwd(
+    # tasks [capacity, 4] int32, then num_tasks (16 bytes), then the workspace
+    head = 16 * max(capacity, 1) + 16
+    buf, nbytes = _ragged_workspace(torch, desc, lhs, rows, cols, k_packed, groups, stream, head)
+    base = buf.data_ptr()
+    device = _device_index(lhs)
+    handle = _stream_handle(torch, lhs, stream)
+    _check(lib, lib.amd_strix_halo_kernels_ragged_group_info(
+        device, handle, group_sizes_i32.data_ptr(), groups, block_m, align_tile, capacity, base,
+        base + head - 16, None))
+    rc = lib.amd_strix_halo_kernels_launch_ragged_fwd_ws(
         desc.index,
-        _device_index(lhs),
-        _stream_handle(torch, lhs, stream),
+        device,
+        handle,
         lhs.data_ptr(),
         rhs.data_ptr(),
         a_scale.data_ptr(),
         b_scale.data_ptr(),
-        tasks.data_ptr(),
-        num.data_ptr(),
+        base,
+        base + head - 16,
         capacity,
         out.data_ptr(),
         rows,
@@ -512,6 +567,8 @@ def launch_ragged_fwd(
         groups,
         subchannel or 0,
         out_mode,
+        base + head if nbytes else None,
+        nbytes,
     )
     _check(lib, rc)
     return out
@@ -532,15 +589,20 @@ def launch_ragged_bwd(
     cols: int,
     k_packed: int,
     out_mode: int = kt.OUT_F32,
+    fp6: bool = False,
     library_path: str | Path | None = None,
     stream: Any | None = None,
 ) -> Any:
     """Grouped K-ragged backward (replaces launch_ragged_bwd_kernel,
-    native.py:603-667)."""
+    native.py:603-667).  fp6: run the fp6 entry (per-channel), whose operands
+    are converted into a workspace."""
     torch = _torch()
     lib = _verified_library(library_path)
-    desc = kt.find_ragged(kt.FAMILY_RAGGED_BWD, layout=kt.LAYOUT_CODES[layout.value], subchannel=subchannel)
-    rc = lib.amd_strix_halo_kernels_launch_ragged_bwd(
+    desc = kt.find_ragged(kt.FAMILY_RAGGED_BWD, layout=kt.LAYOUT_CODES[layout.value], subchannel=subchannel,
+                          fp6=fp6)
+    groups = int(group_sizes_i32.shape[0])
+    work, nbytes = _ragged_workspace(torch, desc, lhs, rows, cols, k_packed, groups, stream)
+    rc = lib.amd_strix_halo_kernels_launch_ragged_bwd_ws(
         desc.index,
         _device_index(lhs),
         _stream_handle(torch, lhs, stream),
@@ -553,10 +615,12 @@ def launch_ragged_bwd(
         rows,
         cols,
         k_packed,
-        int(group_sizes_i32.shape[0]),
+        groups,
         subchannel or 0,
         split_k,
         out_mode,
+        work.data_ptr() if work is not None else None,
+        nbytes,
     )
     _check(lib, rc)
     return out

@@ -10,10 +10,15 @@ ragged.py (ragged.py:11-72, 201-366, 834-1402).  What differs is underneath:
 * the kernels are the gfx950 table kernels; the Triton JIT fallback of the
   reference does not exist, and ``use_native=False`` (which asked for it) is
   rejected;
-* ``RaggedDotConfig.block_m`` / ``align_tile`` set the task tiling when the
-  table has that block_m (16, 32, 64, 128), otherwise 64 is used; block_n,
-  block_k, num_warps and num_stages are Triton tuning knobs with no effect on
-  the result, and the gfx950 kernels use their own;
+* per-channel calls with N a multiple of 8 (and a 16-byte aligned output,
+  an 8-byte aligned b_scale) run the fp6 kernels, which convert both int4
+  operands into a workspace and use the fp6 MFMA at twice the int8 rate; the
+  forward's task tile is then 256 rows with align_tile 32;
+* otherwise ``RaggedDotConfig.block_m`` / ``align_tile`` set the task tiling
+  when the table has that block_m (16, 32, 64, 128), else 64 is used (block_m
+  64, the default, and 256 leave the choice of the fp6 kernel to the
+  library); block_n, block_k, num_warps and num_stages are Triton tuning
+  knobs with no effect on the result, and the gfx950 kernels use their own;
 * ``RaggedBwdDotConfig.split_k`` is honoured: per-channel splits add exact
   int32 partials (the result equals split_k=1), subchannel splits own whole
   scale groups and add fp32 partials (as the reference, atomically);
@@ -384,6 +389,15 @@ def _scales_or_ones(torch, a_scale, b_scale, a_shape, b_shape, device):
     return a_scale, b_scale
 
 
+def _aligned(tensor: Any, nbytes: int) -> bool:
+    return tensor.data_ptr() % nbytes == 0
+
+
+def _fp6_buffers_ok(out: Any, b_scale: Any) -> bool:
+    """Buffer alignment the fp6 ragged kernels need (k_f6ragged.hip)."""
+    return _aligned(out, 16) and _aligned(b_scale, 8)
+
+
 def _reject_jit(use_native: bool | None) -> None:
     if use_native is False:
         raise ValueError("use_native=False requests the Triton JIT path, which this gfx950 build does not have")
@@ -462,8 +476,13 @@ def ragged_dot_int4(
     a_shape = (rows,) if subchannel is None else (rows, scale_cols)
     b_shape = (groups, cols) if subchannel is None else (groups, scale_cols, cols)
     a_scale, b_scale = _scales_or_ones(torch, a_scale, b_scale, a_shape, b_shape, lhs.device)
-    block_m = config.block_m if config.block_m in kt.RAGGED_FWD_BLOCK_M else 64
-    align = config.align_tile if block_m % config.align_tile == 0 else 8
+    if (config.block_m in (64, kt.RAGGED_FP6_BLOCK_M)
+            and kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_FWD, subchannel=subchannel, m=rows, n=cols, k_packed=k_packed)
+            and _fp6_buffers_ok(out, b_scale)):
+        block_m, align = kt.RAGGED_FP6_BLOCK_M, kt.RAGGED_FP6_ALIGN
+    else:
+        block_m = config.block_m if config.block_m in kt.RAGGED_FWD_BLOCK_M else 64
+        align = config.align_tile if block_m % config.align_tile == 0 else 8
     from .native import launch_ragged_fwd
 
     gs = group_sizes.to(device=lhs.device, dtype=torch.int32).contiguous()
@@ -545,9 +564,11 @@ def ragged_dot_int4_bwd(
     from .native import launch_ragged_bwd
 
     gs = group_sizes.to(device=lhs.device, dtype=torch.int32).contiguous()
+    fp6 = (kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_BWD, subchannel=subchannel, m=rows, n=cols, k_packed=k_packed)
+           and _fp6_buffers_ok(out, b_scale))
     return launch_ragged_bwd(
         lhs, rhs, gs, a_scale=a_scale, b_scale=b_scale, out=out, layout=layout, subchannel=subchannel,
-        split_k=config.split_k, rows=rows, cols=cols, k_packed=k_packed,
+        split_k=config.split_k, rows=rows, cols=cols, k_packed=k_packed, fp6=fp6,
         library_path=native_library_path if native_library_path is not None else (
             None if native_root is None else f"{native_root}/libamd_strix_halo_kernels_gfx950.so"),
     )

@@ -65,6 +65,7 @@ def translation_units() -> list[tuple[str, Path, list[str]]]:
     # operand conversion is compiled with the default scheduler.
     units.append(("dense_f6", CSRC / "k_f6.hip", list(DMA_FLAGS)))
     units.append(("f6pack", CSRC / "k_f6pack.hip", []))
+    units.append(("ragged_f6", CSRC / "k_f6ragged.hip", list(DMA_FLAGS)))
     for layout in (0, 1, 2, 3):
         units.append((f"ragged_{layout}", CSRC / "k_ragged.hip", [f"-DSHK_LAYOUT={layout}"]))
     units.append(("capi", CSRC / "capi.hip", []))

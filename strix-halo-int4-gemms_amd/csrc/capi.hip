@@ -239,6 +239,35 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
 }
 
 
+// Workspace of a ragged entry: both operands in fp6 block format for FP6
+// entries (forward: A, then B per group; backward: A per group, then B per
+// group), nothing otherwise.
+uint64_t ragged_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k_packed, int32_t groups) {
+  if (d.operand_format != SHK_OPERANDS_FP6) return 0;
+  if (d.family == SHK_FAMILY_RAGGED_FWD) return shk::f6_ragged_fwd_workspace(m, n, 2 * k_packed, groups);
+  return shk::f6_ragged_bwd_workspace(m, n, 2 * k_packed, groups);
+}
+
+// Requirements of the fp6 ragged entries: a K that keeps fp32 sums exact,
+// whole 16-byte output units (N a multiple of 8, out 16-byte aligned) and
+// 4-scale loads (b_scale 8-byte aligned), 32-bit offsets within a tile, and
+// a large enough workspace.  Operands may have any alignment.
+int check_f6_ragged(const shk_kernel_desc& d, const void* b_scale, const void* out, int32_t m, int32_t n,
+                    int32_t k_packed, int32_t groups, const void* workspace, uint64_t workspace_bytes) {
+  const int k = 2 * k_packed;
+  if (k > shk::F6_MAX_K) return fail("fp6 kernels support K <= " + std::to_string(shk::F6_MAX_K));
+  if (n % 8) return fail("kernel " + std::to_string(d.index) + " needs N to be a multiple of 8; got " + std::to_string(n));
+  if (!aligned(out, 16) || !aligned(b_scale, 8)) return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
+  if ((unsigned long long)n * 4ull * 256ull >= (1ull << 32)) return fail("ragged output rows are limited to 4194304 bytes");
+  // nothing runs without rows, columns or groups
+  const uint64_t need = (m == 0 || n == 0 || groups == 0) ? 0 : ragged_workspace_bytes(d, m, n, k_packed, groups);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    return fail("kernel " + std::to_string(d.index) + " converts its operands into a workspace of " +
+                std::to_string(need) + " bytes (amd_strix_halo_kernels_ragged_workspace_bytes)");
+  if (need > 0 && !aligned(workspace, 16)) return fail("the workspace must be 16-byte aligned");
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -388,16 +417,44 @@ int amd_strix_halo_kernels_ragged_group_info(int device_index, uintptr_t stream,
   return 0;
 }
 
+int amd_strix_halo_kernels_ragged_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k_packed,
+                                                  int32_t groups, uint64_t* bytes) {
+  g_last_error.clear();
+  if (bytes == nullptr) return fail("bytes must be non-null");
+  const auto& t = table();
+  if (kernel_index < 0 || kernel_index >= (int)t.size())
+    return fail("kernel index " + std::to_string(kernel_index) + " is out of range");
+  const shk_kernel_desc& d = t[kernel_index].d;
+  if (d.family != SHK_FAMILY_RAGGED_FWD && d.family != SHK_FAMILY_RAGGED_BWD)
+    return fail("kernel index " + std::to_string(kernel_index) + " is not a ragged kernel");
+  if (m < 0 || n < 0 || k_packed < 0 || groups < 0) return fail("sizes must be non-negative");
+  *bytes = ragged_workspace_bytes(d, m, n, k_packed, groups);
+  return 0;
+}
+
 int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index, uintptr_t stream,
                                              const void* lhs, const void* rhs, const void* a_scale,
                                              const void* b_scale, const int32_t* tasks_i32,
                                              const int32_t* num_tasks_i32, int32_t capacity, void* out, int32_t m,
                                              int32_t n, int32_t k_packed, int32_t groups, int32_t subchannel,
                                              int32_t out_mode) {
+  return amd_strix_halo_kernels_launch_ragged_fwd_ws(kernel_index, device_index, stream, lhs, rhs, a_scale,
+                                                     b_scale, tasks_i32, num_tasks_i32, capacity, out, m, n,
+                                                     k_packed, groups, subchannel, out_mode, nullptr, 0);
+}
+
+int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_index, uintptr_t stream,
+                                                const void* lhs, const void* rhs, const void* a_scale,
+                                                const void* b_scale, const int32_t* tasks_i32,
+                                                const int32_t* num_tasks_i32, int32_t capacity, void* out,
+                                                int32_t m, int32_t n, int32_t k_packed, int32_t groups,
+                                                int32_t subchannel, int32_t out_mode, void* workspace,
+                                                uint64_t workspace_bytes) {
   g_last_error.clear();
   const Entry* e = nullptr;
   if (lookup(kernel_index, SHK_FAMILY_RAGGED_FWD, &e)) return 1;
   const shk_kernel_desc& d = e->d;
+  const bool fp6 = d.operand_format == SHK_OPERANDS_FP6;
   if (lhs == nullptr || rhs == nullptr || a_scale == nullptr || b_scale == nullptr || out == nullptr ||
       tasks_i32 == nullptr || num_tasks_i32 == nullptr)
     return fail("lhs, rhs, scales, task list and out pointers must be non-null");
@@ -405,9 +462,10 @@ int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index,
   if (check_subchannel(d, subchannel)) return 1;
   if (check_out_mode(out_mode)) return 1;
   const int k = 2 * k_packed;
-  if (d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
+  if (!fp6 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
   if (!aligned(tasks_i32, 16)) return fail("tasks buffer must be 16-byte aligned");
+  if (fp6 && check_f6_ragged(d, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
   if (m == 0 || n == 0 || capacity == 0) return 0;
   shk::RaggedFwdArgs p{};
   p.lhs = static_cast<const uint8_t*>(lhs);
@@ -432,6 +490,8 @@ int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index,
   p.a_aligned = a_km ? (aligned(lhs, 16) && p.lda % 16 == 0) : (aligned(lhs, 8) && p.lda % 8 == 0);
   p.b_aligned = b_km ? (aligned(rhs, 16) && p.ldb % 16 == 0) : (aligned(rhs, 8) && p.ldb % 8 == 0);
   p.out_vec = (n % 4 == 0) && aligned(out, 16) && aligned(b_scale, 8);
+  p.layout = d.layout;
+  p.work = static_cast<uint8_t*>(workspace);
   const long tiles_n = (n + d.block_n - 1) / d.block_n;
   const long grid = (long)capacity * tiles_n;
   if (grid > 0x7FFFFFFFL) return fail("ragged forward grid is too large");
@@ -447,10 +507,22 @@ int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index,
                                              const void* b_scale, const int32_t* group_sizes, void* out,
                                              int32_t m, int32_t n, int32_t k_packed, int32_t groups,
                                              int32_t subchannel, int32_t split_k, int32_t out_mode) {
+  return amd_strix_halo_kernels_launch_ragged_bwd_ws(kernel_index, device_index, stream, lhs, rhs, a_scale,
+                                                     b_scale, group_sizes, out, m, n, k_packed, groups, subchannel,
+                                                     split_k, out_mode, nullptr, 0);
+}
+
+int amd_strix_halo_kernels_launch_ragged_bwd_ws(int kernel_index, int device_index, uintptr_t stream,
+                                                const void* lhs, const void* rhs, const void* a_scale,
+                                                const void* b_scale, const int32_t* group_sizes, void* out,
+                                                int32_t m, int32_t n, int32_t k_packed, int32_t groups,
+                                                int32_t subchannel, int32_t split_k, int32_t out_mode,
+                                                void* workspace, uint64_t workspace_bytes) {
   g_last_error.clear();
   const Entry* e = nullptr;
   if (lookup(kernel_index, SHK_FAMILY_RAGGED_BWD, &e)) return 1;
   const shk_kernel_desc& d = e->d;
+  const bool fp6 = d.operand_format == SHK_OPERANDS_FP6;
   if (lhs == nullptr || rhs == nullptr || a_scale == nullptr || b_scale == nullptr || out == nullptr ||
       group_sizes == nullptr)
     return fail("lhs, rhs, scales, group_sizes and out pointers must be non-null");
@@ -460,8 +532,9 @@ int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index,
   if (out_mode != SHK_OUT_F32 && out_mode != SHK_OUT_I32)
     return fail("ragged backward writes fp32 (or raw int32) output");
   const int k_cap = 2 * k_packed;
-  if (d.scale_mode == SHK_SCALE_PER_CHANNEL && k_cap > kMaxInt4AccK)
+  if (!fp6 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k_cap > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
+  if (fp6 && check_f6_ragged(d, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
   if (m == 0 || n == 0 || groups == 0) return 0;
   shk::RaggedBwdArgs p{};
   p.lhs = static_cast<const uint8_t*>(lhs);
@@ -480,19 +553,23 @@ int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index,
   p.ldb = b_km ? k_packed : n;
   p.subchannel = subchannel;
   p.scale_cols = subchannel > 0 ? (k_cap + subchannel - 1) / subchannel : 1;
-  p.split_k = split_k;
+  // fp6 entries compute each output whole: any split_k gives the result of
+  // split_k = 1, which they write directly.
+  p.split_k = fp6 ? 1 : split_k;
   p.out_mode = out_mode;
   p.a_aligned = a_km ? (aligned(lhs, 16) && p.lda % 16 == 0) : (aligned(lhs, 8) && p.lda % 8 == 0);
   p.b_aligned = b_km ? (aligned(rhs, 16) && p.ldb % 16 == 0) : (aligned(rhs, 8) && p.ldb % 8 == 0);
   p.out_vec = (n % 4 == 0) && aligned(out, 16) && aligned(b_scale, 8);
+  p.layout = d.layout;
+  p.work = static_cast<uint8_t*>(workspace);
   const long tiles = (long)groups * ((m + d.block_m - 1) / d.block_m) * ((n + d.block_n - 1) / d.block_n);
   if (tiles > 0x7FFFFFFFL) return fail("ragged backward grid is too large");
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err = e->bwd(p, dim3((unsigned)tiles, (unsigned)split_k), s);
+  hipError_t err = e->bwd(p, dim3((unsigned)tiles, (unsigned)p.split_k), s);
   if (err != hipSuccess) return fail_hip("ragged backward launch", err);
-  if (split_k > 1 && d.scale_mode == SHK_SCALE_PER_CHANNEL && out_mode == SHK_OUT_F32) {
+  if (p.split_k > 1 && d.scale_mode == SHK_SCALE_PER_CHANNEL && out_mode == SHK_OUT_F32) {
     err = shk::launch_bwd_finalize(static_cast<float*>(out), p.a_scale, p.b_scale, groups, m, n, s);
     if (err != hipSuccess) return fail_hip("ragged backward finalize launch", err);
   }

@@ -43,35 +43,93 @@ __device__ __forceinline__ int f6_src_row(int r, int swiglu_n) {
   return 128 * t + 64 * h + (q & 63) + (q >= 64 ? swiglu_n : 0);
 }
 
+// Logical K length of operand g.
+__device__ __forceinline__ int f6_k_len(const F6PackArgs& p, int g) {
+  if (p.k_len == nullptr) return p.k_cap;
+  const int l = p.k_len[g];
+  return l < 0 ? 0 : (l > p.k_cap ? p.k_cap : l);
+}
+// 16 source bytes read one at a time: byte b exists when b < `valid`.
+__device__ __forceinline__ uint4 f6_load_bytes(const uint8_t* q, int valid) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    if (b < valid) w[b / 4] |= (uint32_t)q[b] << (8 * (b % 4));
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// 64-K blocks that the GEMM reads for K length `len`: whole 128-K stages.
+__device__ __forceinline__ int f6_blocks_read(int len) { return 2 * ((len + 127) / 128); }
+
 // K-major source (row r holds its K values contiguously, two per byte): one
 // wave converts one block; a lane loads its 16 source bytes directly.
+// Nibble j of a little-endian source word is K value 8w + j of its 32, so K
+// values at or past the operand's length are cleared word by word.
 __device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
   const int lane = threadIdx.x & 63;
-  const long blk = (long)wg * 4 + (threadIdx.x >> 6);
+  const int panels = f6_panels(p.rows);
+  const long blocks = (long)panels * p.kb;
+  const long per_group = (blocks + 3) / 4;
+  const int g = (int)(wg / per_group);
+  const long blk = (wg - (long)g * per_group) * 4 + (threadIdx.x >> 6);
+  if (blk >= blocks) return;
   const int panel = (int)(blk / p.kb);
   const int kb = (int)(blk - (long)panel * p.kb);
-  const int row = f6_src_row(32 * panel + (lane & 31), p.swiglu_n);
-  const uint4 x = *reinterpret_cast<const uint4*>(p.src + (long)row * p.ld + 32L * kb + 16 * (lane >> 5));
-  f6_store_lane(p.dst + blk * F6_BLOCK, lane, f6_convert(x));
+  const int len = f6_k_len(p, g);
+  if (kb >= f6_blocks_read(len)) return;
+  const int r = 32 * panel + (lane & 31);
+  const int k0 = 64 * kb + 32 * (lane >> 5);
+  uint4 x = make_uint4(0u, 0u, 0u, 0u);
+  if (r < p.rows && k0 < len) {
+    const int row = f6_src_row(r, p.swiglu_n);
+    const uint8_t* q = p.src + g * p.src_group + (long)row * p.ld + 32L * kb + 16 * (lane >> 5);
+    const int keep = len - k0;  // K values of the 32 to keep
+    // bytes holding any of them (the source row ends within the length)
+    x = p.vec ? *reinterpret_cast<const uint4*>(q) : f6_load_bytes(q, (keep + 1) / 2);
+    if (keep < 32) {
+      uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int wq = 0; wq < 4; ++wq) {
+        const int c = keep - 8 * wq;
+        w[wq] &= c >= 8 ? 0xFFFFFFFFu : (c <= 0 ? 0u : (1u << (4 * c)) - 1u);
+      }
+      x = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  f6_store_lane(p.dst + g * p.dst_group + blk * F6_BLOCK, lane, f6_convert(x));
 }
 
 // MN-major source (K row kp holds two K values of every packed row, one per
-// nibble): a workgroup converts the 8 blocks of one 256-row tile and one
-// 64-K block.  The 32 x 256-byte source tile goes through LDS in the
-// MN-major ring layout of the DMA engine, whose transposing reads hand each
-// lane its row's bytes in K order: within a 16-lane group, lane i addresses
-// source row kp + i/2 at byte 8*(i%2) of a 16-row unit and receives the 8
-// bytes of those 8 rows in column i.
+// nibble, the even one low): a workgroup converts the blocks of one 256-row
+// tile and one 64-K block.  The 32 x 256-byte source tile goes through LDS in
+// the MN-major ring layout of the DMA engine, whose transposing reads hand
+// each lane its row's bytes in K order: within a 16-lane group, lane i
+// addresses source row kp + i/2 at byte 8*(i%2) of a 16-row unit and
+// receives the 8 bytes of those 8 rows in column i.  Units past the rows and
+// K rows past the length load as zeros; panels past the rows are not stored.
 __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_t* tile) {
-  const int t = wg / p.kb;
-  const int kb = wg - t * p.kb;
+  const int tiles = (p.rows + F6_TILE - 1) / F6_TILE;
+  const int per_group = tiles * p.kb;
+  const int g = wg / per_group;
+  const int local = wg - g * per_group;
+  const int t = local / p.kb;
+  const int kb = local - t * p.kb;
+  const int len = f6_k_len(p, g);
+  if (kb >= f6_blocks_read(len)) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
   const int u = tid & 15;  // 16-row unit of the tile
-  const long col = f6_src_row(F6_TILE * t + 16 * u, p.swiglu_n);
+  const int r0 = F6_TILE * t + 16 * u;
+  const long col = f6_src_row(r0, p.swiglu_n);
+  const uint8_t* src = p.src + g * p.src_group;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int kp = 16 * q + (tid >> 4);
-    const uint4 x = *reinterpret_cast<const uint4*>(p.src + (32L * kb + kp) * p.ld + col);
+    const int k = 2 * (32 * kb + kp);  // K of the low nibbles
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (r0 < p.rows && k < len) {
+      const uint8_t* q = src + (32L * kb + kp) * p.ld + col;
+      x = p.vec ? *reinterpret_cast<const uint4*>(q) : f6_load_bytes(q, p.rows - r0);
+      if (k + 1 >= len) x = make_uint4(x.x & 0x0F0F0F0Fu, x.y & 0x0F0F0F0Fu, x.z & 0x0F0F0F0Fu, x.w & 0x0F0F0F0Fu);
+    }
     const int swz = (kp & 7) | ((kp & 16) >> 1);
     *reinterpret_cast<uint4*>(tile + kp * 256 + 16 * (u ^ swz)) = x;
   }
@@ -82,23 +140,27 @@ __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_
   const int i = lane & 15;
   const int kp = 16 * (lane >> 5) + i / 2;
   const int swz = (kp & 7) | ((kp & 16) >> 1);
+  const int panels = f6_panels(p.rows);
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int b = 2 * (tid >> 6) + c;
+    if (8 * t + b >= panels) continue;
     const int unit = 2 * b + ((lane >> 4) & 1);
     const uint8_t* q = tile + kp * 256 + 16 * (unit ^ swz) + 8 * (i & 1);
     const v2i lo = ds_read_tr8(q);
     const v2i hi = ds_read_tr8(q + 2048);
     const uint4 x = make_uint4(lo.x, lo.y, hi.x, hi.y);
     const long blk = (long)(8 * t + b) * p.kb + kb;
-    f6_store_lane(p.dst + blk * F6_BLOCK, lane, f6_convert(x));
+    f6_store_lane(p.dst + g * p.dst_group + blk * F6_BLOCK, lane, f6_convert(x));
   }
 }
 
-// Workgroups of one operand: one per 8 blocks (MN-major: a 256-row tile
-// and a 64-K block) or per 4 blocks (K-major: one per wave).
-int pack_groups(const F6PackArgs& a, bool mn_major) {
-  return mn_major ? (a.rows / F6_TILE) * a.kb : (a.rows / 32) * a.kb / 4;
+// Workgroups of one operand batch: per operand, one per 256-row tile and
+// 64-K block (MN-major) or per 4 blocks (K-major: one per wave).
+long pack_groups(const F6PackArgs& a, bool mn_major) {
+  const long per = mn_major ? (long)((a.rows + F6_TILE - 1) / F6_TILE) * a.kb
+                            : ((long)f6_panels(a.rows) * a.kb + 3) / 4;
+  return per * a.groups;
 }
 
 __global__ __launch_bounds__(256) void f6_pack_one(const F6PackArgs p, int mn_major) {
@@ -125,13 +187,18 @@ __global__ __launch_bounds__(256) void f6_pack_two(const F6PackArgs a, const F6P
 }  // namespace
 
 hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s) {
-  hipLaunchKernelGGL(f6_pack_one, dim3(pack_groups(a, mn_major)), dim3(256), 0, s, a, (int)mn_major);
+  const long n = pack_groups(a, mn_major);
+  if (n <= 0) return hipSuccess;
+  if (n > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(f6_pack_one, dim3((unsigned)n), dim3(256), 0, s, a, (int)mn_major);
   return hipGetLastError();
 }
 
 hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s) {
-  const int ga = pack_groups(a, a_mn), gb = pack_groups(b, b_mn);
-  hipLaunchKernelGGL(f6_pack_two, dim3(ga + gb), dim3(256), 0, s, a, b, (int)a_mn, (int)b_mn, ga);
+  const long ga = pack_groups(a, a_mn), gb = pack_groups(b, b_mn);
+  if (ga + gb <= 0) return hipSuccess;
+  if (ga + gb > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(f6_pack_two, dim3((unsigned)(ga + gb)), dim3(256), 0, s, a, b, (int)a_mn, (int)b_mn, (int)ga);
   return hipGetLastError();
 }
 

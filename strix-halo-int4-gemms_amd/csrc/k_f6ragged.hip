@@ -1,0 +1,167 @@
+// Ragged forward and K-ragged backward on the fp6 engine (shk_f6.h).
+//
+// Both convert their int4 operands into fp6 blocks in a caller workspace
+// first (one f6_pack_two launch for both operands), then run the 256 x 256
+// fp6 tile over the converted blocks.  The conversion absorbs the operand
+// layouts, so one GEMM kernel per output mode serves every layout.
+//
+// Forward (ragged.py:1008-1229 semantics): out[rows of group g] =
+// lhs[rows] @ rhs[g].  Workgroup (task, tn) takes the task's 256 rows from
+// block_start (a multiple of 32: the task list is built with align_tile a
+// multiple of 32) against group g's 256-column tile tn, and writes rows
+// [actual_start, actual_end) and columns below N.  K is zero-padded to Kw,
+// a multiple of 128.  Workspace: A as round32(M) rows x Kw, then per group
+// B as round32(N) rows x Kw.
+//
+// Backward (ragged.py:1232-1402 semantics): out[g] = lhs[g] @ rhs[g] over
+// the first group_sizes[g] K values.  The conversion zeroes K at and past
+// that length, so group g runs ceil(len / 128) whole 128-K stages.
+// Workspace: per group A (round32(M) rows x Kw), then per group B
+// (round32(N) rows x Kw), Kw = K capacity rounded up to 128.
+#include "shk_table.h"
+
+namespace shk {
+namespace {
+
+// 256 A rows x 256 B rows, 2 x 2 waves, plain epilogue.
+using F6R = Cfg<4, true, true, 256, 256, 128, 2, 2, false, false, 64, false, 0>;
+constexpr int kTile = 256;
+
+__host__ __device__ inline int round32(int x) { return (x + 31) & ~31; }
+__host__ __device__ inline int round128(int x) { return (x + 127) & ~127; }
+
+template <int MODE>
+__global__ __launch_bounds__(256) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
+  using E = F6Engine<F6R>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  const int tiles_n = (p.N + kTile - 1) / kTile;
+  const int task = blockIdx.x / tiles_n;
+  const int tn = blockIdx.x - task * tiles_n;
+  const int ntasks = *p.num_tasks;
+  // A task list that overflowed its capacity is refused as a whole.
+  if (ntasks > p.capacity || task >= ntasks) return;
+  const int4 t = *reinterpret_cast<const int4*>(p.tasks + 4 * task);
+  const int g = t.x, m0 = t.y;
+  const int kw = round128(p.K);
+  const unsigned long long a_bytes = f6_operand_bytes(round32(p.M), kw);
+  const unsigned long long b_bytes = f6_operand_bytes(round32(p.N), kw);
+  E e;
+  e.setup(smem, p.work, p.work + a_bytes + (unsigned long long)g * b_bytes, m0, tn, kw / 64, a_bytes, b_bytes);
+  float sa[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + e.out_row(i);
+    sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + (m < p.M ? m : p.M - 1));
+  }
+  e.run(kw / 128);
+  const OutView o{p.out, p.b_scale + (long)g * p.N, p.N, p.M, p.N, t.z, t.w, p.N};
+  mfma32_finish<F6R, MODE, EPI_NONE, true>(e, o, smem, m0, tn * kTile, sa);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
+  using E = F6Engine<F6R>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  const int tiles_m = (p.M + kTile - 1) / kTile;
+  const int tiles_n = (p.N + kTile - 1) / kTile;
+  const int per_group = tiles_m * tiles_n;
+  const int g = blockIdx.x / per_group;
+  const int tile = blockIdx.x - g * per_group;
+  const int tm = tile / tiles_n;
+  const int tn = tile - tm * tiles_n;
+  const int m0 = tm * kTile;
+  const int kw = round128(p.k_cap);
+  int len = p.group_sizes[g];
+  len = len < 0 ? 0 : (len > p.k_cap ? p.k_cap : len);
+  const unsigned long long a_bytes = f6_operand_bytes(round32(p.M), kw);
+  const unsigned long long b_bytes = f6_operand_bytes(round32(p.N), kw);
+  const uint8_t* a6 = p.work + (unsigned long long)g * a_bytes;
+  const uint8_t* b6 = p.work + (unsigned long long)p.groups * a_bytes + (unsigned long long)g * b_bytes;
+  E e;
+  e.setup(smem, a6, b6, m0, tn, kw / 64, a_bytes, b_bytes);
+  const uint16_t* sa_g = p.a_scale + (long)g * p.M;
+  float sa[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + e.out_row(i);
+    sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(sa_g + (m < p.M ? m : p.M - 1));
+  }
+  e.run((len + 127) / 128);
+  const OutView o{static_cast<float*>(p.out) + (long)g * p.M * p.N, p.b_scale + (long)g * p.N, p.N, p.M, p.N, 0,
+                  p.M, p.N};
+  mfma32_finish<F6R, MODE, EPI_NONE, true>(e, o, smem, m0, tn * kTile, sa);
+}
+
+bool lhs_mn_major(int layout) { return layout == SHK_LAYOUT_TN || layout == SHK_LAYOUT_TT; }
+bool rhs_mn_major(int layout) { return layout == SHK_LAYOUT_NN || layout == SHK_LAYOUT_TN; }
+// Whether 16-byte source pieces are aligned: base and row pitch (the
+// pitch of an MN-major source is its row count); each operand of a batch
+// starts K/2 * rows bytes after the previous one, a multiple of the pitch.
+int vec16(const uint8_t* src, long ld) { return ((reinterpret_cast<uintptr_t>(src) | (uintptr_t)ld) & 15) == 0; }
+
+hipError_t launch_f6_ragged_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
+  const int kw = round128(a.K);
+  const unsigned long long a_bytes = f6_operand_bytes(round32(a.M), kw);
+  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, vec16(a.lhs, a.lda)};
+  const F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
+                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, vec16(a.rhs, a.ldb)};
+  hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
+  if (err != hipSuccess) return err;
+  if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_fwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);
+  else if (a.out_mode == OUT_F32) hipLaunchKernelGGL(f6_ragged_fwd_kernel<OUT_F32>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(f6_ragged_fwd_kernel<OUT_BF16>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
+  const int kw = round128(a.k_cap);
+  const unsigned long long a_group = f6_operand_bytes(round32(a.M), kw);
+  const long kp = a.k_cap / 2;
+  const F6PackArgs pa{a.lhs,     a.work,  a.lda,         a.M,    kw / 64, 0, a.groups, kp * a.M, a_group,
+                      a.group_sizes, a.k_cap, vec16(a.lhs, a.lda)};
+  const F6PackArgs pb{a.rhs,
+                      a.work + (unsigned long long)a.groups * a_group,
+                      a.ldb,
+                      a.N,
+                      kw / 64,
+                      0,
+                      a.groups,
+                      kp * a.N,
+                      f6_operand_bytes(round32(a.N), kw),
+                      a.group_sizes,
+                      a.k_cap,
+                      vec16(a.rhs, a.ldb)};
+  hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
+  if (err != hipSuccess) return err;
+  if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_F32>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+shk_kernel_desc f6_ragged_desc(int family, int layout) {
+  shk_kernel_desc d = desc_of<F6R>(family, layout, 1);
+  d.num_stages = F6Engine<F6R>::P;
+  d.lds_bytes = F6Engine<F6R>::LDS_BYTES;
+  d.operand_format = SHK_OPERANDS_FP6;
+  return d;
+}
+
+}  // namespace
+
+Entry f6_ragged_fwd_entry(int layout) {
+  return Entry{f6_ragged_desc(SHK_FAMILY_RAGGED_FWD, layout), nullptr, &launch_f6_ragged_fwd, nullptr, nullptr};
+}
+Entry f6_ragged_bwd_entry(int layout) {
+  return Entry{f6_ragged_desc(SHK_FAMILY_RAGGED_BWD, layout), nullptr, nullptr, &launch_f6_ragged_bwd, nullptr};
+}
+
+unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups) {
+  const int kw = round128(k);
+  return f6_operand_bytes(round32(m), kw) + (unsigned long long)groups * f6_operand_bytes(round32(n), kw);
+}
+unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups) {
+  const int kw = round128(k_cap);
+  return (unsigned long long)groups * (f6_operand_bytes(round32(m), kw) + f6_operand_bytes(round32(n), kw));
+}
+
+}  // namespace shk

@@ -27,10 +27,13 @@ void append_fwd(std::vector<Entry>& t) {
   t.push_back(fwd_entry<C<128, 128, 128, 2, 2, SUBCH, MK>>(kLayout));
 }
 
+// The fp6 entries (k_f6ragged.hip) lead each family.
 void append_all(std::vector<Entry>& t) {
+  t.push_back(f6_ragged_fwd_entry(kLayout));
   append_fwd<false, 64>(t);
   append_fwd<true, 64>(t);
   append_fwd<true, 32>(t);
+  t.push_back(f6_ragged_bwd_entry(kLayout));
   t.push_back(bwd_entry<C<128, 128, 128, 2, 2, false, 64>>(kLayout));
   t.push_back(bwd_entry<C<128, 128, 128, 2, 2, true, 64>>(kLayout));
   t.push_back(bwd_entry<C<128, 128, 128, 2, 2, true, 32>>(kLayout));

@@ -61,14 +61,31 @@ __host__ __device__ constexpr unsigned long long f6_operand_bytes(long rows, lon
   return (unsigned long long)rows * (unsigned long long)k * 3ull / 4ull;
 }
 
+// One operand, or a batch of `groups` operands of the same shape (the
+// ragged path's per-expert matrices).  Rows past `rows` convert as zeros up
+// to the next 32-row panel.  K values at or past the operand's length
+// (min(k_len[g], k_cap), or k_cap without k_len) convert as zeros, and 64-K
+// blocks past the last 128-K stage that holds any K of that length are not
+// written (no GEMM reads them).  Sources are read in 16-byte pieces when
+// `vec` says they are aligned to them (base, row pitch and, MN-major, rows),
+// byte by byte otherwise.
 struct F6PackArgs {
   const uint8_t* src;
   uint8_t* dst;
-  long ld;       // bytes between consecutive source rows
-  int rows;      // packed rows (a multiple of 256)
-  int kb;        // K / 64: blocks per panel
-  int swiglu_n;  // > 0: SwiGLU B with N output columns (rows interleave up and gate)
+  long ld;                      // bytes between consecutive source rows
+  int rows;                     // packed rows of one operand
+  int kb;                       // 64-K blocks per panel
+  int swiglu_n;                 // > 0: SwiGLU B with N output columns (rows interleave up and gate)
+  int groups;                   // operands in the batch (1 for a dense call)
+  long src_group;               // source bytes between consecutive operands
+  unsigned long long dst_group; // block bytes between consecutive operands
+  const int32_t* k_len;         // per-operand logical K length, or null
+  int k_cap;                    // K length without k_len; the upper clamp of k_len
+  int vec;                      // 16-byte source pieces are aligned
 };
+
+// 32-row panels of an operand with `rows` rows.
+__host__ __device__ constexpr int f6_panels(int rows) { return (rows + 31) / 32; }
 
 // Converts one operand into block format (k_f6pack.hip).  mn_major: the
 // source is stored K-row by K-row (two K values per byte of every row).
@@ -314,6 +331,27 @@ __device__ __forceinline__ float f6_bf16_at(const uint2& w, int t) {
   return t == 0 ? f6_bf16_lo(w.x) : t == 1 ? f6_bf16_hi(w.x) : t == 2 ? f6_bf16_lo(w.y) : f6_bf16_hi(w.y);
 }
 
+// Where the epilogue of a 32x32 engine writes.  Element (r, c) of the
+// output is at out + r * ld + c (elements); B scale of column c at
+// b_scale[c], the SwiGLU gate's at b_scale[n + c].  A dense tile is written
+// whole; with MASK (the ragged kernels) only rows [row_lo, row_hi) and
+// columns below col_hi are, and B scales of columns at or past col_hi are
+// not read.
+struct OutView {
+  void* out;
+  const uint16_t* b_scale;
+  int ld;    // elements between output rows
+  int rows;  // rows of the output (the range of its stores)
+  int n;     // output columns (SwiGLU: the gate's offset)
+  int row_lo, row_hi, col_hi;
+};
+
+// The view of a dense call: [M, N] (int32 SwiGLU: [M, 2N], up then gate).
+template <class C, int MODE>
+__device__ __forceinline__ OutView dense_view(const DenseArgs& p) {
+  return OutView{p.out, p.b_scale, (MODE == OUT_I32 && C::SWIGLU) ? 2 * p.N : p.N, p.M, p.N, 0, p.M, p.N};
+}
+
 // Writes a wave's results: lane l writes output row out_row(i) and, per
 // register group q, the four columns out_col(j, q) + [0, 4) (for SwiGLU from
 // accumulator j and its gate partner j + 2).
@@ -322,15 +360,22 @@ __device__ __forceinline__ float f6_bf16_at(const uint2& w, int t) {
 //    fp32 or bf16 (NO_NAN: no value is NaN, so the hardware conversion,
 //    which does not canonicalize NaN, may be used).
 // sb[j][q]: the four bf16 B scales of those columns (j >= FN: the gate's).
-template <class C, int MODE, int EPI, bool NO_NAN, class E>
-__device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int m0, int n0, const float (&sa)[4],
+template <class C, int MODE, int EPI, bool NO_NAN, bool MASK, class E>
+__device__ __forceinline__ void f6_epilogue(const E& e, const OutView& o, int m0, int n0, const float (&sa)[4],
                                             const uint2 (&sb)[4][4]) {
   constexpr uint32_t ESZ = MODE == OUT_BF16 ? 2 : 4;
-  const uint32_t ldo = (MODE == OUT_I32 && C::SWIGLU) ? 2u * (uint32_t)p.N : (uint32_t)p.N;
+  const uint32_t ldo = (uint32_t)o.ld;
   const unsigned long long first = (unsigned long long)m0 * ldo + n0;
-  const rsrc_t r = make_rsrc(static_cast<uint8_t*>(p.out) + first * ESZ,
-                             ((unsigned long long)p.M * ldo - first) * ESZ);
+  const rsrc_t r = make_rsrc(static_cast<uint8_t*>(o.out) + first * ESZ,
+                             ((unsigned long long)o.rows * ldo - first) * ESZ);
   const uint32_t voff = ((uint32_t)e.out_row(0) * ldo + (uint32_t)e.out_col(0, 0)) * ESZ;
+  // rows of this lane inside the written range (MASK)
+  bool row_in[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = m0 + e.out_row(i);
+    row_in[i] = !MASK || (row >= o.row_lo && row < o.row_hi);
+  }
   // column group (j, q) outer, rows i inner: each group's four B scales are
   // unpacked once and die after the group
 #pragma unroll
@@ -338,6 +383,7 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t off = voff + (uint32_t)(32 * j + 8 * q) * ESZ;
+      const bool col_in = !MASK || n0 + e.out_col(j, q) < o.col_hi;
       float su[4], sg[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -347,16 +393,18 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t soff = (uint32_t)(32 * i) * ldo * ESZ;
+        const bool in = !MASK || (row_in[i] && col_in);
         if constexpr (MODE == OUT_I32) {
-          __builtin_amdgcn_raw_buffer_store_b128(
-              v4i{e.acc_int(i, j, 4 * q), e.acc_int(i, j, 4 * q + 1), e.acc_int(i, j, 4 * q + 2),
-                  e.acc_int(i, j, 4 * q + 3)},
-              r, off, soff, 0);
+          if (in)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                v4i{e.acc_int(i, j, 4 * q), e.acc_int(i, j, 4 * q + 1), e.acc_int(i, j, 4 * q + 2),
+                    e.acc_int(i, j, 4 * q + 3)},
+                r, off, soff, 0);
           if constexpr (C::SWIGLU) {
             __builtin_amdgcn_raw_buffer_store_b128(
                 v4i{e.acc_int(i, j + 2, 4 * q), e.acc_int(i, j + 2, 4 * q + 1), e.acc_int(i, j + 2, 4 * q + 2),
                     e.acc_int(i, j + 2, 4 * q + 3)},
-                r, off + (uint32_t)p.N * ESZ, soff, 0);
+                r, off + (uint32_t)o.n * ESZ, soff, 0);
           }
         } else {
           float v[4];
@@ -382,11 +430,12 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int 
               lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
               hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
             }
-            __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)lo, (int)hi}, r, off, soff, 0);
+            if (in) __builtin_amdgcn_raw_buffer_store_b64(v2i{(int)lo, (int)hi}, r, off, soff, 0);
           } else {
-            __builtin_amdgcn_raw_buffer_store_b128(
-                v4i{__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]), __float_as_int(v[3])}, r,
-                off, soff, 0);
+            if (in)
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  v4i{__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]), __float_as_int(v[3])}, r,
+                  off, soff, 0);
           }
         }
       }
@@ -406,8 +455,8 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const DenseArgs& p, int 
 //  * 64 columns, SwiGLU (PITCH 128, 8 units): swz(r) = (r / 2) % 8.
 // Both keep the writes (lanes 0-15 hold rows r .. r+15 of one unit) and the
 // reads (16 lanes hold one or two whole rows) free of bank conflicts.
-template <class C, int EPI, bool NO_NAN, class E>
-__device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const DenseArgs& p, uint8_t* smem, int m0, int n0,
+template <class C, int EPI, bool NO_NAN, bool MASK, class E>
+__device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                                     const float (&sa)[4], const uint2 (&sb)[4][4]) {
   constexpr int UNITS = E::TN / 8;
   constexpr int PITCH = 16 * UNITS;
@@ -459,31 +508,38 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const DenseArgs&
     }
   }
   // read back 64 / UNITS rows per instruction and store whole row segments
-  const unsigned long long first = (unsigned long long)m0 * p.N + n0;
-  const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(p.out) + first * 2, ((unsigned long long)p.M * p.N - first) * 2);
+  const uint32_t ldo = (uint32_t)o.ld;
+  const unsigned long long first = (unsigned long long)m0 * ldo + n0;
+  const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(o.out) + first * 2, ((unsigned long long)o.rows * ldo - first) * 2);
   constexpr int ROWS = 64 / UNITS;
   const int rr = lane / UNITS, u = lane % UNITS;
-  const uint32_t voff = ((uint32_t)(e.wm * 128 + rr) * (uint32_t)p.N + (uint32_t)(e.wn * E::TN + 8 * u)) * 2u;
+  const uint32_t voff = ((uint32_t)(e.wm * 128 + rr) * ldo + (uint32_t)(e.wn * E::TN + 8 * u)) * 2u;
+  const bool col_in = !MASK || n0 + e.wn * E::TN + 8 * u < o.col_hi;
 #pragma unroll
   for (int t = 0; t < 128 / ROWS; ++t) {
     const int r = ROWS * t + rr;
     const uint4 x = *reinterpret_cast<const uint4*>(region + r * PITCH + 16 * (u ^ swz(r)));
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff,
-                                           (uint32_t)(ROWS * t) * (uint32_t)p.N * 2u, 0);
+    const int row = m0 + e.wm * 128 + r;
+    if (!MASK || (col_in && row >= o.row_lo && row < o.row_hi))
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(ROWS * t) * ldo * 2u,
+                                             0);
   }
 }
 
 // B scales of the wave's columns (bf16, four per load): [j][q] for
 // fragment j, register group q; fragments j >= FN read the gate's scales.
-template <class C, class E>
-__device__ __forceinline__ void mfma32_load_b_scales(const E& e, const DenseArgs& p, int n0, uint2 (&sb)[4][4]) {
-  const int gate = C::SWIGLU ? p.N : 0;
+template <class C, bool MASK, class E>
+__device__ __forceinline__ void mfma32_load_b_scales(const E& e, const OutView& o, int n0, uint2 (&sb)[4][4]) {
+  const int gate = C::SWIGLU ? o.n : 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int jj = j < E::FN ? j : j - E::FN;
-      sb[j][q] = *reinterpret_cast<const uint2*>(p.b_scale + (j < E::FN ? 0 : gate) + n0 + e.out_col(jj, q));
+      const int col = n0 + e.out_col(jj, q);
+      sb[j][q] = (!MASK || col < o.col_hi)
+                     ? *reinterpret_cast<const uint2*>(o.b_scale + (j < E::FN ? 0 : gate) + col)
+                     : make_uint2(0u, 0u);
     }
 }
 
@@ -492,20 +548,21 @@ __device__ __forceinline__ void mfma32_load_b_scales(const E& e, const DenseArgs
 // value can be NaN (finite scales times a finite integer give at most
 // +-inf, and ReLU^2 of that is no NaN either; SwiGLU always rounds in
 // software).
-template <class C, int MODE, int EPI, class E>
-__device__ __forceinline__ void mfma32_finish(const E& e, const DenseArgs& p, uint8_t* smem, int m0, int n0,
+template <class C, int MODE, int EPI, bool MASK = false, class E>
+__device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                               const float (&sa)[4]) {
+  static_assert(!(MASK && C::SWIGLU), "masked tiles are plain");
   if constexpr (MODE == OUT_I32) {
     const uint2 none[4][4] = {};
-    f6_epilogue<C, OUT_I32, EPI_NONE, false>(e, p, m0, n0, sa, none);
+    f6_epilogue<C, OUT_I32, EPI_NONE, false, MASK>(e, o, m0, n0, sa, none);
     return;
   }
   uint2 sb[4][4];
-  mfma32_load_b_scales<C>(e, p, n0, sb);
+  mfma32_load_b_scales<C, MASK>(e, o, n0, sb);
   if constexpr (MODE == OUT_F32) {
-    f6_epilogue<C, OUT_F32, EPI, false>(e, p, m0, n0, sa, sb);
+    f6_epilogue<C, OUT_F32, EPI, false, MASK>(e, o, m0, n0, sa, sb);
   } else if constexpr (C::SWIGLU) {
-    mfma32_epilogue_lds<C, EPI_NONE, false>(e, p, smem, m0, n0, sa, sb);
+    mfma32_epilogue_lds<C, EPI_NONE, false, MASK>(e, o, smem, m0, n0, sa, sb);
   } else {
     bool finite = true;
 #pragma unroll
@@ -518,8 +575,8 @@ __device__ __forceinline__ void mfma32_finish(const E& e, const DenseArgs& p, ui
         finite = finite && (w.x & 0x7F80u) != 0x7F80u && (w.x & 0x7F800000u) != 0x7F800000u &&
                  (w.y & 0x7F80u) != 0x7F80u && (w.y & 0x7F800000u) != 0x7F800000u;
       }
-    if (__all(finite)) mfma32_epilogue_lds<C, EPI, true>(e, p, smem, m0, n0, sa, sb);
-    else mfma32_epilogue_lds<C, EPI, false>(e, p, smem, m0, n0, sa, sb);
+    if (__all(finite)) mfma32_epilogue_lds<C, EPI, true, MASK>(e, o, smem, m0, n0, sa, sb);
+    else mfma32_epilogue_lds<C, EPI, false, MASK>(e, o, smem, m0, n0, sa, sb);
   }
 }
 
@@ -541,7 +598,7 @@ __global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
   e.run(p.K / 128);
-  mfma32_finish<C, MODE, EPI>(e, p, smem, m0, n0, sa);
+  mfma32_finish<C, MODE, EPI>(e, dense_view<C, MODE>(p), smem, m0, n0, sa);
 }
 
 }  // namespace shk

@@ -394,6 +394,8 @@ struct RaggedFwdArgs {
   int subchannel, scale_cols;
   int out_mode;
   int a_aligned, b_aligned, out_vec;
+  int layout;     // SHK_LAYOUT_* (fp6 entries convert either layout)
+  uint8_t* work;  // fp6 entries: operand workspace
 };
 
 template <class C>
@@ -519,6 +521,8 @@ struct RaggedBwdArgs {
   int split_k;
   int out_mode;            // OUT_F32, or OUT_I32 raw
   int a_aligned, b_aligned, out_vec;
+  int layout;              // SHK_LAYOUT_* (fp6 entries convert either layout)
+  uint8_t* work;           // fp6 entries: operand workspace
 };
 
 template <class C>

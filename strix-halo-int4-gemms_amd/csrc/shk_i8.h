@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const DenseArgs p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
   e.run(p.K / 64);
-  mfma32_finish<C, MODE, EPI>(e, p, smem, m0, n0, sa);
+  mfma32_finish<C, MODE, EPI>(e, dense_view<C, MODE>(p), smem, m0, n0, sa);
 }
 
 }  // namespace shk

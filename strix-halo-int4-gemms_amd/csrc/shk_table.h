@@ -33,8 +33,10 @@ hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
 // then reads both parts.
 inline F6PackArgs f6_pack_args(const DenseArgs& a, int operand, bool swiglu) {
   const int kb = a.K / 64;
-  if (operand == 0) return F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0};
-  return F6PackArgs{a.b, a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0};
+  // dense operands are validated 16-byte aligned
+  if (operand == 0) return F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0, 1, 0, 0, nullptr, a.K, 1};
+  return F6PackArgs{a.b,    a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0, 1, 0, 0,
+                    nullptr, a.K, 1};
 }
 inline bool f6_mn_major(const DenseArgs& a, int operand) {
   return operand == 0 ? a.layout == SHK_LAYOUT_TN : a.layout != SHK_LAYOUT_NT;
@@ -165,6 +167,13 @@ void append_ragged_1(std::vector<Entry>& t);
 void append_ragged_2(std::vector<Entry>& t);
 void append_ragged_3(std::vector<Entry>& t);
 int max_info_groups();
+// fp6 ragged entries of one layout (k_f6ragged.hip): the forward (task
+// tile 256) and the K-ragged backward, both per-channel.
+Entry f6_ragged_fwd_entry(int layout);
+Entry f6_ragged_bwd_entry(int layout);
+// Workspace bytes of the fp6 ragged paths.
+unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups);
+unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups);
 
 // Non-table kernels (ragged.hip).
 hipError_t launch_group_info(const int32_t* sizes, int groups, int tile, int align, int capacity,

@@ -235,3 +235,85 @@ def test_split_fp6_phases_validate_their_arguments(lib):
     assert "does not match the kernel's epilogue kind" in _err(lib)
     assert gemm(fp6, 0, 0, FAKE, FAKE, None, 256, 256, 128, 0, 0, FAKE, 1 << 20) == 1
     assert "a_scale, b_scale, and out pointers must be non-null" in _err(lib)
+
+
+def _ragged_f6(family, layout=kt.LAYOUT_NN):
+    return next(d for d in kt.entries(family) if d.layout == layout and d.operand_format == kt.OPERANDS_FP6)
+
+
+def _ragged_ws(lib, index, m, n, k_packed, groups):
+    out = ctypes.c_uint64(0)
+    rc = lib.amd_strix_halo_kernels_ragged_workspace_bytes(index, m, n, k_packed, groups, ctypes.byref(out))
+    return rc, int(out.value)
+
+
+def test_fp6_ragged_entries_report_their_workspace(lib):
+    for family in (kt.FAMILY_RAGGED_FWD, kt.FAMILY_RAGGED_BWD):
+        fp6 = [d for d in kt.entries(family) if d.operand_format == kt.OPERANDS_FP6]
+        assert sorted(d.layout for d in fp6) == [kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN, kt.LAYOUT_TT]
+        for d in fp6:
+            assert d.scale_mode == kt.SCALE_PER_CHANNEL and d.block_m == 256 and d.lds_bytes == 147456
+            for m, n, kp, g in ((8192, 1408, 1024, 8), (17, 24, 32, 3), (2048, 1408, 1001, 8), (1, 8, 1, 1)):
+                kw = -(-2 * kp // 128) * 128
+                m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
+                if family == kt.FAMILY_RAGGED_FWD:
+                    want = (m32 * kw + g * n32 * kw) * 3 // 4
+                else:
+                    want = g * (m32 * kw + n32 * kw) * 3 // 4
+                assert _ragged_ws(lib, d.index, m, n, kp, g) == (0, want)
+                assert d.ragged_workspace_bytes(m, n, kp, g) == want
+    packed = next(d for d in kt.entries(kt.FAMILY_RAGGED_FWD) if not d.needs_workspace)
+    assert _ragged_ws(lib, packed.index, 8192, 1408, 1024, 8) == (0, 0)
+    dense = kt.entries(kt.FAMILY_DENSE)[0].index
+    assert _ragged_ws(lib, dense, 16, 16, 16, 1)[0] == 1
+    assert "not a ragged kernel" in _err(lib)
+
+
+def test_fp6_ragged_launch_validation(lib):
+    fwd = _ragged_f6(kt.FAMILY_RAGGED_FWD).index
+    F = lib.amd_strix_halo_kernels_launch_ragged_fwd
+    FW = lib.amd_strix_halo_kernels_launch_ragged_fwd_ws
+    # 64 x 16 x 64 (k_packed 32), 2 groups: A 64 x 128 + 2 x (32 x 128) in fp6
+    need = (64 * 128 + 2 * 32 * 128) * 3 // 4
+    assert F(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 32, 2, 0, 0) == 1
+    assert f"workspace of {need} bytes" in _err(lib)
+    args = (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 32, 2, 0, 0)
+    assert FW(fwd, 0, 0, *args, FAKE, need - 1) == 1
+    assert f"workspace of {need} bytes" in _err(lib)
+    assert FW(fwd, 0, 0, *args, FAKE + 4, need + 4) == 1
+    assert "16-byte aligned" in _err(lib)
+    assert FW(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 12, 32, 2, 0, 0, FAKE, 1 << 30) == 1
+    assert "N to be a multiple of 8" in _err(lib)
+    assert FW(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE + 8, 64, 16, 32, 2, 0, 0, FAKE, 1 << 30) == 1
+    assert "out must be 16-byte aligned" in _err(lib)
+    assert FW(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, kt.FP6_MAX_K // 2 + 64, 2, 0, 0,
+              FAKE, 1 << 40) == 1
+    assert "K <= 262144" in _err(lib)
+    bwd = _ragged_f6(kt.FAMILY_RAGGED_BWD, kt.LAYOUT_TN).index
+    B = lib.amd_strix_halo_kernels_launch_ragged_bwd
+    BW = lib.amd_strix_halo_kernels_launch_ragged_bwd_ws
+    # 3 groups of 48 x 16 with K capacity 39 (k_packed 20 -> 128)
+    need = 3 * (64 * 128 + 32 * 128) * 3 // 4
+    assert B(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 0, 2, kt.OUT_F32) == 1
+    assert f"workspace of {need} bytes" in _err(lib)
+    assert BW(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 0, 1, kt.OUT_BF16, FAKE, need) == 1
+    assert "fp32" in _err(lib)
+    assert BW(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 64, 1, kt.OUT_F32, FAKE, need) == 1
+    assert "subchannel = 0" in _err(lib)
+    # nothing to run: no workspace needed
+    assert BW(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 0, 0, 1, kt.OUT_F32, None, 0) == 0
+
+
+def test_fp6_ragged_eligibility():
+    fwd, bwd = kt.FAMILY_RAGGED_FWD, kt.FAMILY_RAGGED_BWD
+    assert kt.ragged_fp6_eligible(fwd, subchannel=None, m=8192, n=1408, k_packed=1024)
+    assert kt.ragged_fp6_eligible(bwd, subchannel=None, m=2048, n=1408, k_packed=1001)
+    assert kt.ragged_fp6_eligible(fwd, subchannel=None, m=17, n=24, k_packed=32)
+    assert not kt.ragged_fp6_eligible(fwd, subchannel=32, m=8192, n=1408, k_packed=1024)
+    assert not kt.ragged_fp6_eligible(bwd, subchannel=None, m=16, n=20, k_packed=16)
+    assert not kt.ragged_fp6_eligible(fwd, subchannel=None, m=16, n=16, k_packed=kt.FP6_MAX_K // 2 + 1)
+    with pytest.raises(LookupError):
+        kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True)
+    assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=None, fp6=True).block_m == kt.RAGGED_FP6_BLOCK_M
+    assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=None).operand_format == kt.OPERANDS_PACKED
+    assert kt.RAGGED_FP6_BLOCK_M not in kt.RAGGED_FWD_BLOCK_M

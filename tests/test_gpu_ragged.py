@@ -159,6 +159,68 @@ def test_ragged_fwd_even_k_and_larger(scale, device):
         assert np.array_equal(bf16_bits(torch, out), ref.bf16_round(want))
 
 
+# fp6 forward (k_f6ragged.hip): every layout and output mode, through the
+# native entry (block_m 256), on shapes that exercise the row and column
+# masks, K padded to 128 and the byte-wise operand loads (K/2 or M not a
+# multiple of 16)
+FP6_FWD_SHAPES = [(17, 64, 24, [5, 0, 12]), (300, 200, 40, [100, 0, 37, 163]),
+                  (640, 384, 264, [1, 300, 0, 339]), (96, 256, 8, [96])]
+
+
+def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode):
+    from amd_strix_halo_kernels import kernel_table as kt
+    from amd_strix_halo_kernels import native
+    lhs, rhs = _pack_fwd(a_q, b_q, layout)
+    m, n = a_q.shape[0], b_q.shape[2]
+    dt = {kt.OUT_BF16: torch.bfloat16, kt.OUT_F32: torch.float32, kt.OUT_I32: torch.int32}[out_mode]
+    out = torch.full((m, n), 7, dtype=dt, device=device)
+    native.launch_ragged_fwd(
+        to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
+        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), out=out, layout=layout, subchannel=None,
+        block_m=block_m, align_tile=32 if block_m == 256 else 8, rows=m, cols=n, k_packed=a_q.shape[1] // 2,
+        out_mode=out_mode)
+    torch.cuda.synchronize()
+    return out
+
+
+def _ragged_int_reference(a_q, b_q, sizes):
+    out = np.zeros((a_q.shape[0], b_q.shape[2]), dtype=np.int64)
+    start = 0
+    for g, size in enumerate(sizes):
+        out[start:start + size] = ref.int_matmul(a_q[start:start + size], b_q[g])
+        start += size
+    return out
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("shape", FP6_FWD_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}x{s[2]}")
+def test_ragged_fwd_fp6_all_layouts_and_modes(layout, shape, device):
+    from amd_strix_halo_kernels import kernel_table as kt
+    m, k, n, sizes = shape
+    a_q, b_q, sa, sb = _fwd_case(stable_seed("fp6fwd", layout.value, m), m, k, n, sizes, SCALES[0])
+    print(f"case fp6 fwd {layout.value} {shape}", flush=True)
+    want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb)
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, 256, kt.OUT_F32)
+    assert np.array_equal(got.cpu().numpy(), want)
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, 256, kt.OUT_BF16)
+    assert np.array_equal(bf16_bits(torch, got), ref.bf16_round(want))
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, 256, kt.OUT_I32)
+    assert np.array_equal(got.cpu().numpy().astype(np.int64), _ragged_int_reference(a_q, b_q, sizes))
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128])
+def test_ragged_fwd_packed_per_channel_kernels(layout, block_m, device):
+    """The int8-MFMA forward kernels, which the API uses for shapes the fp6
+    entry does not take, on the fp6 shapes."""
+    from amd_strix_halo_kernels import kernel_table as kt
+    m, k, n, sizes = FP6_FWD_SHAPES[1]
+    a_q, b_q, sa, sb = _fwd_case(stable_seed("pkfwd", layout.value, block_m), m, k, n, sizes, SCALES[0])
+    want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb)
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, kt.OUT_F32)
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
 def test_config_c5_forward_full(device):
     """C5: G=8, M=8192, K=2048, N=1408, multinomial group sizes with an empty group."""
     r = ref.rng(5)
@@ -243,6 +305,37 @@ def test_ragged_bwd_multi_stage(scale, split_k, device):
     got = _run_bwd(device, a_q, b_q, sizes, sa, sb, scale, shk.GemmLayout.NN, split_k)
     want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=scale.subchannel_size)
     _check_bwd(got, want, scale, split_k)
+
+
+# fp6 backward: every layout, odd and tile-crossing K capacities with
+# random values past each group's length, empty and one-row groups, M and N
+# not multiples of 32
+FP6_BWD_SHAPES = [(3, 48, 39, 24, [5, 0, 37]), (5, 200, 1024, 136, [700, 0, 1, 1023, 512]),
+                  (2, 264, 300, 40, [300, 129])]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("shape", FP6_BWD_SHAPES, ids=lambda s: f"g{s[0]}_{s[1]}x{s[2]}x{s[3]}")
+def test_ragged_bwd_fp6_all_layouts(layout, shape, device):
+    from amd_strix_halo_kernels import kernel_table as kt
+    from amd_strix_halo_kernels import native
+    groups, m, kcap, n, sizes = shape
+    a_q, b_q, sa, sb = _bwd_case(stable_seed("fp6bwd", layout.value, m), groups, m, kcap, n, SCALES[0])
+    print(f"case fp6 bwd {layout.value} {shape}", flush=True)
+    want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb)
+    for split_k in (1, 2):  # the fp6 entry computes each output whole either way
+        got = _run_bwd(device, a_q, b_q, sizes, sa, sb, SCALES[0], layout, split_k)
+        assert np.array_equal(got, want)
+    lhs, rhs = _pack_bwd(a_q, b_q, layout)
+    raw = torch.full((groups, m, n), 7, dtype=torch.int32, device=device)
+    native.launch_ragged_bwd(
+        to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
+        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), out=raw, layout=layout, subchannel=None,
+        split_k=1, rows=m, cols=n, k_packed=lhs.shape[-1] if layout in (shk.GemmLayout.NN, shk.GemmLayout.NT)
+        else lhs.shape[1], out_mode=kt.OUT_I32, fp6=True)
+    torch.cuda.synchronize()
+    want_i = np.stack([ref.int_matmul(a_q[g][:, :sizes[g]], b_q[g][:sizes[g]]) for g in range(groups)])
+    assert np.array_equal(raw.cpu().numpy().astype(np.int64), want_i)
 
 
 def test_config_c5_backward_full(device):
