@@ -49,8 +49,17 @@ __device__ __forceinline__ int f6_k_len(const F6PackArgs& p, int g) {
   const int l = p.k_len[g];
   return l < 0 ? 0 : (l > p.k_cap ? p.k_cap : l);
 }
-// 16 source bytes read one at a time: byte b exists when b < `valid`.
-__device__ __forceinline__ uint4 f6_load_bytes(const uint8_t* q, int valid) {
+// 16 source bytes of which the first `valid` (>= 1) exist, in pieces of
+// `unit` bytes (16, 8 or 1: the alignment of the source): 16-byte pieces
+// are whole by construction, the second 8-byte half exists when more than
+// 8 bytes do, and single bytes past `valid` are not read.
+__device__ __forceinline__ uint4 f6_load(const uint8_t* q, int unit, int valid) {
+  if (unit == 16) return *reinterpret_cast<const uint4*>(q);
+  if (unit == 8) {
+    const uint2 lo = *reinterpret_cast<const uint2*>(q);
+    const uint2 hi = valid > 8 ? *reinterpret_cast<const uint2*>(q + 8) : make_uint2(0u, 0u);
+    return make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
   uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int b = 0; b < 16; ++b)
@@ -84,7 +93,7 @@ __device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
     const uint8_t* q = p.src + g * p.src_group + (long)row * p.ld + 32L * kb + 16 * (lane >> 5);
     const int keep = len - k0;  // K values of the 32 to keep
     // bytes holding any of them (the source row ends within the length)
-    x = p.vec ? *reinterpret_cast<const uint4*>(q) : f6_load_bytes(q, (keep + 1) / 2);
+    x = f6_load(q, p.vec, (keep + 1) / 2);
     if (keep < 32) {
       uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
@@ -127,7 +136,7 @@ __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_
     uint4 x = make_uint4(0u, 0u, 0u, 0u);
     if (r0 < p.rows && k < len) {
       const uint8_t* q = src + (32L * kb + kp) * p.ld + col;
-      x = p.vec ? *reinterpret_cast<const uint4*>(q) : f6_load_bytes(q, p.rows - r0);
+      x = f6_load(q, p.vec, p.rows - r0);
       if (k + 1 >= len) x = make_uint4(x.x & 0x0F0F0F0Fu, x.y & 0x0F0F0F0Fu, x.z & 0x0F0F0F0Fu, x.w & 0x0F0F0F0Fu);
     }
     const int swz = (kp & 7) | ((kp & 16) >> 1);

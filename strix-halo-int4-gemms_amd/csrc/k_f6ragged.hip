@@ -30,16 +30,29 @@ constexpr int kTile = 256;
 __host__ __device__ inline int round32(int x) { return (x + 31) & ~31; }
 __host__ __device__ inline int round128(int x) { return (x + 127) & ~127; }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup w on XCD
+// w % 8), each with its own L2.  Maps the first `total` workgroup ids onto
+// [0, total) so that XCD x runs one contiguous range, x * q + min(x, r) +
+// [0, q + (x < r)) for total = 8q + r.
+__device__ __forceinline__ int xcd_contiguous(int w, int total) {
+  const int x = w & 7, i = w >> 3, q = total >> 3, r = total & 7;
+  return x * q + (x < r ? x : r) + i;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
   using E = F6Engine<F6R>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
   const int tiles_n = (p.N + kTile - 1) / kTile;
-  const int task = blockIdx.x / tiles_n;
-  const int tn = blockIdx.x - task * tiles_n;
   const int ntasks = *p.num_tasks;
   // A task list that overflowed its capacity is refused as a whole.
-  if (ntasks > p.capacity || task >= ntasks) return;
+  const int live = ntasks * tiles_n;
+  if (ntasks > p.capacity || (int)blockIdx.x >= live) return;
+  // each XCD takes consecutive tasks with all their column tiles: A tiles
+  // are shared by the column tiles and B tiles by the tasks of a group
+  const int w = xcd_contiguous(blockIdx.x, live);
+  const int task = w / tiles_n;
+  const int tn = w - task * tiles_n;
   const int4 t = *reinterpret_cast<const int4*>(p.tasks + 4 * task);
   const int g = t.x, m0 = t.y;
   const int kw = round128(p.K);
@@ -64,11 +77,30 @@ __global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs 
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
   const int tiles_m = (p.M + kTile - 1) / kTile;
   const int tiles_n = (p.N + kTile - 1) / kTile;
-  const int per_group = tiles_m * tiles_n;
-  const int g = blockIdx.x / per_group;
-  const int tile = blockIdx.x - g * per_group;
-  const int tm = tile / tiles_n;
-  const int tn = tile - tm * tiles_n;
+  // Each group's tiles_m x tiles_n grid splits into 8 regions of sm x sn
+  // tile rows and columns, one per XCD, so an XCD reads its A tiles for sn
+  // and its B tiles for sm column / row neighbours from its own L2 and holds
+  // tiles of every group, whatever their lengths.  Grids that split no such
+  // way run in order.
+  int sm = 0, sn = 0;  // region counts along M and N (sm * sn = 8)
+  if (tiles_m % 4 == 0 && tiles_n % 2 == 0) sm = 4, sn = 2;
+  else if (tiles_m % 2 == 0 && tiles_n % 4 == 0) sm = 2, sn = 4;
+  else if (tiles_m % 8 == 0) sm = 8, sn = 1;
+  else if (tiles_n % 8 == 0) sm = 1, sn = 8;
+  int g, tm, tn;
+  if (sm) {
+    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
+    const int bm = tiles_m / sm, bn = tiles_n / sn;  // tiles of a region
+    g = i / (bm * bn);
+    const int local = i - g * (bm * bn);
+    tm = (x / sn) * bm + local / bn;
+    tn = (x % sn) * bn + local % bn;
+  } else {
+    g = blockIdx.x / (tiles_m * tiles_n);
+    const int t = blockIdx.x - g * (tiles_m * tiles_n);
+    tm = t / tiles_n;
+    tn = t - tm * tiles_n;
+  }
   const int m0 = tm * kTile;
   const int kw = round128(p.k_cap);
   int len = p.group_sizes[g];
@@ -94,17 +126,21 @@ __global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs 
 
 bool lhs_mn_major(int layout) { return layout == SHK_LAYOUT_TN || layout == SHK_LAYOUT_TT; }
 bool rhs_mn_major(int layout) { return layout == SHK_LAYOUT_NN || layout == SHK_LAYOUT_TN; }
-// Whether 16-byte source pieces are aligned: base and row pitch (the
-// pitch of an MN-major source is its row count); each operand of a batch
-// starts K/2 * rows bytes after the previous one, a multiple of the pitch.
-int vec16(const uint8_t* src, long ld) { return ((reinterpret_cast<uintptr_t>(src) | (uintptr_t)ld) & 15) == 0; }
+// Source piece size of the conversion: the alignment (16, 8 or 1) of the
+// base and the row pitch (the pitch of an MN-major source is its row
+// count); each operand of a batch starts K/2 * rows bytes after the
+// previous one, a multiple of the pitch.
+int piece_bytes(const uint8_t* src, long ld) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src) | (uintptr_t)ld;
+  return (a & 15) == 0 ? 16 : ((a & 7) == 0 ? 8 : 1);
+}
 
 hipError_t launch_f6_ragged_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
   const int kw = round128(a.K);
   const unsigned long long a_bytes = f6_operand_bytes(round32(a.M), kw);
-  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, vec16(a.lhs, a.lda)};
+  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda)};
   const F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
-                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, vec16(a.rhs, a.ldb)};
+                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb)};
   hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
   if (err != hipSuccess) return err;
   if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_fwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);
@@ -118,7 +154,7 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
   const unsigned long long a_group = f6_operand_bytes(round32(a.M), kw);
   const long kp = a.k_cap / 2;
   const F6PackArgs pa{a.lhs,     a.work,  a.lda,         a.M,    kw / 64, 0, a.groups, kp * a.M, a_group,
-                      a.group_sizes, a.k_cap, vec16(a.lhs, a.lda)};
+                      a.group_sizes, a.k_cap, piece_bytes(a.lhs, a.lda)};
   const F6PackArgs pb{a.rhs,
                       a.work + (unsigned long long)a.groups * a_group,
                       a.ldb,
@@ -130,7 +166,7 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
                       f6_operand_bytes(round32(a.N), kw),
                       a.group_sizes,
                       a.k_cap,
-                      vec16(a.rhs, a.ldb)};
+                      piece_bytes(a.rhs, a.ldb)};
   hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
   if (err != hipSuccess) return err;
   if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);

@@ -66,9 +66,9 @@ __host__ __device__ constexpr unsigned long long f6_operand_bytes(long rows, lon
 // to the next 32-row panel.  K values at or past the operand's length
 // (min(k_len[g], k_cap), or k_cap without k_len) convert as zeros, and 64-K
 // blocks past the last 128-K stage that holds any K of that length are not
-// written (no GEMM reads them).  Sources are read in 16-byte pieces when
-// `vec` says they are aligned to them (base, row pitch and, MN-major, rows),
-// byte by byte otherwise.
+// written (no GEMM reads them).  Sources are read in pieces of `vec` bytes
+// (16, 8 or 1), the alignment of their base and row pitch (MN-major: the
+// pitch is the row count).
 struct F6PackArgs {
   const uint8_t* src;
   uint8_t* dst;
@@ -81,7 +81,7 @@ struct F6PackArgs {
   unsigned long long dst_group; // block bytes between consecutive operands
   const int32_t* k_len;         // per-operand logical K length, or null
   int k_cap;                    // K length without k_len; the upper clamp of k_len
-  int vec;                      // 16-byte source pieces are aligned
+  int vec;                      // source alignment: 16, 8 or 1
 };
 
 // 32-row panels of an operand with `rows` rows.

@@ -34,9 +34,9 @@ hipError_t launch_dense_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
 inline F6PackArgs f6_pack_args(const DenseArgs& a, int operand, bool swiglu) {
   const int kb = a.K / 64;
   // dense operands are validated 16-byte aligned
-  if (operand == 0) return F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0, 1, 0, 0, nullptr, a.K, 1};
+  if (operand == 0) return F6PackArgs{a.a, a.work, a.lda, a.M, kb, 0, 1, 0, 0, nullptr, a.K, 16};
   return F6PackArgs{a.b,    a.work + f6_operand_bytes(a.M, a.K), a.ldb, a.b_cols, kb, swiglu ? a.N : 0, 1, 0, 0,
-                    nullptr, a.K, 1};
+                    nullptr, a.K, 16};
 }
 inline bool f6_mn_major(const DenseArgs& a, int operand) {
   return operand == 0 ? a.layout == SHK_LAYOUT_TN : a.layout != SHK_LAYOUT_NT;
