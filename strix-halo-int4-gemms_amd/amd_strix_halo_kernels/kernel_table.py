@@ -99,12 +99,18 @@ class KernelDesc:
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
-          fp6=False):
+          fp6=False, fp6_sub=False):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
+    # fp6_sub: six stages of 128 + 128 rows x 64 K in fp6 (48 bytes) and a
+    # four-group scale ring of 768 bytes per group (shk_f6sub.h).
     brows = 2 * bn if swiglu else bn
-    if fp6:
+    if fp6_sub:
+        fp6 = True
+        pipe = 6
+        lds = pipe * (bm + bn) * 48 + 4 * 768
+    elif fp6:
         pipe = 3
         lds = pipe * (bm + 256) * 96
     else:
@@ -115,7 +121,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         dtype_bits=bits,
         layout=layout,
         scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
-        min_subchannel=(32 if mk == 32 else 64) if subch else 0,
+        min_subchannel=(128 if fp6_sub else 32 if mk == 32 else 64) if subch else 0,
         max_subchannel=(32 if mk == 32 else 256) if subch else 0,
         epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
         block_m=bm,
@@ -142,6 +148,7 @@ def _build() -> tuple[KernelDesc, ...]:
             if bits == 4:
                 add(**d, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
                 add(**d, bm=256, bn=128, bk=128, wm=2, wn=2, swiglu=True, fp6=True)
+                add(**d, bm=128, bn=128, bk=128, wm=2, wn=2, subch=True, fp6_sub=True)
             add(**d, bm=256, bn=256, bk=big_bk, wm=2, wn=2, pipe=4)
             add(**d, bm=256, bn=128, bk=big_bk, wm=2, wn=2, swiglu=True, pipe=4)
             add(**d, bm=128, bn=128, bk=64, wm=2, wn=2)
@@ -170,6 +177,25 @@ def _build() -> tuple[KernelDesc, ...]:
 
 
 TABLE: tuple[KernelDesc, ...] = _build()
+
+
+def measured_tops(desc: KernelDesc) -> float | None:
+    """Throughput measured on MI355X for the entries the BASELINE configs
+    time (bench.py, one GPU; the whole call including operand conversion),
+    used by the registry's selection like the reference's benchmark TOPS
+    (registry.py:254-352): fp6 int4 per-channel 256x256 (C2, 8192^3), fp6
+    int4 subchannel 128x128 (C3), int8 32x32 SwiGLU 256x128 (C4, 4096 x
+    2*11008 x 4096) and int8 plain 256x256 (8192^3).  Other entries have no
+    measurement and rank by tile area."""
+    if desc.family != FAMILY_DENSE:
+        return None
+    if desc.operand_format == OPERANDS_FP6:
+        if desc.scale_mode == SCALE_SUBCHANNEL:
+            return 1572.0
+        return 3535.0 if desc.epilogue_kind == EPI_KIND_PLAIN else None
+    if desc.dtype_bits == 8 and desc.num_stages == 4 and desc.block_m == 256:
+        return 1994.0 if desc.epilogue_kind == EPI_KIND_SWIGLU else 2270.0
+    return None
 
 
 def entries(family: int) -> tuple[KernelDesc, ...]:

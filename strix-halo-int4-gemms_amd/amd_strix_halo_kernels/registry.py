@@ -95,6 +95,7 @@ def iter_supported_kernel_metadata() -> Iterable[KernelMetadata]:
                     assembly_path=None,
                     status=KernelStatus.COMPILED,
                     table_index=desc.index,
+                    measured_tops=kt.measured_tops(desc),
                 )
 
 

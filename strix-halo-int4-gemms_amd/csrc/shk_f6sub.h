@@ -1,0 +1,425 @@
+// int4 x int4 subchannel GEMM on the fp6 MFMA.
+//
+// out = epilogue(sum over K groups g of (float(A_g @ B_g) * a_scale[m, g]) *
+// b_scale[g, n]), groups of S = 128 or 256 K values, summed in fp32 in group
+// order (api.py:299-325).  The operands are the fp6 blocks of shk_f6.h.
+//
+// Each group's partial products must be scaled on their own, so every S K
+// values the accumulators are folded into fp32 totals with VALU work; that
+// fold, not the MFMA, bounds this kernel.  The design keeps it at four VALU
+// operations per value and lets other waves' MFMAs run meanwhile:
+//  * the MFMA is the scaled form (v_mfma_scale_f32_32x32x64_f8f6f4) with a
+//    scale of 2^3 on both v/8 operands, so the accumulators hold the exact
+//    integer partial sums (no x64 pass), and the first MFMA of a group takes
+//    0 as its C operand (no clearing pass);
+//  * a wave owns 64 x 64 outputs (4 accumulators of 32 x 32 and 64 fp32
+//    totals), so a wave stays within 256 registers and two 4-wave
+//    workgroups of 128 x 128 share a CU: while one wave folds, the other
+//    wave on its SIMD issues MFMAs;
+//  * the scales reach LDS by LDS-DMA in the same stream as the operands,
+//    so no load the compiler tracks sits in the K loop.
+//
+// Pipeline: 64-K stages (one 32 x 64 fp6 block per 32-row panel; 6 KiB of
+// A and 6 KiB of B) in a ring of six slots.  Stage k: wait for this wave's
+// DMA of stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
+// carrying the 8 LDS reads of stage k+1's fragments and the 4 DMA loads of
+// stage k+6 into slot k % 6 (3 operand loads and one scale load per wave);
+// then a fence that waits for this stage's LDS reads with every fragment
+// register of the other set as an operand, so no compiler copy of a
+// fragment can precede its data.
+//
+// Scales of group g sit in slot g % 4 of a small ring: the a_scale dword
+// holding row r's scale (dword-aligned pair (e & ~1, e | 1) of e = row * G +
+// g) at 4 r, and the 128 b_scale values at 512.  Every stage loads the
+// scales of the group of the stage it loads (duplicates rewrite the same
+// bytes), 5 stages before that group's first stage; the ring slot of
+// group g is next written for group g+4, after g has been folded.
+#pragma once
+
+#include "shk_f6.h"
+
+namespace shk {
+
+template <class C, int SPG>
+struct F6SubEngine {
+  static constexpr int P = 6;                       // ring slots
+  static constexpr int NW = 4;
+  static constexpr int OPB = 4 * F6_BLOCK;          // 128 rows x 64 K: 6 KiB
+  static constexpr int STAGE = 2 * OPB;             // 12 KiB
+  static constexpr int RING = P * STAGE;            // 72 KiB
+  static constexpr int SCALE_SLOT = 768;            // 128 a dwords + 128 b halves
+  static constexpr int LDS_BYTES = RING + 4 * SCALE_SLOT;
+  static constexpr int OPW = STAGE / 1024 / NW;     // 3 operand loads per wave per stage
+  static constexpr int DPW = OPW + 1;               // and one scale load
+  static constexpr int TN = 64;                     // output columns per wave
+  static constexpr int FN = 2;
+  static_assert(C::BM == 128 && C::BROWS == 128 && C::WM == 2 && C::WN == 2 && C::SUBCH && !C::SWIGLU,
+                "128 x 128 tiles of 2 x 2 waves, subchannel, plain epilogue");
+  static_assert(SPG == 2 || SPG == 4, "groups of 128 or 256 K");
+
+  v16f acc[2][2];
+  float tot[2][2][16];
+  v6i fa[2][2];  // [set][i]
+  v6i fb[2][2];  // [set][j]
+  uint32_t voff[OPW];
+  v4i rs;        // operand DMA resource (waves 0-1: A, 2-3: B)
+  v4i rss;       // scale DMA resource (waves 0-1: a_scale, 2-3: b_scale)
+  int sbase;     // waves 0-1: element index row * G of the lane's row; 2-3: byte of its b_scale pair
+  int groups;    // G = K / S
+  int sb_row;    // bytes of one b_scale row (N * 2)
+  uint32_t lds0;
+  int lane, wave, wm, wn, m0;
+
+  __device__ __forceinline__ int out_row(int i) const { return wm * 64 + 32 * i + (lane & 31); }
+  __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
+
+  // a6 / b6: block-format operands; tile rows m0 (A) and n0 (B).
+  __device__ __forceinline__ void setup(uint8_t* smem, const uint8_t* a6, const uint8_t* b6, int m0_, int n0,
+                                        int kb, unsigned long long a_bytes, unsigned long long b_bytes,
+                                        const uint16_t* a_scale, const uint16_t* b_scale, int m_rows, int n_cols,
+                                        int g) {
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    wm = wave % 2;
+    wn = wave / 2;
+    m0 = m0_;
+    groups = g;
+    lds0 = lds_address(smem);
+    const unsigned long long panel_bytes = (unsigned long long)kb * F6_BLOCK;
+    const bool is_a = wave < 2;
+    const unsigned long long first = (unsigned long long)((is_a ? m0 : n0) / 32) * panel_bytes;
+    rs = buffer_words((is_a ? a6 : b6) + first, (is_a ? a_bytes : b_bytes) - first);
+    // DMA load c of this wave fills stage bytes [1024 * (OPW*wave + c), +1024):
+    // panel o / F6_BLOCK of the operand, byte o % F6_BLOCK of its block
+#pragma unroll
+    for (int c = 0; c < OPW; ++c) {
+      const uint32_t o = 1024u * (OPW * wave + c) + 16u * lane - (is_a ? 0u : (uint32_t)OPB);
+      voff[c] = (o / F6_BLOCK) * (uint32_t)panel_bytes + o % F6_BLOCK;
+    }
+    sb_row = 2 * n_cols;
+    if (is_a) {
+      rss = buffer_words(a_scale, 2ull * (unsigned long long)m_rows * g);
+      sbase = (m0 + 64 * wave + lane) * g;
+    } else {
+      rss = buffer_words(b_scale, 2ull * (unsigned long long)g * n_cols);
+      sbase = 2 * (n0 + 2 * lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          acc[i][j][r] = 0.0f;
+          tot[i][j][r] = 0.0f;
+        }
+  }
+
+  // byte offset of this lane's scale dword for group g
+  __device__ __forceinline__ uint32_t scale_voff(int g) const {
+    return wave < 2 ? (uint32_t)(2 * (sbase + g)) & ~3u : (uint32_t)(g * sb_row + sbase);
+  }
+  // LDS destination of this wave's scale load for group g
+  __device__ __forceinline__ uint32_t scale_m0(int g) const {
+    return lds0 + (uint32_t)RING + (uint32_t)(g & 3) * SCALE_SLOT + (wave < 2 ? 256u * wave : 512u);
+  }
+
+  struct Reads {
+    uint32_t a16, a8, b16, b8;
+    __device__ __forceinline__ void add(uint32_t d) {
+      a16 += d;
+      a8 += d;
+      b16 += d;
+      b8 += d;
+    }
+  };
+  __device__ __forceinline__ Reads reads_of_slot(int slot) const {
+    const uint32_t s = lds0 + (uint32_t)slot * STAGE;
+    const uint32_t a = s + 2u * wm * F6_BLOCK, b = s + OPB + 2u * wn * F6_BLOCK;
+    return Reads{a + 16u * lane, a + 1024u + 8u * lane, b + 16u * lane, b + 1024u + 8u * lane};
+  }
+
+  // LDS read Q (0..7) of a stage into set S: fragments A0, B0, B1, A1 (the
+  // order of first use), each as its 16-byte then its 8-byte part.
+  template <int S, int Q>
+  __device__ __forceinline__ void read(const Reads& r) {
+    constexpr int F = Q / 2;
+    constexpr bool IS_A = F == 0 || F == 3;
+    constexpr int IDX = F == 0 ? 0 : (F == 3 ? 1 : F - 1);
+    constexpr int OFF = IDX * F6_BLOCK;
+    v6i& dst = IS_A ? fa[S][IDX] : fb[S][IDX];
+    if constexpr (Q % 2 == 0) {
+      v4i x;
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(IS_A ? r.a16 : r.b16), "i"(OFF));
+      dst.s0 = x.x;
+      dst.s1 = x.y;
+      dst.s2 = x.z;
+      dst.s3 = x.w;
+    } else {
+      v2i y;
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(y) : "v"(IS_A ? r.a8 : r.b8), "i"(OFF));
+      dst.s4 = y.x;
+      dst.s5 = y.y;
+    }
+  }
+
+  // MFMA T (0..3) of a stage on set S (A fragment T/2, B fragment T%2; ZERO:
+  // the group's first, C = 0), fused with DMA load T (T < 3: operands; 3:
+  // the scale dword), followed by LDS reads 2T, 2T+1 of the next stage.
+  template <int S, int T, bool ZERO>
+  __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0_st,
+                                       const v4i& rss_st, uint32_t svo, uint32_t sm0, int s8) {
+    constexpr int I = T / 2, J = T % 2;
+    if constexpr (T < OPW) {
+      // the compiler writes M0 before the statement; the MFMA is the wait
+      // state the LDS-DMA load needs after that write
+      if constexpr (ZERO)
+        asm volatile(
+            "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+            "buffer_load_dwordx4 %4, %5, %6 offen lds"
+            : "+a"(acc[I][J])
+            : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so), "{m0}"(m0_st + 1024u * T)
+            : "memory");
+      else
+        asm volatile(
+            "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+            "buffer_load_dwordx4 %4, %5, %6 offen lds"
+            : "+a"(acc[I][J])
+            : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so), "{m0}"(m0_st + 1024u * T)
+            : "memory");
+    } else {
+      if constexpr (ZERO)
+        asm volatile(
+            "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+            "buffer_load_dword %4, %5, 0 offen lds"
+            : "+a"(acc[I][J])
+            : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(svo), "s"(rss_st), "{m0}"(sm0)
+            : "memory");
+      else
+        asm volatile(
+            "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+            "buffer_load_dword %4, %5, 0 offen lds"
+            : "+a"(acc[I][J])
+            : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(svo), "s"(rss_st), "{m0}"(sm0)
+            : "memory");
+    }
+    read<1 - S, 2 * T>(r);
+    read<1 - S, 2 * T + 1>(r);
+  }
+
+  // Wait states between accumulator writes and reads outside the asm
+  // MFMAs; every accumulator is an operand, so no access crosses it.
+  template <int N>
+  __device__ __forceinline__ void fence() {
+    static_assert(N == 4 || N == 7, "wait states");
+    if constexpr (N == 4)
+      asm volatile("s_nop 4" : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]));
+    else
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                   : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]));
+  }
+  // This wave's LDS reads into set S have landed; every register of the set
+  // is an operand, so no copy of it is placed before this point.
+  template <int S>
+  __device__ __forceinline__ void frag_fence() {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[S][0]), "+v"(fa[S][1]), "+v"(fb[S][0]), "+v"(fb[S][1])::"memory");
+  }
+
+  // Stage k on set S (ZERO: the first stage of a group).  Past the last
+  // stage the DMA loads go through zero-record resources.
+  template <int S, bool ZERO>
+  __device__ __forceinline__ void stage(const Reads& r, int k, int nst, int slot, const v4i& rs_end,
+                                        const v4i& rss_end, int s8) {
+    wait_vmcnt<(P - 2) * DPW>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int kl = k + P;  // the stage loaded now
+    const bool live = kl < nst;
+    const v4i rs_st = live ? rs : rs_end;
+    const v4i rss_st = live ? rss : rss_end;
+    const int gl = kl / SPG;
+    const uint32_t so = live ? (uint32_t)kl * F6_BLOCK : 0u;
+    const uint32_t svo = live ? scale_voff(gl) : 0u;
+    const uint32_t m0_st = lds0 + (uint32_t)slot * STAGE + 1024u * OPW * wave;
+    const uint32_t sm0 = scale_m0(gl);
+    tick<S, 0, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
+    tick<S, 1, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
+    tick<S, 2, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
+    tick<S, 3, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
+    frag_fence<1 - S>();
+  }
+  static __device__ __forceinline__ void advance(Reads& r, int& slot) {
+    r.add(slot == P - 2 ? (uint32_t)(-(P - 1) * STAGE) : (uint32_t)STAGE);
+    slot = slot == P - 1 ? 0 : slot + 1;
+  }
+
+  // Folds group g's partial sums into the totals:
+  // tot += (float(part) * a_scale[row, g]) * b_scale[g, col].
+  __device__ __forceinline__ void fold(const uint8_t* smem, int g) {
+    const uint8_t* sl = smem + RING + (g & 3) * SCALE_SLOT;
+    float sa[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = out_row(i);
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(sl + 4 * row);
+      const int e = (m0 + row) * groups + g;
+      sa[i] = (e & 1) ? f6_bf16_hi(w) : f6_bf16_lo(w);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint2 w = *reinterpret_cast<const uint2*>(sl + 512 + 2 * out_col(j, q));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float x = acc[i][j][4 * q + t] * sa[i];
+            x = x * f6_bf16_at(w, t);
+            tot[i][j][4 * q + t] = tot[i][j][4 * q + t] + x;
+          }
+      }
+  }
+
+  // nst: 64-K stages (a multiple of SPG).  RAW: no folds, the accumulators
+  // keep the whole K sum (exact up to 2^24, K <= F6_MAX_K).
+  template <bool RAW>
+  __device__ __forceinline__ void run(const uint8_t* smem, int nst) {
+    const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
+    const v4i rss_end = v4i{rss.x, rss.y, 0, rss.w};
+    const int s8 = 130;  // E8M0 2^3: both operands hold v/8
+    // stages 0 .. P-1 (zeros past the last stage) with their groups' scales
+#pragma unroll
+    for (int st = 0; st < P; ++st) {
+      const bool live = st < nst;
+#pragma unroll
+      for (int c = 0; c < OPW; ++c)
+        lds_dma16(live ? rs : rs_end, voff[c], live ? (uint32_t)st * F6_BLOCK : 0u,
+                  lds0 + (uint32_t)st * STAGE + 1024u * (OPW * wave + c));
+      // (the nop: the wait state between the M0 write and the LDS-DMA load)
+      asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+                   :
+                   : "v"(live ? scale_voff(st / SPG) : 0u), "s"(live ? rss : rss_end), "{m0}"(scale_m0(st / SPG))
+                   : "memory");
+    }
+    wait_vmcnt<(P - 1) * DPW>();
+    asm volatile("s_barrier" ::: "memory");
+    Reads r = reads_of_slot(0);
+    read<0, 0>(r);
+    read<0, 1>(r);
+    read<0, 2>(r);
+    read<0, 3>(r);
+    read<0, 4>(r);
+    read<0, 5>(r);
+    read<0, 6>(r);
+    read<0, 7>(r);
+    frag_fence<0>();
+    fence<4>();
+    r = reads_of_slot(1);
+    int slot = 0;
+    for (int k = 0; k < nst; k += SPG) {
+      // one group: SPG stages, alternating register sets (SPG is even)
+      stage<0, !RAW>(r, k, nst, slot, rs_end, rss_end, s8);
+      advance(r, slot);
+      stage<1, false>(r, k + 1, nst, slot, rs_end, rss_end, s8);
+      advance(r, slot);
+      if constexpr (SPG == 4) {
+        stage<0, false>(r, k + 2, nst, slot, rs_end, rss_end, s8);
+        advance(r, slot);
+        stage<1, false>(r, k + 3, nst, slot, rs_end, rss_end, s8);
+        advance(r, slot);
+      }
+      fence<7>();
+      if constexpr (!RAW) fold(smem, k / SPG);
+    }
+    // the loads past the last stage land before the workgroup's LDS is freed
+    wait_vmcnt<0>();
+  }
+};
+
+// Stores a wave's 64 x 64 results v(i, j, x) (accumulator layout) as bf16
+// through its own 8 KiB region of the idle ring: unit u = 4j + q (columns
+// 8u .. 8u+7) of row r at r * 128 + 16 * (u ^ ((r / 2) % 8)), read back one
+// 128-byte row segment per 8 lanes.
+template <class E, class V>
+__device__ __forceinline__ void f6sub_store_bf16(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
+                                                 V v) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  uint8_t* region = smem + (size_t)e.wave * 64 * 128;
+  const int lane = e.lane;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int u = 4 * j + q;
+      const int half = 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int x = 4 * q;
+        const uint32_t lo = f32_to_bf16_rne(v(i, j, x)) | (f32_to_bf16_rne(v(i, j, x + 1)) << 16);
+        const uint32_t hi = f32_to_bf16_rne(v(i, j, x + 2)) | (f32_to_bf16_rne(v(i, j, x + 3)) << 16);
+        const int r = 32 * i + (lane & 31);
+        *reinterpret_cast<uint2*>(region + r * 128 + 16 * (u ^ ((r >> 1) & 7)) + half) = make_uint2(lo, hi);
+      }
+    }
+  const uint32_t ldo = (uint32_t)o.ld;
+  const unsigned long long first = (unsigned long long)m0 * ldo + n0;
+  const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(o.out) + first * 2, ((unsigned long long)o.rows * ldo - first) * 2);
+  const int rr = lane / 8, u = lane % 8;
+  const uint32_t voff = ((uint32_t)(e.wm * 64 + rr) * ldo + (uint32_t)(e.wn * 64 + 8 * u)) * 2u;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int r = 8 * t + rr;
+    const uint4 x = *reinterpret_cast<const uint4*>(region + r * 128 + 16 * (u ^ ((r >> 1) & 7)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(8 * t) * ldo * 2u, 0);
+  }
+}
+
+// fp32 / int32 results: four consecutive columns per store.
+template <class E, class V>
+__device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, int m0, int n0, V v) {
+  const uint32_t ldo = (uint32_t)o.ld;
+  const unsigned long long first = (unsigned long long)m0 * ldo + n0;
+  const rsrc_t r = make_rsrc(static_cast<uint8_t*>(o.out) + first * 4, ((unsigned long long)o.rows * ldo - first) * 4);
+  const uint32_t voff = ((uint32_t)e.out_row(0) * ldo + (uint32_t)e.out_col(0, 0)) * 4u;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int x = 4 * q;
+        __builtin_amdgcn_raw_buffer_store_b128(v4i{v(i, j, x), v(i, j, x + 1), v(i, j, x + 2), v(i, j, x + 3)}, r,
+                                               voff + (uint32_t)(32 * j + 8 * q) * 4u,
+                                               (uint32_t)(32 * i) * ldo * 4u, 0);
+      }
+}
+
+// Subchannel GEMM over fp6 blocks (p.a / p.b point at the converted A and
+// B); SPG = S / 64 stages per scale group.  One kernel per output mode and
+// epilogue.  Two workgroups share a CU.
+template <class C, int MODE, int EPI, int SPG>
+__global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
+  using E = F6SubEngine<C, SPG>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  const int tiles_m = p.M / C::BM;
+  const int tiles_n = p.N / C::BN;
+  int tm, tn;
+  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
+  const int m0 = tm * C::BM;
+  const int n0 = tn * C::BN;
+  E e;
+  e.setup(smem, p.a, p.b, m0, n0, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.N, p.K), p.a_scale,
+          p.b_scale, p.M, p.N, p.K / p.subchannel);
+  e.template run<MODE == OUT_I32>(smem, p.K / 64);
+  const OutView o{p.out, p.b_scale, p.N, p.M, p.N, 0, p.M, p.N};
+  if constexpr (MODE == OUT_I32) {
+    f6sub_store_words(e, o, m0, n0, [&](int i, int j, int x) { return (int)e.acc[i][j][x]; });
+  } else if constexpr (MODE == OUT_F32) {
+    f6sub_store_words(e, o, m0, n0,
+                      [&](int i, int j, int x) { return __float_as_int(apply_epi(e.tot[i][j][x], EPI)); });
+  } else {
+    f6sub_store_bf16(e, o, smem, m0, n0, [&](int i, int j, int x) { return apply_epi(e.tot[i][j][x], EPI); });
+  }
+}
+
+}  // namespace shk

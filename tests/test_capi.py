@@ -180,11 +180,18 @@ def _gemm_ws(lib, index, m, n, k, *, work, work_bytes, epi=0, mode=0):
 
 def test_fp6_entries_report_their_workspace(lib):
     fp6 = [d for d in kt.entries(kt.FAMILY_DENSE) if d.operand_format == kt.OPERANDS_FP6]
-    assert {(d.layout, d.epilogue_kind) for d in fp6} == {
-        (layout, epi) for layout in (kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN)
-        for epi in (kt.EPI_KIND_PLAIN, kt.EPI_KIND_SWIGLU)}
+    layouts = (kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN)
+    assert {(d.layout, d.epilogue_kind, d.scale_mode) for d in fp6} == {
+        (layout, epi, kt.SCALE_PER_CHANNEL) for layout in layouts for epi in (kt.EPI_KIND_PLAIN, kt.EPI_KIND_SWIGLU)
+    } | {(layout, kt.EPI_KIND_PLAIN, kt.SCALE_SUBCHANNEL) for layout in layouts}
     for d in fp6:
-        assert d.dtype_bits == 4 and d.block_m == 256 and d.num_stages == 3 and d.lds_bytes == 147456
+        if d.scale_mode == kt.SCALE_SUBCHANNEL:
+            # 128 x 128 tiles, six 12 KiB stages and the 3 KiB scale ring; groups of 128 or 256
+            assert (d.block_m, d.block_n, d.num_stages, d.lds_bytes) == (128, 128, 6, 76800)
+            assert (d.min_subchannel, d.max_subchannel) == (128, 256)
+        else:
+            assert d.block_m == 256 and d.num_stages == 3 and d.lds_bytes == 147456
+        assert d.dtype_bits == 4
         for m, n, k in ((256, 256, 128), (512, 1024, 4096), (8192, 8192, 8192)):
             rc, got = _ws(lib, d.index, m, n, k)
             b_cols = 2 * n if d.epilogue_kind == kt.EPI_KIND_SWIGLU else n

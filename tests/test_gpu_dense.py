@@ -260,7 +260,10 @@ def test_special_scale_values_store_like_torch(kernel, device):
 
 
 _FP6 = [k for k in shk.default_registry.all()
-        if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.epilogue is not shk.Epilogue.RELU2]
+        if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.epilogue is not shk.Epilogue.RELU2
+        and k.scale.mode is shk.ScaleMode.PER_CHANNEL]
+_FP6_SUB = [k for k in shk.default_registry.all()
+            if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.scale.mode is shk.ScaleMode.SUBCHANNEL]
 
 
 @pytest.mark.parametrize("kernel", _FP6, ids=lambda k: k.kernel_id)
@@ -280,6 +283,26 @@ def test_fp6_kernels_every_stage_count(kernel, k, device):
         assert max_ulp(got, want) <= ULP_TOL
     else:
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kernel", _FP6_SUB, ids=lambda k: k.kernel_id)
+@pytest.mark.parametrize("groups", [1, 2, 3, 5])
+def test_fp6_subchannel_every_group_count(kernel, groups, device):
+    """One to five scale groups: each is folded into the fp32 totals in group
+    order, as the oracle sums them, so the results are bit-identical; the
+    int32 output is the whole exact sum.  Scales spread over two decades so
+    that a fold in the wrong order or with the wrong group's scales shows."""
+    _, layout, sub, epi = _kernel_params(kernel)
+    m, n, k = 256, 384, groups * sub
+    seed = stable_seed(f"{kernel.kernel_id}/{groups}")
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=False, scale_lo=0.001, scale_hi=0.1)
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q)), "int32 accumulators differ"
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=4, layout=layout, a_scale=sa, b_scale=sb, subchannel=sub,
+                                   epilogue=epi)
+    assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])

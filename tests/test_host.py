@@ -63,15 +63,23 @@ def test_registry_is_built_from_the_table():
         (shk.OperandDType.INT4, PC, shk.Epilogue.NONE, (128, 1024, 64), (128, 128)),           # C1
         (shk.OperandDType.INT4, PC, shk.Epilogue.NONE, (8192, 8192, 8192), (256, 256)),        # C2
         (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 256), shk.Epilogue.RELU2,
-         (4096, 16384, 4096), (256, 128)),                                                     # C3
+         (4096, 16384, 4096), (128, 128)),                                                     # C3
         (shk.OperandDType.INT8, PC, shk.Epilogue.SWIGLU, (4096, 11008, 4096), (256, 128)),     # C4
+        (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 64), shk.Epilogue.NONE,
+         (4096, 4096, 4096), (256, 128)),
     ],
 )
-def test_select_picks_the_largest_fitting_tile(dtype, scale, epilogue, shape, tile):
+def test_select_picks_the_fastest_then_the_largest_fitting_tile(dtype, scale, epilogue, shape, tile):
+    """Measured MI355X throughput ranks first (C2-C4 pick the measured fp6
+    and int8 32x32 entries), tile area next (C1, subchannel 64)."""
     m, n, k = shape
     kernel = shk.default_registry.select(dtype=dtype, scale=scale, epilogue=epilogue, m=m, n=n, k=k)
     assert (kernel.tile.block_m, kernel.tile.block_n) == tile
     assert not tile_multiple_rejection_reasons(kernel, LaunchShape(m, n, k))
+    fitting = [c for c in shk.default_registry.all() if c.scale == scale and c.epilogue is epilogue
+               and c.a_dtype is dtype and c.layout is kernel.layout
+               and not tile_multiple_rejection_reasons(c, LaunchShape(m, n, k))]
+    assert (kernel.measured_tops or 0) == max(c.measured_tops or 0 for c in fitting)
 
 
 def test_select_raises_for_shapes_no_kernel_accepts():
@@ -91,7 +99,8 @@ def test_select_reference_ignores_shape():
 def test_measured_tops_overrides_tile_size():
     reg = shk.default_registry
     small = reg.select(dtype=shk.OperandDType.INT4, scale=PC, epilogue=shk.Epilogue.NONE, m=64, n=64, k=64)
-    bumped = reg.with_status(small.kernel_id, shk.KernelStatus.BENCHMARKED, measured_tops=1.0)
+    top = max(k.measured_tops or 0.0 for k in reg.all())
+    bumped = reg.with_status(small.kernel_id, shk.KernelStatus.BENCHMARKED, measured_tops=top + 1.0)
     pick = bumped.select(dtype=shk.OperandDType.INT4, scale=PC, epilogue=shk.Epilogue.NONE, m=256, n=256, k=128)
     assert pick.kernel_id == small.kernel_id
 
