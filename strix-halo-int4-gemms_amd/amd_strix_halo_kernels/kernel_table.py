@@ -191,10 +191,10 @@ def measured_tops(desc: KernelDesc) -> float | None:
         return None
     if desc.operand_format == OPERANDS_FP6:
         if desc.scale_mode == SCALE_SUBCHANNEL:
-            return 1572.0
-        return 3535.0 if desc.epilogue_kind == EPI_KIND_PLAIN else None
+            return 2001.0
+        return 3504.0 if desc.epilogue_kind == EPI_KIND_PLAIN else None
     if desc.dtype_bits == 8 and desc.num_stages == 4 and desc.block_m == 256:
-        return 1994.0 if desc.epilogue_kind == EPI_KIND_SWIGLU else 2270.0
+        return 2014.0 if desc.epilogue_kind == EPI_KIND_SWIGLU else 2270.0
     return None
 
 

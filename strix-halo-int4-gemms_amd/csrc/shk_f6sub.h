@@ -16,14 +16,17 @@
 //    totals), so a wave stays within 256 registers and two 4-wave
 //    workgroups of 128 x 128 share a CU: while one wave folds, the other
 //    wave on its SIMD issues MFMAs;
+//  * the accumulators are VGPRs (the MFMA reads and writes them there), so
+//    the fold reads them directly instead of copying each out of an AGPR;
 //  * the scales reach LDS by LDS-DMA in the same stream as the operands,
 //    so no load the compiler tracks sits in the K loop.
 //
 // Pipeline: 64-K stages (one 32 x 64 fp6 block per 32-row panel; 6 KiB of
 // A and 6 KiB of B) in a ring of six slots.  Stage k: wait for this wave's
 // DMA of stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
-// carrying the 8 LDS reads of stage k+1's fragments and the 4 DMA loads of
-// stage k+6 into slot k % 6 (3 operand loads and one scale load per wave);
+// carrying (the first two) the 8 LDS reads of stage k+1's fragments and
+// the 4 DMA loads of stage k+6 into slot k % 6 (3 operand loads and one
+// scale load per wave);
 // then a fence that waits for this stage's LDS reads with every fragment
 // register of the other set as an operand, so no compiler copy of a
 // fragment can precede its data.
@@ -165,7 +168,9 @@ struct F6SubEngine {
 
   // MFMA T (0..3) of a stage on set S (A fragment T/2, B fragment T%2; ZERO:
   // the group's first, C = 0), fused with DMA load T (T < 3: operands; 3:
-  // the scale dword), followed by LDS reads 2T, 2T+1 of the next stage.
+  // the scale dword), followed by LDS reads 4T .. 4T+3 of the next stage
+  // for T < 2: all reads go out early, so they have landed when the stage's
+  // closing fence waits for them.
   template <int S, int T, bool ZERO>
   __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0_st,
                                        const v4i& rss_st, uint32_t svo, uint32_t sm0, int s8) {
@@ -177,14 +182,14 @@ struct F6SubEngine {
         asm volatile(
             "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
             "buffer_load_dwordx4 %4, %5, %6 offen lds"
-            : "+a"(acc[I][J])
+            : "+v"(acc[I][J])
             : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so), "{m0}"(m0_st + 1024u * T)
             : "memory");
       else
         asm volatile(
             "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
             "buffer_load_dwordx4 %4, %5, %6 offen lds"
-            : "+a"(acc[I][J])
+            : "+v"(acc[I][J])
             : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so), "{m0}"(m0_st + 1024u * T)
             : "memory");
     } else {
@@ -192,31 +197,35 @@ struct F6SubEngine {
         asm volatile(
             "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
             "buffer_load_dword %4, %5, 0 offen lds"
-            : "+a"(acc[I][J])
+            : "+v"(acc[I][J])
             : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(svo), "s"(rss_st), "{m0}"(sm0)
             : "memory");
       else
         asm volatile(
             "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
             "buffer_load_dword %4, %5, 0 offen lds"
-            : "+a"(acc[I][J])
+            : "+v"(acc[I][J])
             : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(svo), "s"(rss_st), "{m0}"(sm0)
             : "memory");
     }
-    read<1 - S, 2 * T>(r);
-    read<1 - S, 2 * T + 1>(r);
+    if constexpr (T < 2) {
+      read<1 - S, 4 * T>(r);
+      read<1 - S, 4 * T + 1>(r);
+      read<1 - S, 4 * T + 2>(r);
+      read<1 - S, 4 * T + 3>(r);
+    }
   }
 
-  // Wait states between accumulator writes and reads outside the asm
-  // MFMAs; every accumulator is an operand, so no access crosses it.
+  // Wait states between the asm MFMAs' accumulator writes and any other
+  // access; every accumulator is an operand, so no access crosses it.
   template <int N>
   __device__ __forceinline__ void fence() {
     static_assert(N == 4 || N == 7, "wait states");
     if constexpr (N == 4)
-      asm volatile("s_nop 4" : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]));
+      asm volatile("s_nop 4" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
     else
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                   : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[1][0]), "+a"(acc[1][1]));
+                   : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
   }
   // This wave's LDS reads into set S have landed; every register of the set
   // is an operand, so no copy of it is placed before this point.
@@ -333,6 +342,7 @@ struct F6SubEngine {
     }
     // the loads past the last stage land before the workgroup's LDS is freed
     wait_vmcnt<0>();
+    fence<7>();
   }
 };
 
