@@ -98,6 +98,11 @@ class KernelDesc:
         return size is not None and self.min_subchannel <= size <= self.max_subchannel
 
 
+# The 32x32 engines (fp6 per-channel, int8 direct-to-LDS) keep each wave's
+# 256 bytes of B scales in LDS past the stage ring (shk_f6.h).
+MFMA32_SCALE_BYTES = 4 * 256
+
+
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
           fp6=False, fp6_sub=False):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
@@ -112,9 +117,11 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         lds = pipe * (bm + bn) * 48 + 4 * 768
     elif fp6:
         pipe = 3
-        lds = pipe * (bm + 256) * 96
+        lds = pipe * (bm + 256) * 96 + MFMA32_SCALE_BYTES
     else:
         lds = pipe * (bm + brows) * 64 if pipe else 2 * (bm * bk + brows * bk)
+        if bits == 8 and pipe:
+            lds += MFMA32_SCALE_BYTES
     return KernelDesc(
         index=index,
         family=family,

@@ -68,80 +68,116 @@ __device__ __forceinline__ uint4 f6_load(const uint8_t* q, int unit, int valid) 
 }
 // 64-K blocks that the GEMM reads for K length `len`: whole 128-K stages.
 __device__ __forceinline__ int f6_blocks_read(int len) { return 2 * ((len + 127) / 128); }
+// bytes of one MN-major source tile in LDS: 32 K rows x 256 packed rows
+constexpr int F6_KTILE = 32 * 256;
 
-// K-major source (row r holds its K values contiguously, two per byte): one
-// wave converts one block; a lane loads its 16 source bytes directly.
-// Nibble j of a little-endian source word is K value 8w + j of its 32, so K
-// values at or past the operand's length are cleared word by word.
+// Blocks per wave (K-major) and 64-K blocks per workgroup (MN-major), with
+// every load of a wave issued before its first conversion.  Measured on
+// the C2 operands (8192 x 8192): one block per K-major wave runs at the
+// speed of a device copy of the same bytes (more per wave is 4-6% slower),
+// while two 64-K blocks per MN-major workgroup are 19% faster than one when
+// the source is cache-resident and equal from HBM.
+constexpr int kNB = 1;
+constexpr int kKW = 2;
+
+// K-major source (row r holds its K values contiguously, two per byte): a
+// wave converts kNB consecutive blocks (panel-major order, so mostly the
+// same panel's next 64-K blocks); a lane loads its 16 source bytes of each
+// directly.  Nibble j of a little-endian source word is K value 8w + j of
+// its 32, so K values at or past the operand's length are cleared word by
+// word.
 __device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
   const int lane = threadIdx.x & 63;
-  const int panels = f6_panels(p.rows);
-  const long blocks = (long)panels * p.kb;
-  const long per_group = (blocks + 3) / 4;
+  const long blocks = (long)f6_panels(p.rows) * p.kb;
+  const long per_group = (blocks + 4 * kNB - 1) / (4 * kNB);
   const int g = (int)(wg / per_group);
-  const long blk = (wg - (long)g * per_group) * 4 + (threadIdx.x >> 6);
-  if (blk >= blocks) return;
-  const int panel = (int)(blk / p.kb);
-  const int kb = (int)(blk - (long)panel * p.kb);
+  const long first = ((wg - (long)g * per_group) * 4 + (threadIdx.x >> 6)) * kNB;
+  if (first >= blocks) return;
   const int len = f6_k_len(p, g);
-  if (kb >= f6_blocks_read(len)) return;
-  const int r = 32 * panel + (lane & 31);
-  const int k0 = 64 * kb + 32 * (lane >> 5);
-  uint4 x = make_uint4(0u, 0u, 0u, 0u);
-  if (r < p.rows && k0 < len) {
-    const int row = f6_src_row(r, p.swiglu_n);
-    const uint8_t* q = p.src + g * p.src_group + (long)row * p.ld + 32L * kb + 16 * (lane >> 5);
-    const int keep = len - k0;  // K values of the 32 to keep
-    // bytes holding any of them (the source row ends within the length)
-    x = f6_load(q, p.vec, (keep + 1) / 2);
-    if (keep < 32) {
-      uint32_t w[4] = {x.x, x.y, x.z, x.w};
+  const int nread = f6_blocks_read(len);
+  const uint8_t* src = p.src + g * p.src_group;
+  int panel = (int)(first / p.kb);
+  int kb = (int)(first - (long)panel * p.kb);
+  uint4 x[kNB];
+  bool live[kNB];
 #pragma unroll
-      for (int wq = 0; wq < 4; ++wq) {
-        const int c = keep - 8 * wq;
-        w[wq] &= c >= 8 ? 0xFFFFFFFFu : (c <= 0 ? 0u : (1u << (4 * c)) - 1u);
+  for (int b = 0; b < kNB; ++b) {
+    live[b] = first + b < blocks && kb < nread;
+    x[b] = make_uint4(0u, 0u, 0u, 0u);
+    const int r = 32 * panel + (lane & 31);
+    const int k0 = 64 * kb + 32 * (lane >> 5);
+    if (live[b] && r < p.rows && k0 < len) {
+      const uint8_t* q = src + (long)f6_src_row(r, p.swiglu_n) * p.ld + 32L * kb + 16 * (lane >> 5);
+      const int keep = len - k0;  // K values of the 32 to keep
+      // bytes holding any of them (the source row ends within the length)
+      x[b] = f6_load(q, p.vec, (keep + 1) / 2);
+      if (keep < 32) {
+        uint32_t w[4] = {x[b].x, x[b].y, x[b].z, x[b].w};
+#pragma unroll
+        for (int wq = 0; wq < 4; ++wq) {
+          const int c = keep - 8 * wq;
+          w[wq] &= c >= 8 ? 0xFFFFFFFFu : (c <= 0 ? 0u : (1u << (4 * c)) - 1u);
+        }
+        x[b] = make_uint4(w[0], w[1], w[2], w[3]);
       }
-      x = make_uint4(w[0], w[1], w[2], w[3]);
     }
+    if (++kb == p.kb) kb = 0, ++panel;
   }
-  f6_store_lane(p.dst + g * p.dst_group + blk * F6_BLOCK, lane, f6_convert(x));
+  uint8_t* dst = p.dst + g * p.dst_group + first * F6_BLOCK;
+#pragma unroll
+  for (int b = 0; b < kNB; ++b)
+    if (live[b]) f6_store_lane(dst + b * F6_BLOCK, lane, f6_convert(x[b]));
 }
 
 // MN-major source (K row kp holds two K values of every packed row, one per
 // nibble, the even one low): a workgroup converts the blocks of one 256-row
-// tile and one 64-K block.  The 32 x 256-byte source tile goes through LDS in
-// the MN-major ring layout of the DMA engine, whose transposing reads hand
-// each lane its row's bytes in K order: within a 16-lane group, lane i
-// addresses source row kp + i/2 at byte 8*(i%2) of a 16-row unit and
-// receives the 8 bytes of those 8 rows in column i.  Units past the rows and
-// K rows past the length load as zeros; panels past the rows are not stored.
+// tile and kKW consecutive 64-K blocks.  Each 32 x 256-byte source tile goes
+// through LDS in the MN-major ring layout of the DMA engine, whose
+// transposing reads hand each lane its row's bytes in K order: within a
+// 16-lane group, lane i addresses source row kp + i/2 at byte 8*(i%2) of a
+// 16-row unit and receives the 8 bytes of those 8 rows in column i.  Units
+// past the rows and K rows past the length load as zeros; panels past the
+// rows and 64-K blocks the GEMM does not read are not stored.
 __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_t* tile) {
   const int tiles = (p.rows + F6_TILE - 1) / F6_TILE;
-  const int per_group = tiles * p.kb;
+  const int kgroups = (p.kb + kKW - 1) / kKW;
+  const int per_group = tiles * kgroups;
   const int g = wg / per_group;
   const int local = wg - g * per_group;
-  const int t = local / p.kb;
-  const int kb = local - t * p.kb;
+  const int t = local / kgroups;
+  const int kb0 = (local - t * kgroups) * kKW;
   const int len = f6_k_len(p, g);
-  if (kb >= f6_blocks_read(len)) return;  // uniform over the workgroup
+  const int nread = min(f6_blocks_read(len), p.kb);
+  if (kb0 >= nread) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
   const int u = tid & 15;  // 16-row unit of the tile
   const int r0 = F6_TILE * t + 16 * u;
   const long col = f6_src_row(r0, p.swiglu_n);
   const uint8_t* src = p.src + g * p.src_group;
+  uint4 x[kKW][2];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int kp = 16 * q + (tid >> 4);
-    const int k = 2 * (32 * kb + kp);  // K of the low nibbles
-    uint4 x = make_uint4(0u, 0u, 0u, 0u);
-    if (r0 < p.rows && k < len) {
-      const uint8_t* q = src + (32L * kb + kp) * p.ld + col;
-      x = f6_load(q, p.vec, p.rows - r0);
-      if (k + 1 >= len) x = make_uint4(x.x & 0x0F0F0F0Fu, x.y & 0x0F0F0F0Fu, x.z & 0x0F0F0F0Fu, x.w & 0x0F0F0F0Fu);
+  for (int w = 0; w < kKW; ++w)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int kb = kb0 + w;
+      const int kp = 16 * q + (tid >> 4);
+      const int k = 2 * (32 * kb + kp);  // K of the low nibbles
+      x[w][q] = make_uint4(0u, 0u, 0u, 0u);
+      if (kb < nread && r0 < p.rows && k < len) {
+        x[w][q] = f6_load(src + (32L * kb + kp) * p.ld + col, p.vec, p.rows - r0);
+        if (k + 1 >= len)
+          x[w][q] = make_uint4(x[w][q].x & 0x0F0F0F0Fu, x[w][q].y & 0x0F0F0F0Fu, x[w][q].z & 0x0F0F0F0Fu,
+                               x[w][q].w & 0x0F0F0F0Fu);
+      }
     }
-    const int swz = (kp & 7) | ((kp & 16) >> 1);
-    *reinterpret_cast<uint4*>(tile + kp * 256 + 16 * (u ^ swz)) = x;
-  }
+#pragma unroll
+  for (int w = 0; w < kKW; ++w)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int kp = 16 * q + (tid >> 4);
+      const int swz = (kp & 7) | ((kp & 16) >> 1);
+      *reinterpret_cast<uint4*>(tile + w * F6_KTILE + kp * 256 + 16 * (u ^ swz)) = x[w][q];
+    }
   __syncthreads();
   // lane l of a block: packed row 32b + l % 32 (unit 2b + (l/16) % 2, column
   // l % 16 of it), K rows 16*(l/32) + [0, 16)
@@ -150,30 +186,36 @@ __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_
   const int kp = 16 * (lane >> 5) + i / 2;
   const int swz = (kp & 7) | ((kp & 16) >> 1);
   const int panels = f6_panels(p.rows);
+  uint8_t* dst = p.dst + g * p.dst_group;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int b = 2 * (tid >> 6) + c;
-    if (8 * t + b >= panels) continue;
-    const int unit = 2 * b + ((lane >> 4) & 1);
-    const uint8_t* q = tile + kp * 256 + 16 * (unit ^ swz) + 8 * (i & 1);
-    const v2i lo = ds_read_tr8(q);
-    const v2i hi = ds_read_tr8(q + 2048);
-    const uint4 x = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    const long blk = (long)(8 * t + b) * p.kb + kb;
-    f6_store_lane(p.dst + g * p.dst_group + blk * F6_BLOCK, lane, f6_convert(x));
+  for (int w = 0; w < kKW; ++w) {
+    const int kb = kb0 + w;
+    if (kb >= nread) break;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int b = 2 * (tid >> 6) + c;
+      if (8 * t + b >= panels) continue;
+      const int unit = 2 * b + ((lane >> 4) & 1);
+      const uint8_t* q = tile + w * F6_KTILE + kp * 256 + 16 * (unit ^ swz) + 8 * (i & 1);
+      const v2i lo = ds_read_tr8(q);
+      const v2i hi = ds_read_tr8(q + 2048);
+      const uint4 y = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      const long blk = (long)(8 * t + b) * p.kb + kb;
+      f6_store_lane(dst + blk * F6_BLOCK, lane, f6_convert(y));
+    }
   }
 }
 
-// Workgroups of one operand batch: per operand, one per 256-row tile and
-// 64-K block (MN-major) or per 4 blocks (K-major: one per wave).
+// Workgroups of one operand batch: per operand, one per 256-row tile and kKW
+// 64-K blocks (MN-major) or per 4 * kNB blocks (K-major: kNB per wave).
 long pack_groups(const F6PackArgs& a, bool mn_major) {
-  const long per = mn_major ? (long)((a.rows + F6_TILE - 1) / F6_TILE) * a.kb
-                            : ((long)f6_panels(a.rows) * a.kb + 3) / 4;
+  const long per = mn_major ? (long)((a.rows + F6_TILE - 1) / F6_TILE) * ((a.kb + kKW - 1) / kKW)
+                            : ((long)f6_panels(a.rows) * a.kb + 4 * kNB - 1) / (4 * kNB);
   return per * a.groups;
 }
 
 __global__ __launch_bounds__(256) void f6_pack_one(const F6PackArgs p, int mn_major) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kKW * F6_KTILE];
   if (mn_major) pack_mnmajor(p, blockIdx.x, tile);
   else pack_kmajor(p, blockIdx.x);
 }
@@ -182,7 +224,7 @@ __global__ __launch_bounds__(256) void f6_pack_one(const F6PackArgs p, int mn_ma
 // A, the rest B.
 __global__ __launch_bounds__(256) void f6_pack_two(const F6PackArgs a, const F6PackArgs b, int a_mn, int b_mn,
                                                    int a_groups) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kKW * F6_KTILE];
   const int wg = blockIdx.x;
   if (wg < a_groups) {
     if (a_mn) pack_mnmajor(a, wg, tile);

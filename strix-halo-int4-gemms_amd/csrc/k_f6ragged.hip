@@ -42,7 +42,7 @@ __device__ __forceinline__ int xcd_contiguous(int w, int total) {
 template <int MODE>
 __global__ __launch_bounds__(256) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
   using E = F6Engine<F6R>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_n = (p.N + kTile - 1) / kTile;
   const int ntasks = *p.num_tasks;
   // A task list that overflowed its capacity is refused as a whole.
@@ -66,15 +66,16 @@ __global__ __launch_bounds__(256) void f6_ragged_fwd_kernel(const RaggedFwdArgs 
     const int m = m0 + e.out_row(i);
     sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + (m < p.M ? m : p.M - 1));
   }
-  e.run(kw / 128);
   const OutView o{p.out, p.b_scale + (long)g * p.N, p.N, p.M, p.N, t.z, t.w, p.N};
+  mfma32_prefetch_b_scales<F6R, MODE, true>(e, o, tn * kTile, e.lds0 + E::LDS_BYTES + 256u * e.wave);
+  e.run(kw / 128);
   mfma32_finish<F6R, MODE, EPI_NONE, true>(e, o, smem, m0, tn * kTile, sa);
 }
 
 template <int MODE>
 __global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
   using E = F6Engine<F6R>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = (p.M + kTile - 1) / kTile;
   const int tiles_n = (p.N + kTile - 1) / kTile;
   // Each group's tiles_m x tiles_n grid splits into 8 regions of sm x sn
@@ -118,9 +119,10 @@ __global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs 
     const int m = m0 + e.out_row(i);
     sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(sa_g + (m < p.M ? m : p.M - 1));
   }
-  e.run((len + 127) / 128);
   const OutView o{static_cast<float*>(p.out) + (long)g * p.M * p.N, p.b_scale + (long)g * p.N, p.N, p.M, p.N, 0,
                   p.M, p.N};
+  mfma32_prefetch_b_scales<F6R, MODE, true>(e, o, tn * kTile, e.lds0 + E::LDS_BYTES + 256u * e.wave);
+  e.run((len + 127) / 128);
   mfma32_finish<F6R, MODE, EPI_NONE, true>(e, o, smem, m0, tn * kTile, sa);
 }
 
@@ -177,7 +179,7 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
 shk_kernel_desc f6_ragged_desc(int family, int layout) {
   shk_kernel_desc d = desc_of<F6R>(family, layout, 1);
   d.num_stages = F6Engine<F6R>::P;
-  d.lds_bytes = F6Engine<F6R>::LDS_BYTES;
+  d.lds_bytes = F6Engine<F6R>::LDS_BYTES + MFMA32_SCALE_BYTES;
   d.operand_format = SHK_OPERANDS_FP6;
   return d;
 }

@@ -85,6 +85,16 @@ __device__ __forceinline__ void lds_dma16(const v4i& rs, uint32_t voff, uint32_t
       : "memory");
 }
 
+// The same with 4 bytes per lane: lane L's land at m0 + 4*L.
+__device__ __forceinline__ void lds_dma4(const v4i& rs, uint32_t voff, uint32_t soff, uint32_t m0) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "buffer_load_dword %0, %1, %2 offen lds"
+      :
+      : "v"(voff), "s"(rs), "s"(soff), "{m0}"(m0)
+      : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is six bits");

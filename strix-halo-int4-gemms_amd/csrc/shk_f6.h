@@ -465,6 +465,7 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   uint8_t* region = smem + (size_t)e.wave * 128 * PITCH;
   const int lane = e.lane;
+  const int half = 8 * (lane >> 5);  // columns +4 .. +7 of a unit
 #pragma unroll
   for (int j = 0; j < E::FN; ++j) {
 #pragma unroll
@@ -475,31 +476,55 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
         su[t] = f6_bf16_at(sb[j][q], t);
         sg[t] = C::SWIGLU ? f6_bf16_at(sb[j + 2 < 4 ? j + 2 : j][q], t) : 0.0f;
       }
-      const int u = 4 * j + q;           // columns 32j + 8q .. +7
-      const int half = 8 * (lane >> 5);  // columns +4 .. +7 of the unit
+      const int u = 4 * j + q;  // columns 32j + 8q .. +7
+      float v[4][4];            // [row i][column t]
+      if constexpr (C::SWIGLU) {
+        float up[4][4], gt[4][4];
+        float gmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            up[i][t] = e.acc_value(i, j, 4 * q + t) * sa[i];
+            up[i][t] = up[i][t] * su[t];
+            gt[i][t] = e.acc_value(i, j + 2, 4 * q + t) * sa[i];
+            gt[i][t] = gt[i][t] * sg[t];
+            gmax = __builtin_fmaxf(gmax, __builtin_fabsf(gt[i][t]));
+          }
+        // one wave-uniform choice per 16 outputs: the hardware exp2 /
+        // reciprocal path where it is accurate (fmax skips a NaN gate, which
+        // gives NaN on either path)
+        if (__all(gmax <= SWIGLU_FAST_MAX)) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[i][t] = swiglu_fast(up[i][t], gt[i][t]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[i][t] = swiglu(up[i][t], gt[i][t]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float x = e.acc_value(i, j, 4 * q + t) * sa[i];
+            x = x * su[t];
+            if constexpr (EPI == EPI_RELU2) x = apply_epi(x, EPI_RELU2);
+            v[i][t] = x;
+          }
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          float x = e.acc_value(i, j, 4 * q + t) * sa[i];
-          x = x * su[t];
-          if constexpr (C::SWIGLU) {
-            float g = e.acc_value(i, j + 2, 4 * q + t) * sa[i];
-            g = g * sg[t];
-            x = swiglu(x, g);
-          } else if constexpr (EPI == EPI_RELU2) {
-            x = apply_epi(x, EPI_RELU2);
-          }
-          v[t] = x;
-        }
         uint32_t lo, hi;
         if constexpr (NO_NAN) {
-          lo = pack_bf16x2_nonan(v[0], v[1]);
-          hi = pack_bf16x2_nonan(v[2], v[3]);
+          lo = pack_bf16x2_nonan(v[i][0], v[i][1]);
+          hi = pack_bf16x2_nonan(v[i][2], v[i][3]);
         } else {
-          lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
-          hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+          lo = f32_to_bf16_rne(v[i][0]) | (f32_to_bf16_rne(v[i][1]) << 16);
+          hi = f32_to_bf16_rne(v[i][2]) | (f32_to_bf16_rne(v[i][3]) << 16);
         }
         const int r = 32 * i + (lane & 31);
         *reinterpret_cast<uint2*>(region + r * PITCH + 16 * (u ^ swz(r)) + half) = make_uint2(lo, hi);
@@ -526,28 +551,49 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
   }
 }
 
-// B scales of the wave's columns (bf16, four per load): [j][q] for
-// fragment j, register group q; fragments j >= FN read the gate's scales.
-template <class C, bool MASK, class E>
-__device__ __forceinline__ void mfma32_load_b_scales(const E& e, const OutView& o, int n0, uint2 (&sb)[4][4]) {
-  const int gate = C::SWIGLU ? o.n : 0;
+// B scales of a 32x32-engine tile.  Before the K loop each wave copies its
+// window of TN columns (SwiGLU: TN up, then the same TN gate columns, 256
+// bytes either way) into its own 256-byte slot past the ring with one
+// direct-to-LDS dword load per lane: lane l fetches scales 2l, 2l + 1 (for
+// SwiGLU lanes 32.. the gate's).  The loop's final wait for every vector
+// load covers the copy, so the epilogue reads the slot after the loop;
+// neither holds a register across the loop.  Columns at or past the
+// buffer's range (col_hi with MASK) read as zeros.  OUT_I32 reads none.
+constexpr int MFMA32_SCALE_BYTES = 4 * 256;
+
+template <class C, int MODE, bool MASK = false, class E>
+__device__ __forceinline__ void mfma32_prefetch_b_scales(const E& e, const OutView& o, int n0, uint32_t slot) {
+  if constexpr (MODE != OUT_I32) {
+    const int c0 = n0 + e.wn * E::TN;  // the window's first column
+    const int lane = e.lane;
+    const int col = C::SWIGLU ? c0 + 2 * (lane & 31) + (lane >> 5) * o.n : c0 + 2 * lane;
+    const unsigned long long cols = MASK ? (unsigned long long)o.col_hi : (C::SWIGLU ? 2ull : 1ull) * o.n;
+    lds_dma4(buffer_words(o.b_scale, 2 * cols), 2u * (uint32_t)col, 0u, slot);
+  }
+}
+
+// sb[j][q]: the four bf16 B scales of fragment j, register group q (j >= FN:
+// the gate's), from the wave's slot.
+template <class C, class E>
+__device__ __forceinline__ void mfma32_read_b_scales(const E& e, const uint8_t* slot, uint2 (&sb)[4][4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int jj = j < E::FN ? j : j - E::FN;
-      const int col = n0 + e.out_col(jj, q);
-      sb[j][q] = (!MASK || col < o.col_hi)
-                     ? *reinterpret_cast<const uint2*>(o.b_scale + (j < E::FN ? 0 : gate) + col)
-                     : make_uint2(0u, 0u);
+      const int c = e.out_col(jj, q) - e.wn * E::TN;
+      sb[j][q] = *reinterpret_cast<const uint2*>(slot + 2 * c + (j < E::FN ? 0 : 2 * E::TN));
     }
 }
 
 // Epilogue of the 32x32 engines after the K loop: OUT_I32 and OUT_F32 store
 // directly; bf16 goes through LDS, with the hardware conversion when no
-// value can be NaN (finite scales times a finite integer give at most
-// +-inf, and ReLU^2 of that is no NaN either; SwiGLU always rounds in
-// software).
+// value can be NaN.  That holds when every scale is below 2^48 in
+// magnitude: |acc| < 2^31, so each scaled product stays below 2^127 and
+// finite, ReLU^2 of a finite value is no NaN, and SwiGLU of finite up and
+// gate is finite or +-0 (a large negative gate gives gate / inf = -0) or
+// +-inf, never NaN.  Larger or non-finite scales round in software.
+// smem: the ring, followed by the scale slots.
 template <class C, int MODE, int EPI, bool MASK = false, class E>
 __device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                               const float (&sa)[4]) {
@@ -558,24 +604,23 @@ __device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint
     return;
   }
   uint2 sb[4][4];
-  mfma32_load_b_scales<C, MASK>(e, o, n0, sb);
+  mfma32_read_b_scales<C>(e, smem + E::LDS_BYTES + 256 * e.wave, sb);
   if constexpr (MODE == OUT_F32) {
     f6_epilogue<C, OUT_F32, EPI, false, MASK>(e, o, m0, n0, sa, sb);
-  } else if constexpr (C::SWIGLU) {
-    mfma32_epilogue_lds<C, EPI_NONE, false, MASK>(e, o, smem, m0, n0, sa, sb);
   } else {
-    bool finite = true;
+    constexpr uint32_t F32_LIM = (127u + 48u) << 23, BF16_LIM = (127u + 48u) << 7;
+    bool bounded = true;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) finite = finite && (__float_as_uint(sa[i]) & 0x7F800000u) != 0x7F800000u;
+    for (int i = 0; i < 4; ++i) bounded = bounded && (__float_as_uint(sa[i]) & 0x7F800000u) < F32_LIM;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint2 w = sb[j][q];
-        finite = finite && (w.x & 0x7F80u) != 0x7F80u && (w.x & 0x7F800000u) != 0x7F800000u &&
-                 (w.y & 0x7F80u) != 0x7F80u && (w.y & 0x7F800000u) != 0x7F800000u;
+        bounded = bounded && (w.x & 0x7F80u) < BF16_LIM && (w.x & 0x7F800000u) < (BF16_LIM << 16) &&
+                  (w.y & 0x7F80u) < BF16_LIM && (w.y & 0x7F800000u) < (BF16_LIM << 16);
       }
-    if (__all(finite)) mfma32_epilogue_lds<C, EPI, true, MASK>(e, o, smem, m0, n0, sa, sb);
+    if (__all(bounded)) mfma32_epilogue_lds<C, EPI, true, MASK>(e, o, smem, m0, n0, sa, sb);
     else mfma32_epilogue_lds<C, EPI, false, MASK>(e, o, smem, m0, n0, sa, sb);
   }
 }
@@ -585,7 +630,7 @@ __device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint
 template <class C, int MODE, int EPI>
 __global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
   using E = F6Engine<C>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
@@ -597,8 +642,10 @@ __global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
   float sa[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
+  const OutView o = dense_view<C, MODE>(p);
+  mfma32_prefetch_b_scales<C, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
   e.run(p.K / 128);
-  mfma32_finish<C, MODE, EPI>(e, dense_view<C, MODE>(p), smem, m0, n0, sa);
+  mfma32_finish<C, MODE, EPI>(e, o, smem, m0, n0, sa);
 }
 
 }  // namespace shk

@@ -290,7 +290,7 @@ struct I8Engine {
 template <class C, int MODE, int EPI>
 __global__ __launch_bounds__(256) void i8_gemm_kernel(const DenseArgs p) {
   using E = I8Engine<C>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
@@ -302,8 +302,10 @@ __global__ __launch_bounds__(256) void i8_gemm_kernel(const DenseArgs p) {
   float sa[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
+  const OutView o = dense_view<C, MODE>(p);
+  mfma32_prefetch_b_scales<C, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
   e.run(p.K / 64);
-  mfma32_finish<C, MODE, EPI>(e, dense_view<C, MODE>(p), smem, m0, n0, sa);
+  mfma32_finish<C, MODE, EPI>(e, o, smem, m0, n0, sa);
 }
 
 }  // namespace shk

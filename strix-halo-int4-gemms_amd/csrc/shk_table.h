@@ -127,13 +127,15 @@ Entry dense_entry(int layout, int group_m) {
 template <class C>
 Entry i8_entry(int layout, int group_m) {
   static_assert(C::LDS_BYTES == I8Engine<C>::LDS_BYTES && C::NUM_STAGES == I8Engine<C>::P, "table geometry");
-  return Entry{desc_of<C>(SHK_FAMILY_DENSE, layout, group_m), &launch_i8_t<C>, nullptr, nullptr, nullptr};
+  shk_kernel_desc d = desc_of<C>(SHK_FAMILY_DENSE, layout, group_m);
+  d.lds_bytes += MFMA32_SCALE_BYTES;
+  return Entry{d, &launch_i8_t<C>, nullptr, nullptr, nullptr};
 }
 template <class C>
 Entry f6_entry(int layout) {
   shk_kernel_desc d = desc_of<C>(SHK_FAMILY_DENSE, layout, 8);
   d.num_stages = F6Engine<C>::P;
-  d.lds_bytes = F6Engine<C>::LDS_BYTES;
+  d.lds_bytes = F6Engine<C>::LDS_BYTES + MFMA32_SCALE_BYTES;
   d.operand_format = SHK_OPERANDS_FP6;
   return Entry{d, &launch_f6_t<C>, nullptr, nullptr, &launch_f6_gemm_t<C>};
 }
