@@ -259,6 +259,34 @@ def test_special_scale_values_store_like_torch(kernel, device):
         assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("kernel", [k for k in shk.default_registry.all() if k.epilogue is shk.Epilogue.SWIGLU
+                                    and k.scale.mode is shk.ScaleMode.PER_CHANNEL and k.layout is shk.GemmLayout.NN],
+                         ids=lambda k: k.kernel_id)
+def test_swiglu_gates_on_both_sides_of_the_fast_range(kernel, device):
+    """SwiGLU takes the hardware exp2 / reciprocal path for a wave's group of
+    outputs only when every gate of the group has |gate| <= 80, and the exact
+    path otherwise.  Rows 0..255 get small A scales, so their tiles hold only
+    small gates (the fast path); below them the gates straddle 80 (mostly the
+    exact path, including large negative gates, whose outputs underflow
+    towards zero).  Every output stays within the bf16 tolerance."""
+    bits, layout, _, _ = _kernel_params(kernel)
+    m, n = 512, 256
+    k, lo, hi = (1024, 0.1, 0.6) if bits == 4 else (256, 0.01, 0.05)
+    seed = stable_seed("swiglu-range", kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=None,
+                                                 swiglu=True, scale_lo=lo, scale_hi=hi)
+    sa[:256] = ref.uniform_bf16(ref.rng(seed + 1), (256,), lo / 20, lo / 10)
+    gate = np.abs(ref.scaled_mm(a_q, b_q, sa, sb, subchannel=None)[:, n:])
+    assert gate[:256].max() <= 80.0, "rows 0..255 must hold only small gates"
+    assert 0.1 < np.mean(gate[256:] > 80.0) < 0.9, "rows 256.. must put gates on both sides of 80"
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q))
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=bits, layout=layout, a_scale=sa, b_scale=sb,
+                                   subchannel=None, epilogue="swiglu")
+    assert max_ulp(got, want) <= ULP_TOL
+
+
 _FP6 = [k for k in shk.default_registry.all()
         if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.epilogue is not shk.Epilogue.RELU2
         and k.scale.mode is shk.ScaleMode.PER_CHANNEL]
