@@ -150,6 +150,9 @@ struct F6Engine {
   __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
   // the exact integer sum of accumulator register x of [i][j], as fp32 / int32
   __device__ __forceinline__ float acc_value(int i, int j, int x) const { return acc[i][j][x] * F6_UNSCALE; }
+  // the accumulator as held (the sum / 64) and the power of two restoring it
+  static constexpr float UNSCALE = F6_UNSCALE;
+  __device__ __forceinline__ float acc_stored(int i, int j, int x) const { return acc[i][j][x]; }
   __device__ __forceinline__ int acc_int(int i, int j, int x) const { return (int)(acc[i][j][x] * F6_UNSCALE); }
 
   // a6 / b6: block-format operands; the tile's first panels are m0 / 32 and
@@ -461,6 +464,15 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
   constexpr int UNITS = E::TN / 8;
   constexpr int PITCH = 16 * UNITS;
   auto swz = [](int r) { return UNITS == 16 ? (r & 15) : ((r >> 1) & 7); };
+  // With bounded scales (NO_NAN) the engine's power-of-two factor folds into
+  // the A scale: UNSCALE * sa is exact below 2^48, so stored * (UNSCALE * sa)
+  // is the same real product as (stored * UNSCALE) * sa and rounds alike.
+  float sx[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sx[i] = NO_NAN ? sa[i] * E::UNSCALE : sa[i];
+  auto scaled = [&](int i, int j, int x) {
+    return (NO_NAN ? e.acc_stored(i, j, x) : e.acc_value(i, j, x)) * sx[i];
+  };
   // every wave has finished reading the ring
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   uint8_t* region = smem + (size_t)e.wave * 128 * PITCH;
@@ -485,9 +497,9 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            up[i][t] = e.acc_value(i, j, 4 * q + t) * sa[i];
+            up[i][t] = scaled(i, j, 4 * q + t);
             up[i][t] = up[i][t] * su[t];
-            gt[i][t] = e.acc_value(i, j + 2, 4 * q + t) * sa[i];
+            gt[i][t] = scaled(i, j + 2, 4 * q + t);
             gt[i][t] = gt[i][t] * sg[t];
             gmax = __builtin_fmaxf(gmax, __builtin_fabsf(gt[i][t]));
           }
@@ -510,7 +522,7 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            float x = e.acc_value(i, j, 4 * q + t) * sa[i];
+            float x = scaled(i, j, 4 * q + t);
             x = x * su[t];
             if constexpr (EPI == EPI_RELU2) x = apply_epi(x, EPI_RELU2);
             v[i][t] = x;

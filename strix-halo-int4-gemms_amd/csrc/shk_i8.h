@@ -71,6 +71,8 @@ struct I8Engine {
   __device__ __forceinline__ int out_row(int i) const { return wm * 128 + 32 * i + (lane & 31); }
   __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
   __device__ __forceinline__ float acc_value(int i, int j, int x) const { return (float)acc[i][j][x]; }
+  static constexpr float UNSCALE = 1.0f;
+  __device__ __forceinline__ float acc_stored(int i, int j, int x) const { return (float)acc[i][j][x]; }
   __device__ __forceinline__ int acc_int(int i, int j, int x) const { return acc[i][j][x]; }
 
   // K-major read base of step s (fragment rows are a multiple of 32, so the
