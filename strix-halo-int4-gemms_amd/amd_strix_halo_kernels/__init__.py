@@ -49,6 +49,7 @@ from .ragged import (
     ragged_dot_int4_bwd,
 )
 from .registry import KernelRegistry, default_registry
+from .torch_ops import TORCH_GEMM_OP, TORCH_OP_NAMESPACE, register_torch_ops, torch_gemm
 
 __all__ = [
     "ACC_DTYPE",
@@ -72,6 +73,8 @@ __all__ = [
     "SUPPORTED_SUBCHANNELS",
     "ScaleMode",
     "ScaleSpec",
+    "TORCH_GEMM_OP",
+    "TORCH_OP_NAMESPACE",
     "TileConfig",
     "calculate_group_info",
     "default_registry",
@@ -89,6 +92,8 @@ __all__ = [
     "ragged_dot_int4",
     "ragged_dot_int4_bwd",
     "reference_mm",
+    "register_torch_ops",
     "tops_for_runtime",
+    "torch_gemm",
     "unpack_int4_k_major",
 ]

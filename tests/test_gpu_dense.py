@@ -388,3 +388,38 @@ def test_fp6_converted_operands_are_reusable(layout, epilogue, device):
         direct = shk.explicit_mm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
         torch.cuda.synchronize()
         assert np.array_equal(bf16_bits(torch, out), bf16_bits(torch, direct))
+
+
+def _one_kernel_per_family():
+    seen, out = set(), []
+    for kernel in shk.default_registry.all():
+        key = (kernel.a_dtype, kernel.layout, kernel.epilogue, kernel.scale.mode)
+        if key not in seen:
+            seen.add(key)
+            out.append(kernel)
+    return out
+
+
+@pytest.mark.parametrize("kernel", _one_kernel_per_family(), ids=lambda k: k.kernel_id)
+def test_torch_gemm_custom_op_matches_explicit_mm(kernel, device):
+    """torch_gemm (the registered custom op, reference torch_ops.py) gives the
+    bits of explicit_mm, eagerly and traced by torch.compile through the fake
+    implementation (reference tests/test_native_generated.py:118-140)."""
+    bits, layout, sub, epi = _kernel_params(kernel)
+    shape = representative_generation_shape(kernel)
+    seed = stable_seed("custom-op", kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=shape.m, n=shape.n, k=shape.k,
+                                                 subchannel=sub, swiglu=epi == "swiglu")
+    a, b = to_dev(torch, a_arg, device), to_dev(torch, b_arg, device)
+    ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
+    print(f"case {kernel.kernel_id} shape=({shape.m},{shape.n},{shape.k})", flush=True)
+    want = shk.explicit_mm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    got = shk.torch_gemm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    torch._dynamo.reset()  # each case compiles the same lambda for another kernel
+    traced = torch.compile(lambda *t: shk.torch_gemm(t[0], t[1], kernel=kernel, a_scale=t[2], b_scale=t[3]),
+                           backend="eager", fullgraph=True)(a, b, ta, tb)
+    torch.cuda.synchronize()
+    for out in (got, traced):
+        assert out.dtype == want.dtype and tuple(out.shape) == tuple(want.shape)
+        assert torch.equal(out.view(torch.int16) if out.dtype == torch.bfloat16 else out,
+                           want.view(torch.int16) if want.dtype == torch.bfloat16 else want)

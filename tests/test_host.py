@@ -328,3 +328,44 @@ def test_public_api_surface():
     assert shk.ARCH == "gfx950" and shk.ACC_DTYPE == "int32"
     assert shk.SUPPORTED_SUBCHANNELS == (32, 64, 128, 256)
     assert [layout.value for layout in shk.SUPPORTED_GEMM_LAYOUTS] == ["nn", "nt", "tn"]
+
+
+# ---------------------------------------------------------------------------
+# torch custom op (torch_ops.py of the reference)
+
+
+def _logical_operand_shapes(kernel, m, n, k):
+    packed = kernel.a_dtype is shk.OperandDType.INT4
+    kk = k // 2 if packed else k
+    b_cols = 2 * n if kernel.epilogue is shk.Epilogue.SWIGLU else n
+    a_shape = (kk, m) if kernel.layout is shk.GemmLayout.TN else (m, kk)
+    b_shape = (b_cols, kk) if kernel.layout is shk.GemmLayout.NT else (kk, b_cols)
+    return a_shape, b_shape, torch.uint8 if packed else torch.int8
+
+
+def test_torch_op_registers_once_and_fakes_every_layout():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    shk.register_torch_ops()
+    shk.register_torch_ops()
+    assert shk.TORCH_GEMM_OP == "amd_strix_halo_kernels::gemm"
+    assert hasattr(torch.ops.amd_strix_halo_kernels, "gemm")
+    seen = set()
+    for kernel in shk.default_registry.all():
+        key = (kernel.a_dtype, kernel.layout, kernel.epilogue, kernel.scale.mode)
+        if key in seen:
+            continue
+        seen.add(key)
+        shape = representative_generation_shape(kernel)
+        m, n, k = shape.m, shape.n, shape.k
+        a_shape, b_shape, dtype = _logical_operand_shapes(kernel, m, n, k)
+        with FakeTensorMode():
+            a = torch.empty(a_shape, device="cuda", dtype=dtype)
+            b = torch.empty(b_shape, device="cuda", dtype=dtype)
+            sa = torch.empty((m,), device="cuda", dtype=torch.bfloat16)
+            sb = torch.empty((n,), device="cuda", dtype=torch.bfloat16)
+            out = shk.torch_gemm(a, b, kernel=kernel, a_scale=sa, b_scale=sb)
+            assert tuple(out.shape) == (m, n), kernel.kernel_id
+            want = torch.bfloat16 if kernel.output_dtype == "bfloat16" else torch.float32
+            assert out.dtype == want and out.device.type == "cuda", kernel.kernel_id
+    assert len(seen) >= 8
