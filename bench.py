@@ -5,7 +5,8 @@ M=N=K=8192 (config C2) through ``amd_strix_halo_kernels.mm``, as a fraction of
 the gfx950 dense int8 MFMA peak.  Secondary lines in the same JSON object:
 C3 (int4 subchannel-256 ReLU2, 4096x16384x4096), C4 (int8 fused SwiGLU,
 4096 x 11008 x 4096, TOPS count up + gate) and C5 (ragged MoE forward and
-K-ragged backward, G=8, M=8192, K=2048, N=1408).
+K-ragged backward, G=8, M=8192, K=2048, N=1408), and the device
+quantize-and-pack of a C2-sized bf16 operand (GB/s against HBM).
 
     python bench.py [--steps K] [--warmup W] [--no-secondary] [--no-cpu-baseline]
 
@@ -212,6 +213,32 @@ def bench_c4(torch, shk, steps, warmup):
             "frac_int8_peak": ops / (kern * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS}
 
 
+def bench_quant(torch, shk, steps, warmup):
+    """Device fake quantization + int4 packing of a C2-sized bf16 operand
+    (8192 x 8192), along each axis, against the HBM roofline: algorithmic
+    bytes = 2 per value read + 0.5 per value written.  The reference's torch
+    formulas (fake_quant_int then pack_int4_k_major, several element-wise
+    launches with int8/int16 intermediates) run on the same tensor beside it."""
+    m = n = 8192
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    x = (torch.randn((m, n), generator=gen, device="cuda") * 0.05).to(torch.bfloat16)
+    nbytes = m * n * 2 + m * n // 2
+    out = {}
+    for axis in (-1, -2):
+        _, kern, _ = _time_steps(torch, lambda: shk.quantize_pack_int4(x, scale=0.01, axis=axis), steps, warmup)
+        gbs = nbytes / (kern * 1e-3) / 1e9
+        out[f"axis{axis}"] = {"kernel_ms": kern, "gbs": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+    def torch_formulas():
+        q = torch.clamp(torch.round(x.float() / 0.01), -8, 7).to(torch.int8)
+        return ((q[:, 1::2].to(torch.int16) & 0xF) << 4 | (q[:, 0::2].to(torch.int16) & 0xF)).to(torch.uint8)
+
+    _, kern, _ = _time_steps(torch, torch_formulas, max(3, steps // 4), 2)
+    out["torch_formulas_axis-1_ms"] = kern
+    out["bytes"] = nbytes
+    return out
+
+
 def _multinomial_sizes(torch, rows, groups, seed):
     g = torch.Generator().manual_seed(seed)
     # Dirichlet(1) = normalised exponentials; multinomial counts; then the
@@ -370,6 +397,9 @@ def main(argv=None) -> int:
         secondary["c4_int8_swiglu_4096x11008x4096"] = bench_c4(torch, shk, max(10, args.steps // 2), args.warmup)
         _log("bench: C5 ragged fwd/bwd")
         secondary["c5_ragged_g8_m8192_k2048_n1408"] = bench_c5(torch, shk, max(10, args.steps // 2), args.warmup)
+        _log("bench: device quantize + int4 pack, 8192x8192 bf16")
+        secondary["quantize_pack_int4_8192x8192_bf16"] = bench_quant(torch, shk, max(10, args.steps // 2),
+                                                                     args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         _log("bench: CPU baseline (C oracle)")

@@ -71,6 +71,18 @@ extern "C" {
 #define SHK_OPERANDS_PACKED 0
 #define SHK_OPERANDS_FP6 1
 
+/* Sources of amd_strix_halo_kernels_quantize: float values to quantize, or
+ * existing int8 codes to pack. */
+#define SHK_SRC_F32 0
+#define SHK_SRC_F16 1
+#define SHK_SRC_BF16 2
+#define SHK_SRC_I8 3
+
+/* Outputs of amd_strix_halo_kernels_quantize. */
+#define SHK_QUANT_CODES 0     /* int8 codes, rows x cols */
+#define SHK_QUANT_PACK_COLS 1 /* int4 pairs along each row: rows x ceil(cols/2) bytes */
+#define SHK_QUANT_PACK_ROWS 2 /* int4 pairs of rows 2r, 2r+1: ceil(rows/2) x cols bytes */
+
 typedef struct shk_kernel_desc {
   int32_t index;
   int32_t family;          /* SHK_FAMILY_* */
@@ -269,6 +281,26 @@ int amd_strix_halo_kernels_launch_ragged_bwd_ws(int kernel_index, int device_ind
                                                 void* out, int32_t m, int32_t n, int32_t k_packed,
                                                 int32_t groups, int32_t subchannel, int32_t split_k,
                                                 int32_t out_mode, void* workspace, uint64_t workspace_bytes);
+
+/* Fake quantization and int4 packing on the device, in one pass over HBM.
+ * No counterpart in the reference's dispatcher: its quant.py:14-51
+ * (fake_quant_int, pack_int4_k_major) does this with torch element-wise ops,
+ * which this replaces for device tensors.
+ * x holds rows x cols values (row pitch ld_x elements) of type `src`.
+ * For a float source the code of value v is
+ *   clamp(rint(v * inv_scale), -2^(bits-1), 2^(bits-1) - 1)
+ * with rint rounding half to even and NaN giving 0, which is what torch's
+ * clamp(round(x.float() / scale)).to(int8) computes on the GPU: it divides
+ * by a Python scalar by multiplying with its reciprocal, rounded once to
+ * fp32 from double, so the caller passes inv_scale = (float)(1.0 / scale).
+ * For SHK_SRC_I8 the codes are the source bytes, packed as given (their low
+ * nibbles), as pack_int4_k_major does; bits must be 4 and mode a PACK mode.
+ * PACK modes put the even element in the low nibble and the odd one in the
+ * high nibble; an odd count pads with a zero element.  out has row pitch
+ * ld_out bytes; bits is 4 for the PACK modes and 4 or 8 for CODES. */
+int amd_strix_halo_kernels_quantize(int device_index, uintptr_t stream, const void* x, int32_t src, int64_t rows,
+                                    int64_t cols, int64_t ld_x, float inv_scale, int32_t bits, int32_t mode,
+                                    void* out, int64_t ld_out);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,28 @@ def fake_quant_int(x, *, bits: int, scale: float) -> np.ndarray:
     return np.clip(q, qmin, qmax).astype(np.int8)
 
 
+def fake_quant_int_device(x, *, bits: int, scale: float) -> np.ndarray:
+    """fake_quant_int (quant.py:14-29) as torch evaluates it on a GPU.
+
+    There ``x.float() / scale`` with a Python scalar multiplies by the
+    reciprocal of the scale, rounded once from double to float32 (measured on
+    MI355X, torch 2.10: bit-identical to ``x * float32(1.0 / scale)`` for
+    every value and scale tried, where ``x / float32(scale)`` and
+    ``x * (1 / float32(scale))`` both differ); then round half to even and
+    clamp as on the CPU, and NaN converts to the code 0.
+    """
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
+    if isinstance(scale, bool) or not isinstance(scale, (int, float)) or scale <= 0:
+        raise ValueError("scale must be a positive Python int or float scalar")
+    qmin = -(1 << (bits - 1))
+    qmax = (1 << (bits - 1)) - 1
+    with np.errstate(invalid="ignore", over="ignore"):
+        q = np.rint(np.asarray(x, dtype=np.float32) * np.float32(1.0 / scale))
+        q = np.clip(q, qmin, qmax)
+    return np.where(np.isnan(q), 0, q).astype(np.int8)
+
+
 def pack_int4_k_major(x) -> np.ndarray:
     """Packs pairs along the last axis: byte = (odd << 4) | (even & 0xF),
     zero-padding an odd length (quant.py:32-38)."""

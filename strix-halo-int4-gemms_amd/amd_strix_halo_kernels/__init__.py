@@ -38,6 +38,7 @@ from .quant import (
     pack_int4_k_major,
     pack_ragged_rhs_subchannel_scales,
     pack_rhs_subchannel_scales,
+    quantize_pack_int4,
     unpack_int4_k_major,
 )
 from .ragged import (
@@ -89,6 +90,7 @@ __all__ = [
     "pack_int4_k_major",
     "pack_ragged_rhs_subchannel_scales",
     "pack_rhs_subchannel_scales",
+    "quantize_pack_int4",
     "ragged_dot_int4",
     "ragged_dot_int4_bwd",
     "reference_mm",

@@ -46,6 +46,15 @@ OPERANDS_PACKED = 0
 OPERANDS_FP6 = 1
 FP6_MAX_K = 262144
 
+# Device quantization (amd_strix_halo_kernels_quantize): sources and outputs.
+SRC_F32 = 0
+SRC_F16 = 1
+SRC_BF16 = 2
+SRC_I8 = 3
+QUANT_CODES = 0
+QUANT_PACK_COLS = 1
+QUANT_PACK_ROWS = 2
+
 
 @dataclass(frozen=True)
 class KernelDesc:

@@ -106,6 +106,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_launch_ragged_bwd_ws.argtypes = [I, I, U, P, P, P, P, P, P, I32, I32, I32, I32, I32,
                                                                 I32, I32, P, ctypes.c_uint64]
     lib.amd_strix_halo_kernels_launch_ragged_bwd_ws.restype = I
+    I64 = ctypes.c_int64
+    lib.amd_strix_halo_kernels_quantize.argtypes = [I, U, P, I32, I64, I64, I64, ctypes.c_float, I32, I32, P, I64]
+    lib.amd_strix_halo_kernels_quantize.restype = I
 
 
 def load_dispatch_library(path: str | Path | None = None) -> ctypes.CDLL:
@@ -437,6 +440,54 @@ def launch_generated_kernel_i32(
     c = torch.empty((m, cols), device=a.device, dtype=torch.int32)
     _gemm_call(torch, a, b, a_scale, b_scale, c, kernel, m, n, k, kt.OUT_I32, library_path, stream)
     return c
+
+
+# ---------------------------------------------------------------------------
+# Device quantization and int4 packing
+
+
+def _quant_source(torch: Any, x: Any) -> int:
+    codes = {torch.float32: kt.SRC_F32, torch.float16: kt.SRC_F16, torch.bfloat16: kt.SRC_BF16,
+             torch.int8: kt.SRC_I8}
+    if x.dtype not in codes:
+        raise ValueError(f"device quantization reads float32, float16, bfloat16 or int8 tensors; got {x.dtype}")
+    return codes[x.dtype]
+
+
+def quantize_device(x: Any, *, mode: int, bits: int = 4, inv_scale: float = 1.0, library_path=None,
+                    stream: Any | None = None) -> Any:
+    """Runs amd_strix_halo_kernels_quantize over the rows of a 2-D CUDA tensor
+    whose rows are contiguous (x.stride(1) == 1): int8 codes (QUANT_CODES),
+    int4 pairs along each row (QUANT_PACK_COLS, [rows, ceil(cols/2)] uint8) or
+    int4 pairs of consecutive rows (QUANT_PACK_ROWS, [ceil(rows/2), cols]
+    uint8).  inv_scale is the fp32 reciprocal of the scale (unused for int8
+    sources, which are packed as given)."""
+    torch = _torch()
+    if x.dim() != 2:
+        raise ValueError(f"device quantization takes a 2-D tensor; got {x.dim()} dimensions")
+    if x.device.type != "cuda":
+        raise ValueError("device quantization requires a CUDA tensor")
+    if x.numel() > 0 and (x.stride(1) != 1 or (x.shape[0] > 1 and x.stride(0) < x.shape[1])):
+        x = x.contiguous()
+    src = _quant_source(torch, x)
+    rows, cols = int(x.shape[0]), int(x.shape[1])
+    if mode == kt.QUANT_CODES:
+        out = torch.empty((rows, cols), device=x.device, dtype=torch.int8)
+    elif mode == kt.QUANT_PACK_COLS:
+        out = torch.empty((rows, (cols + 1) // 2), device=x.device, dtype=torch.uint8)
+    elif mode == kt.QUANT_PACK_ROWS:
+        out = torch.empty(((rows + 1) // 2, cols), device=x.device, dtype=torch.uint8)
+    else:
+        raise ValueError(f"unknown quantize mode {mode}")
+    if out.numel() == 0:
+        return out
+    lib = _verified_library(library_path)
+    ld_x = int(x.stride(0)) if rows > 1 else cols
+    rc = lib.amd_strix_halo_kernels_quantize(_device_index(x), _stream_handle(torch, x, stream), x.data_ptr(), src,
+                                             rows, cols, ld_x, float(inv_scale), bits, mode, out.data_ptr(),
+                                             int(out.shape[1]))
+    _check(lib, rc)
+    return out
 
 
 # ---------------------------------------------------------------------------

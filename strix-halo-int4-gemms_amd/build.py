@@ -66,6 +66,7 @@ def translation_units() -> list[tuple[str, Path, list[str]]]:
     units.append(("dense_f6", CSRC / "k_f6.hip", list(DMA_FLAGS)))
     units.append(("f6pack", CSRC / "k_f6pack.hip", []))
     units.append(("ragged_f6", CSRC / "k_f6ragged.hip", list(DMA_FLAGS)))
+    units.append(("quant", CSRC / "k_quant.hip", []))
     for layout in (0, 1, 2, 3):
         units.append((f"ragged_{layout}", CSRC / "k_ragged.hip", [f"-DSHK_LAYOUT={layout}"]))
     units.append(("capi", CSRC / "capi.hip", []))

@@ -6,6 +6,7 @@
 #include <string>
 #include <vector>
 
+#include "shk_quant.h"
 #include "shk_table.h"
 
 namespace {
@@ -573,6 +574,33 @@ int amd_strix_halo_kernels_launch_ragged_bwd_ws(int kernel_index, int device_ind
     err = shk::launch_bwd_finalize(static_cast<float*>(out), p.a_scale, p.b_scale, groups, m, n, s);
     if (err != hipSuccess) return fail_hip("ragged backward finalize launch", err);
   }
+  return 0;
+}
+
+int amd_strix_halo_kernels_quantize(int device_index, uintptr_t stream, const void* x, int32_t src, int64_t rows,
+                                    int64_t cols, int64_t ld_x, float inv_scale, int32_t bits, int32_t mode,
+                                    void* out, int64_t ld_out) {
+  g_last_error.clear();
+  if (src < SHK_SRC_F32 || src > SHK_SRC_I8) return fail("unknown source type " + std::to_string(src));
+  if (mode < SHK_QUANT_CODES || mode > SHK_QUANT_PACK_ROWS) return fail("unknown quantize mode " + std::to_string(mode));
+  if (bits != 4 && bits != 8) return fail("bits must be 4 or 8");
+  if (mode != SHK_QUANT_CODES && bits != 4) return fail("only int4 codes are packed (bits must be 4)");
+  if (src == SHK_SRC_I8 && mode == SHK_QUANT_CODES) return fail("int8 sources are codes already; pack them");
+  if (src != SHK_SRC_I8 && !(inv_scale > 0.0f)) return fail("inv_scale must be positive");
+  if (rows < 0 || cols < 0) return fail("rows and cols must be non-negative");
+  const int64_t out_rows = mode == SHK_QUANT_PACK_ROWS ? (rows + 1) / 2 : rows;
+  const int64_t out_cols = mode == SHK_QUANT_PACK_COLS ? (cols + 1) / 2 : cols;
+  if (ld_x < cols) return fail("ld_x must be at least cols");
+  if (ld_out < out_cols) return fail("ld_out must be at least the output row length");
+  if (rows == 0 || cols == 0) return 0;
+  if (x == nullptr || out == nullptr) return fail("x and out pointers must be non-null");
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const shk::QuantArgs p{x,        static_cast<uint8_t*>(out), rows, cols, ld_x, ld_out, out_rows, out_cols,
+                         inv_scale, bits,                       src,  mode};
+  const hipError_t err = shk::launch_quantize(p, reinterpret_cast<hipStream_t>(stream));
+  if (err == hipErrorInvalidValue) return fail("quantize grid is too large");
+  if (err != hipSuccess) return fail_hip("quantize launch", err);
   return 0;
 }
 

@@ -324,3 +324,35 @@ def test_fp6_ragged_eligibility():
     assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=None, fp6=True).block_m == kt.RAGGED_FP6_BLOCK_M
     assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=None).operand_format == kt.OPERANDS_PACKED
     assert kt.RAGGED_FP6_BLOCK_M not in kt.RAGGED_FWD_BLOCK_M
+
+
+def test_quantize_validates_before_launch(lib):
+    q = lib.amd_strix_halo_kernels_quantize
+
+    def call(src=kt.SRC_BF16, rows=4, cols=8, ld_x=8, inv=10.0, bits=4, mode=kt.QUANT_PACK_COLS, out=FAKE, ld_out=4,
+             x=FAKE):
+        return q(0, 0, x, src, rows, cols, ld_x, inv, bits, mode, out, ld_out)
+
+    for kwargs, msg in (
+        (dict(src=9), b"unknown source"),
+        (dict(mode=7), b"unknown quantize mode"),
+        (dict(bits=6), b"bits must be 4 or 8"),
+        (dict(bits=8), b"only int4 codes are packed"),
+        (dict(src=kt.SRC_I8, mode=kt.QUANT_CODES, ld_out=8), b"codes already"),
+        (dict(inv=0.0), b"inv_scale must be positive"),
+        (dict(inv=float("nan")), b"inv_scale must be positive"),
+        (dict(rows=-1), b"non-negative"),
+        (dict(ld_x=7), b"ld_x must be at least cols"),
+        (dict(ld_out=3), b"ld_out must be at least"),
+        (dict(mode=kt.QUANT_PACK_ROWS, ld_out=7), b"ld_out must be at least"),
+        (dict(x=None), b"non-null"),
+        (dict(out=None), b"non-null"),
+    ):
+        assert call(**kwargs) == 1, kwargs
+        assert msg in lib.amd_strix_halo_kernels_last_error(), (kwargs, lib.amd_strix_halo_kernels_last_error())
+    # nothing to do: no pointer is touched
+    assert call(rows=0, x=None, out=None) == 0
+    assert call(cols=0, ld_x=0, ld_out=0, x=None, out=None) == 0
+    # int8 codes are packed without a scale
+    assert call(src=kt.SRC_I8, inv=0.0, x=None) == 1
+    assert b"non-null" in lib.amd_strix_halo_kernels_last_error()

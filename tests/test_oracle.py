@@ -302,3 +302,25 @@ def test_c_oracle_matches_numpy_oracle():
                                        epilogue="relu2" if epi else "none")
         got = native.dense_int4_nn(ap, bp, sa, sb, m=m, n=n, k=k, subchannel=sub, epilogue=epi)
         assert np.array_equal(got, want), (sub, epi)
+
+
+def test_device_fake_quant_closed_forms():
+    """fake_quant_int_device: for power-of-two scales the reciprocal is
+    exact, so it must equal the CPU division form everywhere; ties round half
+    to even; NaN gives 0 and infinities clamp.  (Its reciprocal rule for
+    other scales is pinned against torch on the GPU, tests/test_gpu_quant.py.)"""
+    r = ref.rng(77)
+    x = (r.standard_normal(200_000) * 6).astype(np.float32)
+    ties = (np.arange(-20, 20) + 0.5).astype(np.float32)
+    for scale in (0.125, 0.5, 2.0, 1.0 / 64):
+        for bits in (4, 8):
+            assert np.array_equal(ref.fake_quant_int_device(x * scale, bits=bits, scale=scale),
+                                  ref.fake_quant_int(x * scale, bits=bits, scale=scale))
+        got = ref.fake_quant_int_device(ties * np.float32(scale), bits=8, scale=scale)
+        assert np.array_equal(got, np.rint(ties).astype(np.int8))  # half to even: 0.5 -> 0, 1.5 -> 2
+        assert np.all(got % 2 == 0)
+    special = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e30, -1e30], dtype=np.float32)
+    assert ref.fake_quant_int_device(special, bits=4, scale=0.1).tolist() == [0, 7, -8, 0, 0, 7, -8]
+    assert ref.fake_quant_int_device(special, bits=8, scale=3.0).tolist() == [0, 127, -128, 0, 0, 127, -128]
+    # the reciprocal is rounded once from double: 1/0.017 in float32 differs from 1/float32(0.017)
+    assert np.float32(1.0 / 0.017) != np.float32(1.0) / np.float32(0.017)
