@@ -213,6 +213,26 @@ def bench_c4(torch, shk, steps, warmup):
             "frac_int8_peak": ops / (kern * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS}
 
 
+def bench_c2_persistent(torch, shk, steps, warmup):
+    """C2 through mm(schedule=KernelSchedule.PERSISTENT): the same fp6 tile on
+    one workgroup per CU, each taking every 256th tile (the whole call,
+    conversions included, as `value`)."""
+    m = n = k = 8192
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    a = torch.randint(0, 256, (m, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
+    b = torch.randint(0, 256, (k // 2, n), dtype=torch.uint8, device="cuda", generator=gen)
+    sa = _uniform_bf16(torch, (m,), 0.005, 0.02, gen)
+    sb = _uniform_bf16(torch, (n,), 0.005, 0.02, gen)
+
+    def step():
+        return shk.mm(a, b, a_scale=sa, b_scale=sb, schedule=shk.KernelSchedule.PERSISTENT)
+
+    wall, kern, _ = _time_steps(torch, step, steps, warmup)
+    ops = 2 * m * n * k
+    return {"tops": ops / (wall * 1e-3) / 1e12, "wall_ms": wall, "kernel_ms": kern,
+            "frac_int8_peak": ops / (wall * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS}
+
+
 def bench_quant(torch, shk, steps, warmup):
     """Device fake quantization + int4 packing of a C2-sized bf16 operand
     (8192 x 8192), along each axis, against the HBM roofline: algorithmic
@@ -397,6 +417,9 @@ def main(argv=None) -> int:
         secondary["c4_int8_swiglu_4096x11008x4096"] = bench_c4(torch, shk, max(10, args.steps // 2), args.warmup)
         _log("bench: C5 ragged fwd/bwd")
         secondary["c5_ragged_g8_m8192_k2048_n1408"] = bench_c5(torch, shk, max(10, args.steps // 2), args.warmup)
+        _log("bench: C2 on the persistent schedule")
+        secondary["c2_persistent_schedule_8192_cubed"] = bench_c2_persistent(torch, shk, max(10, args.steps // 2),
+                                                                            args.warmup)
         _log("bench: device quantize + int4 pack, 8192x8192 bf16")
         secondary["quantize_pack_int4_8192x8192_bf16"] = bench_quant(torch, shk, max(10, args.steps // 2),
                                                                      args.warmup)

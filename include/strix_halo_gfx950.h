@@ -71,6 +71,14 @@ extern "C" {
 #define SHK_OPERANDS_PACKED 0
 #define SHK_OPERANDS_FP6 1
 
+/* Tile schedules of a dense entry (reference metadata.KernelSchedule,
+ * metadata.py:51-53).  STANDARD launches one workgroup per output tile;
+ * PERSISTENT launches one workgroup per resident slot (occupancy x CUs,
+ * a multiple of 8 so each workgroup keeps its XCD, at most the tile count),
+ * each taking every gridDim-th tile in the same XCD-aware order. */
+#define SHK_SCHEDULE_STANDARD 0
+#define SHK_SCHEDULE_PERSISTENT 1
+
 /* Sources of amd_strix_halo_kernels_quantize: float values to quantize, or
  * existing int8 codes to pack. */
 #define SHK_SRC_F32 0
@@ -100,6 +108,7 @@ typedef struct shk_kernel_desc {
   int32_t lds_bytes;       /* LDS per workgroup */
   int32_t group_size_m;    /* tile-row swizzle width (dense) */
   int32_t operand_format;  /* SHK_OPERANDS_* */
+  int32_t schedule;        /* SHK_SCHEDULE_* */
 } shk_kernel_desc;
 
 /* ---- status (reference dispatch.cpp:206-222) ---------------------------- */

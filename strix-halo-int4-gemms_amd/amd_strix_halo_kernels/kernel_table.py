@@ -46,6 +46,11 @@ OPERANDS_PACKED = 0
 OPERANDS_FP6 = 1
 FP6_MAX_K = 262144
 
+# Tile schedules (reference metadata.KernelSchedule): STANDARD launches one
+# workgroup per tile, PERSISTENT one per resident slot, striding over tiles.
+SCHEDULE_STANDARD = 0
+SCHEDULE_PERSISTENT = 1
+
 # Device quantization (amd_strix_halo_kernels_quantize): sources and outputs.
 SRC_F32 = 0
 SRC_F16 = 1
@@ -76,6 +81,7 @@ class KernelDesc:
     lds_bytes: int
     group_size_m: int
     operand_format: int = OPERANDS_PACKED
+    schedule: int = SCHEDULE_STANDARD
 
     @property
     def needs_workspace(self) -> bool:
@@ -113,7 +119,7 @@ MFMA32_SCALE_BYTES = 4 * 256
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
-          fp6=False, fp6_sub=False):
+          fp6=False, fp6_sub=False, schedule=SCHEDULE_STANDARD):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
@@ -148,6 +154,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         lds_bytes=lds,
         group_size_m=group_m,
         operand_format=OPERANDS_FP6 if fp6 else OPERANDS_PACKED,
+        schedule=schedule,
     )
 
 
@@ -189,6 +196,13 @@ def _build() -> tuple[KernelDesc, ...]:
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1, bm=128, bn=128,
                 bk=128, wm=2, wn=2)
+    # persistent int4 entries (plain epilogue kind) after the ragged families
+    for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
+        d = dict(family=FAMILY_DENSE, bits=4, layout=layout, schedule=SCHEDULE_PERSISTENT)
+        add(**d, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
+        add(**d, bm=128, bn=128, bk=128, wm=2, wn=2, subch=True, fp6_sub=True)
+        add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True)
+        add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True, mk=32)
     return tuple(out)
 
 
@@ -203,7 +217,7 @@ def measured_tops(desc: KernelDesc) -> float | None:
     int4 subchannel 128x128 (C3), int8 32x32 SwiGLU 256x128 (C4, 4096 x
     2*11008 x 4096) and int8 plain 256x256 (8192^3).  Other entries have no
     measurement and rank by tile area."""
-    if desc.family != FAMILY_DENSE:
+    if desc.family != FAMILY_DENSE or desc.schedule != SCHEDULE_STANDARD:
         return None
     if desc.operand_format == OPERANDS_FP6:
         if desc.scale_mode == SCALE_SUBCHANNEL:

@@ -44,7 +44,7 @@ class _Desc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "index", "family", "dtype_bits", "layout", "scale_mode", "min_subchannel", "max_subchannel",
         "epilogue_kind", "block_m", "block_n", "block_k", "num_waves", "num_stages", "lds_bytes",
-        "group_size_m", "operand_format")]
+        "group_size_m", "operand_format", "schedule")]
 
 
 @functools.lru_cache(maxsize=None)

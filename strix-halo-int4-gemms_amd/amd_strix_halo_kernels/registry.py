@@ -66,6 +66,8 @@ def _scales_of(desc: kt.KernelDesc) -> tuple[ScaleSpec, ...]:
 def _epilogues_of(desc: kt.KernelDesc) -> tuple[Epilogue, ...]:
     if desc.epilogue_kind == kt.EPI_KIND_SWIGLU:
         return (Epilogue.SWIGLU,)
+    if desc.schedule == kt.SCHEDULE_PERSISTENT:
+        return (Epilogue.NONE,)  # the reference's persistent kernels (registry.py:230-251)
     return (Epilogue.NONE, Epilogue.RELU2)
 
 
@@ -77,7 +79,9 @@ def iter_supported_kernel_metadata() -> Iterable[KernelMetadata]:
         layout = _LAYOUT_OF_CODE[desc.layout]
         for scale in _scales_of(desc):
             for epilogue in _epilogues_of(desc):
-                kernel_id = make_kernel_id(dtype, scale, epilogue, tile, arch=ARCH, layout=layout)
+                schedule = (KernelSchedule.PERSISTENT if desc.schedule == kt.SCHEDULE_PERSISTENT
+                            else KernelSchedule.STANDARD)
+                kernel_id = make_kernel_id(dtype, scale, epilogue, tile, arch=ARCH, layout=layout, schedule=schedule)
                 yield KernelMetadata(
                     kernel_id=kernel_id,
                     arch=ARCH,
@@ -91,7 +95,7 @@ def iter_supported_kernel_metadata() -> Iterable[KernelMetadata]:
                     tile=tile,
                     triton_kernel_name=f"shk::dense_gemm_kernel#{desc.index}",
                     layout=layout,
-                    schedule=KernelSchedule.STANDARD,
+                    schedule=schedule,
                     assembly_path=None,
                     status=KernelStatus.COMPILED,
                     table_index=desc.index,

@@ -3,11 +3,49 @@
 // reference interface each symbol replaces are in include/strix_halo_gfx950.h.
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "shk_quant.h"
 #include "shk_table.h"
+
+namespace shk {
+
+// Resident workgroups of a persistent launch, cached per (kernel, device):
+// the occupancy query walks the kernel's resource use on the host.
+hipError_t persistent_grid(const void* kernel, int block, unsigned tiles, unsigned* grid) {
+  struct Slot {
+    const void* kernel;
+    int device, block;
+    unsigned slots;
+  };
+  static std::mutex lock;
+  static std::vector<Slot> cache;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  unsigned slots = 0;
+  {
+    std::lock_guard<std::mutex> g(lock);
+    for (const Slot& c : cache)
+      if (c.kernel == kernel && c.device == dev && c.block == block) slots = c.slots;
+  }
+  if (slots == 0) {
+    int cus = 0, occ = 0;
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err == hipSuccess) err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, block, 0);
+    if (err != hipSuccess) return err;
+    slots = (unsigned)(cus > 0 ? cus : 1) * (unsigned)(occ > 0 ? occ : 1);
+    if (slots >= 8) slots &= ~7u;  // a workgroup keeps its XCD across its tiles
+    std::lock_guard<std::mutex> g(lock);
+    cache.push_back(Slot{kernel, dev, block, slots});
+  }
+  *grid = slots < tiles ? slots : tiles;
+  return hipSuccess;
+}
+
+}  // namespace shk
 
 namespace {
 
@@ -48,6 +86,12 @@ const std::vector<Entry>& table() {
     shk::append_ragged_1(v);
     shk::append_ragged_2(v);
     shk::append_ragged_3(v);
+    shk::append_persistent_f6(v, SHK_LAYOUT_NN);
+    shk::append_persistent_4_0(v);
+    shk::append_persistent_f6(v, SHK_LAYOUT_NT);
+    shk::append_persistent_4_1(v);
+    shk::append_persistent_f6(v, SHK_LAYOUT_TN);
+    shk::append_persistent_4_2(v);
     for (size_t i = 0; i < v.size(); ++i) v[i].d.index = (int32_t)i;
     return v;
   }();

@@ -71,9 +71,24 @@ void append_all(std::vector<Entry>& t) {
 }
 #endif
 
+#if !SHK_DENSE_DMA
+// Persistent schedule: the 64 x 64 subchannel tiles for groups of 64 and up
+// and of 32 (int4; the fp6 tiles serve per-channel and groups of 128, 256).
+void append_persistent(std::vector<Entry>& t) {
+  if constexpr (kBits == 4) {
+    t.push_back(dense_persistent_entry<C<64, 64, 64, 2, 2, false, true, 64>>(kLayout, 8));
+    t.push_back(dense_persistent_entry<C<64, 64, 64, 2, 2, false, true, 32>>(kLayout, 8));
+  }
+}
+#endif
+
 }  // namespace
 
 #define SHK_CAT3(a, b, c) a##b##_##c
+#if !SHK_DENSE_DMA
+#define SHK_PERSISTENT_NAME(b, l) SHK_CAT3(append_persistent_, b, l)
+void SHK_PERSISTENT_NAME(SHK_BITS, SHK_LAYOUT)(std::vector<Entry>& t) { append_persistent(t); }
+#endif
 #if SHK_DENSE_DMA
 #define SHK_APPEND_NAME(b, l) SHK_CAT3(append_dense_dma_, b, l)
 #else

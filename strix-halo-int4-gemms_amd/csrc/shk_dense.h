@@ -83,13 +83,13 @@ __device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int 
   }
 }
 
+// One output tile, tile index `tile` in the XCD-aware order.
 template <class C>
-__global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
+__device__ __forceinline__ void dense_tile(const DenseArgs& p, uint8_t* smem, int tile) {
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
-  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
+  dense_tile_coords(tile, tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
   const int gate = C::SWIGLU ? p.N : 0;
@@ -191,6 +191,26 @@ __global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
     } else {
       dense_store<C>(e, p, m0, n0, scaled, raw_of, no_nan);
     }
+  }
+}
+
+// One workgroup per tile.
+template <class C>
+__global__ __launch_bounds__(C::NT) void dense_gemm_kernel(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
+  dense_tile<C>(p, smem, blockIdx.x);
+}
+
+// Persistent schedule: gridDim.x workgroups (a multiple of 8, at most one
+// per resident slot) stride over the tiles, so a workgroup stays on one XCD;
+// every LDS read is done before the next tile's stages refill LDS.
+template <class C>
+__global__ __launch_bounds__(C::NT) void dense_gemm_persistent(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
+  const int tiles = (p.M / C::BM) * (p.N / C::BN);
+  for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+    dense_tile<C>(p, smem, t);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }
 

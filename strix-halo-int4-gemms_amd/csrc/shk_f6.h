@@ -253,6 +253,25 @@ struct F6Engine {
     (read<S, Q>(r), ...);
   }
 
+  // Clears the accumulators with MFMAs (A = B = 0, C = 0).  A persistent
+  // workgroup calls it before each tile: an asm MFMA whose C operand was
+  // last written by VALU code after an earlier MFMA of the same wave has
+  // read stale values, while an accumulator an MFMA wrote reads back right.
+  __device__ __forceinline__ void mfma_clear() {
+    v6i z;
+#pragma unroll
+    for (int w = 0; w < 6; ++w) z[w] = 0;
+    asm volatile("s_nop 4" : "+v"(z));  // VALU writes before the MFMAs read them
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %1, 0 cbsz:2 blgp:2" : "+a"(acc[i][j]) : "v"(z));
+    // tied operands keep each accumulator in place; the fence lands the
+    // results before any other access
+    fence<7>();
+  }
+
   // Wait states between accumulator writes and reads outside the asm
   // MFMAs; every accumulator is an operand, so no access crosses it.
   template <int N>
@@ -637,20 +656,20 @@ __device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint
   }
 }
 
-// One kernel per output mode and epilogue (chosen by the host), so that
-// each holds a single straight-line epilogue.
-template <class C, int MODE, int EPI>
-__global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
+// One output tile of the fp6 GEMM: tile index `tile` in the XCD-aware order
+// of dense_tile_coords.
+template <class C, int MODE, int EPI, bool PERSIST = false>
+__device__ __forceinline__ void f6_gemm_tile(const DenseArgs& p, uint8_t* smem, int tile) {
   using E = F6Engine<C>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
-  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
+  dense_tile_coords(tile, tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
   E e;
   e.setup(smem, p.a, p.b, m0, tn, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.b_cols, p.K));
+  if constexpr (PERSIST) e.mfma_clear();
   float sa[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
@@ -658,6 +677,29 @@ __global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
   mfma32_prefetch_b_scales<C, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
   e.run(p.K / 128);
   mfma32_finish<C, MODE, EPI>(e, o, smem, m0, n0, sa);
+}
+
+// One kernel per output mode and epilogue (chosen by the host), so that
+// each holds a single straight-line epilogue.  One workgroup per tile.
+template <class C, int MODE, int EPI>
+__global__ __launch_bounds__(256) void f6_gemm_kernel(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6Engine<C>::LDS_BYTES + MFMA32_SCALE_BYTES];
+  f6_gemm_tile<C, MODE, EPI>(p, smem, blockIdx.x);
+}
+
+// Persistent schedule: gridDim.x workgroups (a multiple of 8, at most one
+// per resident slot) take tiles blockIdx.x, blockIdx.x + gridDim.x, ...; a
+// workgroup therefore stays on one XCD, as in the one-tile-per-workgroup
+// order.  Between tiles, every wave has finished reading LDS before the next
+// tile's prologue refills it.
+template <class C, int MODE, int EPI>
+__global__ __launch_bounds__(256) void f6_gemm_persistent(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6Engine<C>::LDS_BYTES + MFMA32_SCALE_BYTES];
+  const int tiles = (p.M / C::BM) * (p.N / C::BN);
+  for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+    f6_gemm_tile<C, MODE, EPI, true>(p, smem, t);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
 }
 
 }  // namespace shk

@@ -289,8 +289,23 @@ struct F6SubEngine {
       }
   }
 
-  // nst: 64-K stages (a multiple of SPG).  RAW: no folds, the accumulators
-  // keep the whole K sum (exact up to 2^24, K <= F6_MAX_K).
+  // RAW mode: adds group g's exact integer partial sums into the totals,
+  // which then hold int32 bit patterns.
+  __device__ __forceinline__ void fold_raw() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          tot[i][j][x] = __int_as_float(__float_as_int(tot[i][j][x]) + (int)acc[i][j][x]);
+  }
+
+  // nst: 64-K stages (a multiple of SPG).  RAW: the totals receive the exact
+  // int32 sum over all K instead of the scaled fp32 sum.  Every group's first
+  // MFMA takes 0 as its C operand in both modes: no MFMA reads accumulators
+  // that VALU code wrote (between the tiles of a persistent workgroup, such a
+  // read returned stale values).
   template <bool RAW>
   __device__ __forceinline__ void run(const uint8_t* smem, int nst) {
     const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
@@ -327,7 +342,7 @@ struct F6SubEngine {
     int slot = 0;
     for (int k = 0; k < nst; k += SPG) {
       // one group: SPG stages, alternating register sets (SPG is even)
-      stage<0, !RAW>(r, k, nst, slot, rs_end, rss_end, s8);
+      stage<0, true>(r, k, nst, slot, rs_end, rss_end, s8);
       advance(r, slot);
       stage<1, false>(r, k + 1, nst, slot, rs_end, rss_end, s8);
       advance(r, slot);
@@ -338,7 +353,8 @@ struct F6SubEngine {
         advance(r, slot);
       }
       fence<7>();
-      if constexpr (!RAW) fold(smem, k / SPG);
+      if constexpr (RAW) fold_raw();
+      else fold(smem, k / SPG);
     }
     // the loads past the last stage land before the workgroup's LDS is freed
     wait_vmcnt<0>();
@@ -404,17 +420,15 @@ __device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, 
       }
 }
 
-// Subchannel GEMM over fp6 blocks (p.a / p.b point at the converted A and
-// B); SPG = S / 64 stages per scale group.  One kernel per output mode and
-// epilogue.  Two workgroups share a CU.
+// One 128 x 128 output tile of the subchannel GEMM over fp6 blocks (p.a /
+// p.b point at the converted A and B); SPG = S / 64 stages per scale group.
 template <class C, int MODE, int EPI, int SPG>
-__global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
+__device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, int tile) {
   using E = F6SubEngine<C, SPG>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
-  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
+  dense_tile_coords(tile, tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
   E e;
@@ -423,12 +437,32 @@ __global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
   e.template run<MODE == OUT_I32>(smem, p.K / 64);
   const OutView o{p.out, p.b_scale, p.N, p.M, p.N, 0, p.M, p.N};
   if constexpr (MODE == OUT_I32) {
-    f6sub_store_words(e, o, m0, n0, [&](int i, int j, int x) { return (int)e.acc[i][j][x]; });
+    f6sub_store_words(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
   } else if constexpr (MODE == OUT_F32) {
     f6sub_store_words(e, o, m0, n0,
                       [&](int i, int j, int x) { return __float_as_int(apply_epi(e.tot[i][j][x], EPI)); });
   } else {
     f6sub_store_bf16(e, o, smem, m0, n0, [&](int i, int j, int x) { return apply_epi(e.tot[i][j][x], EPI); });
+  }
+}
+
+// One kernel per output mode, epilogue and group size; one workgroup per
+// tile, two workgroups per CU.
+template <class C, int MODE, int EPI, int SPG>
+__global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C, SPG>::LDS_BYTES];
+  f6_sub_tile<C, MODE, EPI, SPG>(p, smem, blockIdx.x);
+}
+
+// Persistent schedule (as f6_gemm_persistent): gridDim.x workgroups stride
+// over the tiles, with every LDS read done before the next tile's prologue.
+template <class C, int MODE, int EPI, int SPG>
+__global__ __launch_bounds__(256, 2) void f6_sub_persistent(const DenseArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C, SPG>::LDS_BYTES];
+  const int tiles = (p.M / C::BM) * (p.N / C::BN);
+  for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
+    f6_sub_tile<C, MODE, EPI, SPG>(p, smem, t);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }
 

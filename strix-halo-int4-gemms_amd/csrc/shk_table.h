@@ -70,6 +70,45 @@ hipError_t launch_f6_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   if (err == hipSuccess) err = launch_f6_gemm_t<C>(a, grid, s);
   return err;
 }
+// Workgroups of a persistent launch of `kernel` with `block` threads: its
+// resident slots on the current device (occupancy x CUs), rounded down to a
+// multiple of 8 so that a workgroup keeps its XCD, and at most `tiles`
+// (capi.hip).
+hipError_t persistent_grid(const void* kernel, int block, unsigned tiles, unsigned* grid);
+template <auto K>
+hipError_t launch_persistent(const DenseArgs& g, unsigned tiles, int block, hipStream_t s) {
+  unsigned n = 0;
+  const hipError_t err = persistent_grid(reinterpret_cast<const void*>(K), block, tiles, &n);
+  if (err != hipSuccess) return err;
+  void* args[] = {const_cast<DenseArgs*>(&g)};
+  return hipLaunchKernel(reinterpret_cast<const void*>(K), dim3(n), dim3(block), args, 0, s);
+}
+// fp6 GEMM on converted operands, persistent schedule (plain epilogues).
+template <class C>
+hipError_t launch_f6_gemm_persistent_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  static_assert(!C::SWIGLU, "persistent entries are plain");
+  DenseArgs g = a;
+  g.a = a.work;
+  g.b = a.work + f6_operand_bytes(a.M, a.K);
+  const bool relu2 = a.epilogue == EPI_RELU2;
+  if (a.out_mode == OUT_I32) return launch_persistent<&f6_gemm_persistent<C, OUT_I32, EPI_NONE>>(g, grid.x, 256, s);
+  if (a.out_mode == OUT_F32)
+    return relu2 ? launch_persistent<&f6_gemm_persistent<C, OUT_F32, EPI_RELU2>>(g, grid.x, 256, s)
+                 : launch_persistent<&f6_gemm_persistent<C, OUT_F32, EPI_NONE>>(g, grid.x, 256, s);
+  return relu2 ? launch_persistent<&f6_gemm_persistent<C, OUT_BF16, EPI_RELU2>>(g, grid.x, 256, s)
+               : launch_persistent<&f6_gemm_persistent<C, OUT_BF16, EPI_NONE>>(g, grid.x, 256, s);
+}
+template <class C>
+hipError_t launch_f6_persistent_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  hipError_t err = launch_f6_pack2(f6_pack_args(a, 0, false), f6_mn_major(a, 0), f6_pack_args(a, 1, false),
+                                   f6_mn_major(a, 1), s);
+  if (err == hipSuccess) err = launch_f6_gemm_persistent_t<C>(a, grid, s);
+  return err;
+}
+template <class C>
+hipError_t launch_dense_persistent_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  return launch_persistent<&dense_gemm_persistent<C>>(a, grid.x, C::NT, s);
+}
 // int8 32x32 engine: one kernel per output mode and epilogue.
 template <class C>
 hipError_t launch_i8_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
@@ -117,6 +156,7 @@ constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
       C::LDS_BYTES,
       group_m,
       SHK_OPERANDS_PACKED,
+      SHK_SCHEDULE_STANDARD,
   };
 }
 
@@ -138,6 +178,22 @@ Entry f6_entry(int layout) {
   d.lds_bytes = F6Engine<C>::LDS_BYTES + MFMA32_SCALE_BYTES;
   d.operand_format = SHK_OPERANDS_FP6;
   return Entry{d, &launch_f6_t<C>, nullptr, nullptr, &launch_f6_gemm_t<C>};
+}
+// Persistent-schedule entries of the same kernels.
+template <class C>
+Entry f6_persistent_entry(int layout) {
+  Entry e = f6_entry<C>(layout);
+  e.d.schedule = SHK_SCHEDULE_PERSISTENT;
+  e.dense = &launch_f6_persistent_t<C>;
+  e.converted = &launch_f6_gemm_persistent_t<C>;
+  return e;
+}
+template <class C>
+Entry dense_persistent_entry(int layout, int group_m) {
+  Entry e = dense_entry<C>(layout, group_m);
+  e.d.schedule = SHK_SCHEDULE_PERSISTENT;
+  e.dense = &launch_dense_persistent_t<C>;
+  return e;
 }
 template <class C>
 Entry fwd_entry(int layout) {
@@ -164,6 +220,14 @@ void append_dense_4_2(std::vector<Entry>& t);
 void append_dense_8_0(std::vector<Entry>& t);
 void append_dense_8_1(std::vector<Entry>& t);
 void append_dense_8_2(std::vector<Entry>& t);
+// Persistent-schedule int4 entries (plain epilogue kind), appended after
+// the ragged families: the fp6 per-channel and subchannel tiles
+// (append_persistent_f6(layout)) and the register-staged 64 x 64
+// subchannel tiles for groups of 64 and 32 (append_persistent_4_<layout>).
+void append_persistent_f6(std::vector<Entry>& t, int layout);
+void append_persistent_4_0(std::vector<Entry>& t);
+void append_persistent_4_1(std::vector<Entry>& t);
+void append_persistent_4_2(std::vector<Entry>& t);
 void append_ragged_0(std::vector<Entry>& t);
 void append_ragged_1(std::vector<Entry>& t);
 void append_ragged_2(std::vector<Entry>& t);

@@ -423,3 +423,56 @@ def test_torch_gemm_custom_op_matches_explicit_mm(kernel, device):
         assert out.dtype == want.dtype and tuple(out.shape) == tuple(want.shape)
         assert torch.equal(out.view(torch.int16) if out.dtype == torch.bfloat16 else out,
                            want.view(torch.int16) if want.dtype == torch.bfloat16 else want)
+
+
+_PERSISTENT = [k for k in shk.default_registry.all() if k.schedule is shk.KernelSchedule.PERSISTENT]
+
+
+@pytest.mark.parametrize("kernel", _PERSISTENT, ids=lambda k: k.kernel_id)
+def test_persistent_kernels_loop_over_tiles(kernel, device):
+    """Persistent schedule (reference KernelSchedule.PERSISTENT): at 4096 x
+    8192 every workgroup takes two or more tiles (256 x 256 tiles: 512 for
+    256 resident workgroups; 128 x 128 and 64 x 64 tiles: 2048 and 8192).
+    The output equals the standard schedule's bit for bit, and on sampled
+    rows the oracle's."""
+    bits, layout, sub, epi = _kernel_params(kernel)
+    m, n, k = 4096, 8192, 512
+    seed = stable_seed("persistent", kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=False)
+    a, b = to_dev(torch, a_arg, device), to_dev(torch, b_arg, device)
+    ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
+    standard = shk.default_registry.select(dtype=kernel.a_dtype, scale=kernel.scale, epilogue=kernel.epilogue,
+                                           layout=kernel.layout, m=m, n=n, k=k)
+    print(f"case {kernel.kernel_id} vs {standard.kernel_id} shape=({m},{n},{k})", flush=True)
+    got = shk.explicit_mm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    want = shk.explicit_mm(a, b, kernel=standard, a_scale=ta, b_scale=tb)
+    raw = native.launch_generated_kernel_i32(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    rows = _sampled_rows(m, 64, seed)
+    a_rows_q = a_q[rows]
+    assert np.array_equal(raw[torch.from_numpy(rows).to(device)].cpu().numpy(), ref.int_matmul(a_rows_q, b_q))
+    if layout == "nn":
+        oracle = ref.reference_gemm_bf16(a_arg[rows], b_arg, bits=bits, layout=layout, a_scale=sa[rows],
+                                         b_scale=sb, subchannel=sub, epilogue=epi)
+        assert np.array_equal(bf16_bits(torch, got[torch.from_numpy(rows).to(device)]), oracle)
+
+
+@pytest.mark.parametrize("scale", ["pc", "sc32", "sc64", "sc128", "sc256"])
+@pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
+def test_mm_persistent_schedule_matches_oracle(scale, layout, device):
+    """mm(schedule=KernelSchedule.PERSISTENT) (reference api.py:119-164)."""
+    m, n, k = 512, 768, 512
+    sub = None if scale == "pc" else int(scale[2:])
+    seed = stable_seed("mm-persistent", scale, layout)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=False)
+    spec = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL) if sub is None else shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, sub)
+    print(f"case mm persistent {scale} {layout}", flush=True)
+    out = shk.mm(to_dev(torch, a_arg, device), to_dev(torch, b_arg, device), a_scale=to_dev(torch, sa, device),
+                 b_scale=to_dev(torch, sb, device), layout=shk.GemmLayout(layout), scale=spec,
+                 schedule=shk.KernelSchedule.PERSISTENT)
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=4, layout=layout, a_scale=sa, b_scale=sb, subchannel=sub,
+                                   epilogue="none")
+    assert np.array_equal(bf16_bits(torch, out), want)

@@ -369,3 +369,23 @@ def test_torch_op_registers_once_and_fakes_every_layout():
             want = torch.bfloat16 if kernel.output_dtype == "bfloat16" else torch.float32
             assert out.dtype == want and out.device.type == "cuda", kernel.kernel_id
     assert len(seen) >= 8
+
+
+def test_persistent_schedule_selection():
+    """The persistent schedule serves int4 with the NONE epilogue for every
+    scale mode and layout, and nothing else (reference registry.py:230-251)."""
+    for layout in (shk.GemmLayout.NN, shk.GemmLayout.NT, shk.GemmLayout.TN):
+        for spec in (PC, *(shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, s) for s in (32, 64, 128, 256))):
+            k = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=spec, epilogue=shk.Epilogue.NONE,
+                                            layout=layout, m=1024, n=1024, k=1024,
+                                            schedule=shk.KernelSchedule.PERSISTENT)
+            assert k.schedule is shk.KernelSchedule.PERSISTENT and "_none_persistent_" in k.kernel_id
+            assert k.kernel_id.startswith(f"gfx950_int4xint4_{layout.value}_{spec.label}_none_persistent_")
+    for dtype, epilogue in ((shk.OperandDType.INT4, shk.Epilogue.RELU2), (shk.OperandDType.INT8, shk.Epilogue.NONE)):
+        with pytest.raises(LookupError):
+            shk.default_registry.select(dtype=dtype, scale=PC, epilogue=epilogue, m=1024, n=1024, k=1024,
+                                        schedule=shk.KernelSchedule.PERSISTENT)
+    # the standard schedule never picks a persistent kernel
+    assert all(k.schedule is shk.KernelSchedule.STANDARD for k in (
+        shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=PC, epilogue=shk.Epilogue.NONE,
+                                    m=8192, n=8192, k=8192),))
