@@ -256,7 +256,7 @@ def test_quant_helpers_match_oracle():
 
 
 def test_tops_known_answer():
-    assert shk.tops_for_runtime(1024, 1024, 1024, 1.0) == pytest.approx(2.147483648)
+    assert shk.tops_for_runtime(shk.BenchmarkShape(1024, 1024, 1024), 1.0) == pytest.approx(2.147483648)
 
 
 # ---------------------------------------------------------------------------
