@@ -109,6 +109,8 @@ typedef struct shk_kernel_desc {
   int32_t group_size_m;    /* tile-row swizzle width (dense) */
   int32_t operand_format;  /* SHK_OPERANDS_* */
   int32_t schedule;        /* SHK_SCHEDULE_* */
+  int32_t split_k;         /* K slices per output tile (dense); > 1: float32 output that the
+                              slices add into with atomics, so `out` must hold zeros */
 } shk_kernel_desc;
 
 /* ---- status (reference dispatch.cpp:206-222) ---------------------------- */

@@ -82,6 +82,7 @@ class KernelDesc:
     group_size_m: int
     operand_format: int = OPERANDS_PACKED
     schedule: int = SCHEDULE_STANDARD
+    split_k: int = 1
 
     @property
     def needs_workspace(self) -> bool:
@@ -119,7 +120,7 @@ MFMA32_SCALE_BYTES = 4 * 256
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
-          fp6=False, fp6_sub=False, schedule=SCHEDULE_STANDARD):
+          fp6=False, fp6_sub=False, schedule=SCHEDULE_STANDARD, split_k=1):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
@@ -155,6 +156,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         group_size_m=group_m,
         operand_format=OPERANDS_FP6 if fp6 else OPERANDS_PACKED,
         schedule=schedule,
+        split_k=split_k,
     )
 
 
@@ -203,6 +205,16 @@ def _build() -> tuple[KernelDesc, ...]:
         add(**d, bm=128, bn=128, bk=128, wm=2, wn=2, subch=True, fp6_sub=True)
         add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True)
         add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True, mk=32)
+    # split-K 2/4/8 (fp32 output): 128x128 per-channel, int4 64x64 subchannel
+    for bits in (4, 8):
+        for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
+            d = dict(family=FAMILY_DENSE, bits=bits, layout=layout)
+            for split in (2, 4, 8):
+                add(**d, bm=128, bn=128, bk=64, wm=2, wn=2, split_k=split)
+            if bits == 4:
+                for mk in (64, 32):
+                    for split in (2, 4, 8):
+                        add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True, mk=mk, split_k=split)
     return tuple(out)
 
 
@@ -217,7 +229,7 @@ def measured_tops(desc: KernelDesc) -> float | None:
     int4 subchannel 128x128 (C3), int8 32x32 SwiGLU 256x128 (C4, 4096 x
     2*11008 x 4096) and int8 plain 256x256 (8192^3).  Other entries have no
     measurement and rank by tile area."""
-    if desc.family != FAMILY_DENSE or desc.schedule != SCHEDULE_STANDARD:
+    if desc.family != FAMILY_DENSE or desc.schedule != SCHEDULE_STANDARD or desc.split_k > 1:
         return None
     if desc.operand_format == OPERANDS_FP6:
         if desc.scale_mode == SCALE_SUBCHANNEL:

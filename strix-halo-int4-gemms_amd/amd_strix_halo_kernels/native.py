@@ -44,7 +44,7 @@ class _Desc(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "index", "family", "dtype_bits", "layout", "scale_mode", "min_subchannel", "max_subchannel",
         "epilogue_kind", "block_m", "block_n", "block_k", "num_waves", "num_stages", "lds_bytes",
-        "group_size_m", "operand_format", "schedule")]
+        "group_size_m", "operand_format", "schedule", "split_k")]
 
 
 @functools.lru_cache(maxsize=None)
@@ -417,6 +417,13 @@ def launch_generated_kernel(
         raise ValueError(f"output shape must be {(m, n)}; got {tuple(c.shape[-2:])}")
     out_mode = kt.OUT_BF16 if out_dtype == torch.bfloat16 else kt.OUT_F32
     lib_path = library_path if library_path is not None else (native_library_path(root=root) if root else None)
+    if kernel.tile.split_k > 1:
+        # K slices add into the output (native.py:739-740 zeroes it too), on the launch stream
+        if stream is None:
+            c.zero_()
+        else:
+            with torch.cuda.stream(stream):
+                c.zero_()
     _gemm_call(torch, a, b, a_scale, b_scale, c, kernel, m, n, k, out_mode, lib_path, stream)
     return c
 

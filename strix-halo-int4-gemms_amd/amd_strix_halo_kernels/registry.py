@@ -49,7 +49,7 @@ def _tile_of(desc: kt.KernelDesc) -> TileConfig:
         num_stages=desc.num_stages,
         waves_per_eu=max(1, desc.num_waves // 4),
         even_k=True,
-        split_k=1,
+        split_k=desc.split_k,
     )
 
 
@@ -66,7 +66,7 @@ def _scales_of(desc: kt.KernelDesc) -> tuple[ScaleSpec, ...]:
 def _epilogues_of(desc: kt.KernelDesc) -> tuple[Epilogue, ...]:
     if desc.epilogue_kind == kt.EPI_KIND_SWIGLU:
         return (Epilogue.SWIGLU,)
-    if desc.schedule == kt.SCHEDULE_PERSISTENT:
+    if desc.schedule == kt.SCHEDULE_PERSISTENT or desc.split_k > 1:
         return (Epilogue.NONE,)  # the reference's persistent kernels (registry.py:230-251)
     return (Epilogue.NONE, Epilogue.RELU2)
 

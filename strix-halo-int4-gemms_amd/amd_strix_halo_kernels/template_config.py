@@ -38,6 +38,10 @@ def tile_multiple_rejection_reasons(kernel: KernelMetadata, shape: LaunchShape) 
     sub = kernel.scale.subchannel_size
     if kernel.scale.mode is ScaleMode.SUBCHANNEL and sub is not None and shape.k % sub:
         out.append(f"K={shape.k} is not divisible by SUBCHANNEL={sub}")
+    elif (kernel.scale.mode is ScaleMode.SUBCHANNEL and sub is not None and tile.split_k > 1
+          and (shape.k // tile.split_k) % sub):
+        # each K slice of a split-K kernel starts at a scale group boundary
+        out.append(f"K/SPLIT_K={shape.k // tile.split_k} is not divisible by SUBCHANNEL={sub}")
     return tuple(out)
 
 

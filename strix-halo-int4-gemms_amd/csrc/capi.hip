@@ -92,6 +92,12 @@ const std::vector<Entry>& table() {
     shk::append_persistent_4_1(v);
     shk::append_persistent_f6(v, SHK_LAYOUT_TN);
     shk::append_persistent_4_2(v);
+    shk::append_split_4_0(v);
+    shk::append_split_4_1(v);
+    shk::append_split_4_2(v);
+    shk::append_split_8_0(v);
+    shk::append_split_8_1(v);
+    shk::append_split_8_2(v);
     for (size_t i = 0; i < v.size(); ++i) v[i].d.index = (int32_t)i;
     return v;
   }();
@@ -206,15 +212,24 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
     if (!why.empty()) why += "; ";
     why += "N=" + std::to_string(n) + " is not divisible by BLOCK_N=" + std::to_string(d.block_n);
   }
-  if (k % d.block_k) {
+  const int split = d.split_k > 1 ? d.split_k : 1;
+  if (k % (d.block_k * split)) {
     if (!why.empty()) why += "; ";
-    why += "K=" + std::to_string(k) + " is not divisible by BLOCK_K*SPLIT_K=" + std::to_string(d.block_k);
+    why += "K=" + std::to_string(k) + " is not divisible by BLOCK_K*SPLIT_K=" + std::to_string(d.block_k * split);
   }
   if (d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && k % subchannel) {
     if (!why.empty()) why += "; ";
     why += "K=" + std::to_string(k) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
   }
+  if (split > 1 && d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && (k / split) % subchannel) {
+    if (!why.empty()) why += "; ";
+    why += "K/SPLIT_K=" + std::to_string(k / split) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
+  }
   if (!why.empty()) return fail("kernel " + std::to_string(kernel_index) + " requires tile-multiple shape: " + why);
+  if (split > 1 && gemm && epilogue != SHK_EPILOGUE_NONE)
+    return fail("split-K kernels support the NONE epilogue only (SPLIT_K=" + std::to_string(split) + ")");
+  if (split > 1 && gemm && out_mode != SHK_OUT_F32)
+    return fail("split-K kernels write float32 output (out_mode " + std::to_string(SHK_OUT_F32) + ")");
   const bool swiglu = d.epilogue_kind == SHK_EPI_KIND_SWIGLU;
   if (gemm) {
     if (check_subchannel(d, subchannel)) return 1;
@@ -392,7 +407,8 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
     return 1;
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
-  const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles), reinterpret_cast<hipStream_t>(stream));
+  const unsigned split = c.e->d.split_k > 1 ? (unsigned)c.e->d.split_k : 1u;
+  const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles, split), reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail_hip("kernel launch", err);
   return 0;
 }

@@ -80,6 +80,16 @@ void append_persistent(std::vector<Entry>& t) {
     t.push_back(dense_persistent_entry<C<64, 64, 64, 2, 2, false, true, 32>>(kLayout, 8));
   }
 }
+
+// Split-K: the 128x128 per-channel tile and the 64x64 subchannel tiles, in
+// 2, 4 and 8 K slices.
+void append_split(std::vector<Entry>& t) {
+  for (int split : {2, 4, 8}) t.push_back(split_entry<C<128, 128, 64, 2, 2, false, false, 64>>(kLayout, 8, split));
+  if constexpr (kBits == 4) {
+    for (int split : {2, 4, 8}) t.push_back(split_entry<C<64, 64, 64, 2, 2, false, true, 64>>(kLayout, 8, split));
+    for (int split : {2, 4, 8}) t.push_back(split_entry<C<64, 64, 64, 2, 2, false, true, 32>>(kLayout, 8, split));
+  }
+}
 #endif
 
 }  // namespace
@@ -88,6 +98,8 @@ void append_persistent(std::vector<Entry>& t) {
 #if !SHK_DENSE_DMA
 #define SHK_PERSISTENT_NAME(b, l) SHK_CAT3(append_persistent_, b, l)
 void SHK_PERSISTENT_NAME(SHK_BITS, SHK_LAYOUT)(std::vector<Entry>& t) { append_persistent(t); }
+#define SHK_SPLIT_NAME(b, l) SHK_CAT3(append_split_, b, l)
+void SHK_SPLIT_NAME(SHK_BITS, SHK_LAYOUT)(std::vector<Entry>& t) { append_split(t); }
 #endif
 #if SHK_DENSE_DMA
 #define SHK_APPEND_NAME(b, l) SHK_CAT3(append_dense_dma_, b, l)

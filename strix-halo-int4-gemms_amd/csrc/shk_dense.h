@@ -63,7 +63,17 @@ __device__ __forceinline__ void store_values(const E& e, const DenseArgs& p, int
 template <class C, class E, class Value, class Raw>
 __device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int m0, int n0, Value value, Raw raw,
                                             bool no_nan = false) {
-  if (p.out_mode == OUT_I32) {
+  if (p.out_mode == OUT_F32_ADD) {
+    float* o = static_cast<float*>(p.out);
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) {
+        float* row = o + (long)(m0 + e.out_row(i)) * p.N + n0 + e.out_col(j);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) unsafeAtomicAdd(row + r, value(i, j, r));
+      }
+  } else if (p.out_mode == OUT_I32) {
     const long ldo = C::SWIGLU ? 2L * p.N : (long)p.N;
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
@@ -83,9 +93,31 @@ __device__ __forceinline__ void dense_store(const E& e, const DenseArgs& p, int 
   }
 }
 
+// The arguments of K slice blockIdx.y of gridDim.y (split-K): the operands
+// start at the slice's first K value, subchannel scales at its first group,
+// and the tile adds its fp32 result into the output.  The host checks that
+// K is a multiple of BK * gridDim.y and, for subchannel scales, that a slice
+// holds whole groups.
+template <class C>
+__device__ __forceinline__ DenseArgs k_slice(DenseArgs p) {
+  const int ks = p.K / (int)gridDim.y;
+  const long k0 = (long)blockIdx.y * ks * C::BITS / 8;  // bytes into a K row
+  p.a += C::A_KMAJOR ? k0 : k0 * p.lda;
+  p.b += C::B_KMAJOR ? k0 : k0 * p.ldb;
+  if (C::SUBCH) {
+    const int g0 = (int)blockIdx.y * (ks / p.subchannel);
+    p.a_scale += g0;
+    p.b_scale += (long)g0 * p.b_cols;
+  }
+  p.K = ks;
+  p.out_mode = OUT_F32_ADD;
+  return p;
+}
+
 // One output tile, tile index `tile` in the XCD-aware order.
 template <class C>
-__device__ __forceinline__ void dense_tile(const DenseArgs& p, uint8_t* smem, int tile) {
+__device__ __forceinline__ void dense_tile(const DenseArgs& p_all, uint8_t* smem, int tile) {
+  const DenseArgs p = gridDim.y > 1 ? k_slice<C>(p_all) : p_all;
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;

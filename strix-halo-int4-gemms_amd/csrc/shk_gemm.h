@@ -28,7 +28,8 @@
 
 namespace shk {
 
-enum OutMode : int { OUT_BF16 = 0, OUT_F32 = 1, OUT_I32 = 2 };
+// OUT_F32_ADD is internal: a split-K slice adds its fp32 partial into out.
+enum OutMode : int { OUT_BF16 = 0, OUT_F32 = 1, OUT_I32 = 2, OUT_F32_ADD = 3 };
 enum EpiKind : int { EPI_NONE = 0, EPI_RELU2 = 1 };
 
 template <int BITS_, bool A_KMAJOR_, bool B_KMAJOR_, int BM_, int BN_, int BK_, int WM_, int WN_,

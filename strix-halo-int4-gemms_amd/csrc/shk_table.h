@@ -157,6 +157,7 @@ constexpr shk_kernel_desc desc_of(int family, int layout, int group_m) {
       group_m,
       SHK_OPERANDS_PACKED,
       SHK_SCHEDULE_STANDARD,
+      1,
   };
 }
 
@@ -195,6 +196,14 @@ Entry dense_persistent_entry(int layout, int group_m) {
   e.dense = &launch_dense_persistent_t<C>;
   return e;
 }
+// Split-K entries of a dense tile: grid.y = split, each workgroup sums one
+// K slice and adds its scaled fp32 partial into the zeroed output.
+template <class C>
+Entry split_entry(int layout, int group_m, int split) {
+  Entry e = dense_entry<C>(layout, group_m);
+  e.d.split_k = split;
+  return e;
+}
 template <class C>
 Entry fwd_entry(int layout) {
   return Entry{desc_of<C>(SHK_FAMILY_RAGGED_FWD, layout, 1), nullptr, &launch_fwd_t<C>, nullptr, nullptr};
@@ -228,6 +237,14 @@ void append_persistent_f6(std::vector<Entry>& t, int layout);
 void append_persistent_4_0(std::vector<Entry>& t);
 void append_persistent_4_1(std::vector<Entry>& t);
 void append_persistent_4_2(std::vector<Entry>& t);
+// Split-K 2/4/8 entries of the 128x128 per-channel tile (int4, int8) and of
+// the 64x64 subchannel tiles (int4), per layout (append_split_<bits>_<layout>).
+void append_split_4_0(std::vector<Entry>& t);
+void append_split_4_1(std::vector<Entry>& t);
+void append_split_4_2(std::vector<Entry>& t);
+void append_split_8_0(std::vector<Entry>& t);
+void append_split_8_1(std::vector<Entry>& t);
+void append_split_8_2(std::vector<Entry>& t);
 void append_ragged_0(std::vector<Entry>& t);
 void append_ragged_1(std::vector<Entry>& t);
 void append_ragged_2(std::vector<Entry>& t);

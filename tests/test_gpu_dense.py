@@ -27,6 +27,9 @@ from amd_strix_halo_kernels.template_config import representative_generation_sha
 
 pytestmark = pytest.mark.gpu
 
+# split-K kernels write fp32 sums of K slices; tests/test_gpu_splitk.py covers them
+_UNSPLIT = tuple(k for k in shk.default_registry.all() if k.tile.split_k == 1)
+
 ULP_TOL = 2
 
 
@@ -47,7 +50,7 @@ def _kernel_params(kernel):
     return bits, kernel.layout.value, sub, kernel.epilogue.value
 
 
-@pytest.mark.parametrize("kernel", shk.default_registry.all(), ids=lambda k: k.kernel_id)
+@pytest.mark.parametrize("kernel", _UNSPLIT, ids=lambda k: k.kernel_id)
 def test_every_registry_kernel_matches_oracle(kernel, device):
     bits, layout, sub, epi = _kernel_params(kernel)
     shape = representative_generation_shape(kernel)
@@ -78,7 +81,7 @@ def _odd_stage_k(kernel):
     return 3 * unit if (3 * unit // bk) % 2 == 1 else None
 
 
-@pytest.mark.parametrize("kernel", [k for k in shk.default_registry.all() if _odd_stage_k(k)],
+@pytest.mark.parametrize("kernel", [k for k in _UNSPLIT if _odd_stage_k(k)],
                          ids=lambda k: k.kernel_id)
 def test_every_registry_kernel_odd_stage_count(kernel, device):
     """Pipelined kernels run K blocks in pairs; an odd count ends on a single
@@ -232,7 +235,7 @@ def _sprinkle(scales, seed, every):
     return s
 
 
-@pytest.mark.parametrize("kernel", [k for k in shk.default_registry.all() if k.scale.mode is shk.ScaleMode.PER_CHANNEL
+@pytest.mark.parametrize("kernel", [k for k in _UNSPLIT if k.scale.mode is shk.ScaleMode.PER_CHANNEL
                                     and k.layout is shk.GemmLayout.NN], ids=lambda k: k.kernel_id)
 def test_special_scale_values_store_like_torch(kernel, device):
     """Per-channel bf16 outputs stay bit-exact (NaN canonical 0x7FC0, subnormals
@@ -259,7 +262,7 @@ def test_special_scale_values_store_like_torch(kernel, device):
         assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("kernel", [k for k in shk.default_registry.all() if k.epilogue is shk.Epilogue.SWIGLU
+@pytest.mark.parametrize("kernel", [k for k in _UNSPLIT if k.epilogue is shk.Epilogue.SWIGLU
                                     and k.scale.mode is shk.ScaleMode.PER_CHANNEL and k.layout is shk.GemmLayout.NN],
                          ids=lambda k: k.kernel_id)
 def test_swiglu_gates_on_both_sides_of_the_fast_range(kernel, device):
@@ -287,10 +290,10 @@ def test_swiglu_gates_on_both_sides_of_the_fast_range(kernel, device):
     assert max_ulp(got, want) <= ULP_TOL
 
 
-_FP6 = [k for k in shk.default_registry.all()
+_FP6 = [k for k in _UNSPLIT
         if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.epilogue is not shk.Epilogue.RELU2
         and k.scale.mode is shk.ScaleMode.PER_CHANNEL]
-_FP6_SUB = [k for k in shk.default_registry.all()
+_FP6_SUB = [k for k in _UNSPLIT
             if kt.TABLE[k.table_index].operand_format == kt.OPERANDS_FP6 and k.scale.mode is shk.ScaleMode.SUBCHANNEL]
 
 
@@ -392,7 +395,7 @@ def test_fp6_converted_operands_are_reusable(layout, epilogue, device):
 
 def _one_kernel_per_family():
     seen, out = set(), []
-    for kernel in shk.default_registry.all():
+    for kernel in _UNSPLIT:
         key = (kernel.a_dtype, kernel.layout, kernel.epilogue, kernel.scale.mode)
         if key not in seen:
             seen.add(key)
@@ -425,7 +428,7 @@ def test_torch_gemm_custom_op_matches_explicit_mm(kernel, device):
                            want.view(torch.int16) if want.dtype == torch.bfloat16 else want)
 
 
-_PERSISTENT = [k for k in shk.default_registry.all() if k.schedule is shk.KernelSchedule.PERSISTENT]
+_PERSISTENT = [k for k in _UNSPLIT if k.schedule is shk.KernelSchedule.PERSISTENT]
 
 
 @pytest.mark.parametrize("kernel", _PERSISTENT, ids=lambda k: k.kernel_id)
