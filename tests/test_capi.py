@@ -356,3 +356,19 @@ def test_quantize_validates_before_launch(lib):
     # int8 codes are packed without a scale
     assert call(src=kt.SRC_I8, inv=0.0, x=None) == 1
     assert b"non-null" in lib.amd_strix_halo_kernels_last_error()
+
+
+def test_split_k_entries_validate_before_launch(lib):
+    """Split-K entries take float32 output, the NONE epilogue, K a multiple of
+    BLOCK_K*SPLIT_K, and (subchannel) whole scale groups per K slice."""
+    pc = _dense_index(dtype_bits=4, layout=kt.LAYOUT_NN, scale_mode=kt.SCALE_PER_CHANNEL, split_k=8, block_m=128)
+    assert _gemm(lib, pc, 128, 128, 256, mode=kt.OUT_F32) == 1
+    assert "BLOCK_K*SPLIT_K=512" in _err(lib)
+    assert _gemm(lib, pc, 128, 128, 512, mode=kt.OUT_BF16) == 1
+    assert "float32" in _err(lib)
+    assert _gemm(lib, pc, 128, 128, 512, epi=kt.EPILOGUE_RELU2, mode=kt.OUT_F32) == 1
+    assert "NONE epilogue" in _err(lib)
+    sc = _dense_index(dtype_bits=4, layout=kt.LAYOUT_NN, scale_mode=kt.SCALE_SUBCHANNEL, split_k=2, block_m=64,
+                      max_subchannel=256)
+    assert _gemm(lib, sc, 64, 64, 384, sub=128, mode=kt.OUT_F32) == 1
+    assert "K/SPLIT_K=192 is not divisible by SUBCHANNEL=128" in _err(lib)
