@@ -13,7 +13,9 @@
  *   - on failure amd_strix_halo_kernels_last_error() returns a message that
  *     stays valid until the next call on the same thread;
  *   - all device pointers are borrowed; the library never allocates or frees
- *     device memory; workspaces are passed in by the caller;
+ *     device memory; workspaces are passed in by the caller (except for
+ *     amd_strix_halo_kernels_launch_gemm_noalloc, whose workspace is a static
+ *     array of the library's code object);
  *   - launches are asynchronous on the given stream (a hipStream_t passed as
  *     uintptr_t, 0 = the null stream) on device `device_index`; the calling
  *     thread's current device is restored before returning.
@@ -182,6 +184,33 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
                                           const void* b_scale, void* out, int32_t m, int32_t n,
                                           int32_t k, int32_t subchannel, int32_t epilogue,
                                           int32_t out_mode, void* workspace, uint64_t workspace_bytes);
+
+/* Size of the library's scratch array (per device): the largest fp6 operand
+ * workspace amd_strix_halo_kernels_launch_gemm_noalloc accepts, 128 MiB
+ * (0.75 byte per value of A and B: covers M*K + b_cols*K <= 178956970
+ * values, e.g. M = N = K = 8192). */
+#define SHK_NOALLOC_SCRATCH_BYTES (128u * 1024u * 1024u)
+
+/* amd_strix_halo_kernels_launch_gemm_ws without a workspace argument, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  FP6 entries convert their operands into the library's own
+ * static scratch array of SHK_NOALLOC_SCRATCH_BYTES on `device_index`
+ * instead of a caller workspace; PACKED entries need none and run as
+ * amd_strix_halo_kernels_launch_gemm.  The call allocates and frees nothing
+ * (its first call on a device looks the array's address up once).  Shapes
+ * whose workspace (amd_strix_halo_kernels_gemm_workspace_bytes) exceeds
+ * SHK_NOALLOC_SCRATCH_BYTES are rejected with rc 1.  Every call on a device
+ * shares that device's array: the conversion rewrites every byte the GEMM
+ * reads, so no state carries over from an earlier call, but calls that
+ * overlap in time on one device (different streams, or threads without
+ * stream ordering) race on the array and give undefined results.  Same
+ * arguments, validation and errors as amd_strix_halo_kernels_launch_gemm. */
+int amd_strix_halo_kernels_launch_gemm_noalloc(int kernel_index, int device_index, uintptr_t stream,
+                                               const void* a, const void* b, const void* a_scale,
+                                               const void* b_scale, void* out, int32_t m, int32_t n,
+                                               int32_t k, int32_t subchannel, int32_t epilogue,
+                                               int32_t out_mode);
 
 /* The two halves of a fp6 launch, for callers that convert an operand once
  * and multiply it many times (a weight matrix), and for timing the GEMM

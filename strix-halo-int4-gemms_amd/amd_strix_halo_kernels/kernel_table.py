@@ -45,6 +45,9 @@ OUT_I32 = 2
 OPERANDS_PACKED = 0
 OPERANDS_FP6 = 1
 FP6_MAX_K = 262144
+# Bytes of the library's static scratch array (SHK_NOALLOC_SCRATCH_BYTES): the
+# largest fp6 workspace amd_strix_halo_kernels_launch_gemm_noalloc accepts.
+NOALLOC_SCRATCH_BYTES = 128 * 1024 * 1024
 
 # Tile schedules (reference metadata.KernelSchedule): STANDARD launches one
 # workgroup per tile, PERSISTENT one per resident slot, striding over tiles.

@@ -82,6 +82,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_launch_gemm_ws.argtypes = [I, I, U, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P,
                                                           ctypes.c_uint64]
     lib.amd_strix_halo_kernels_launch_gemm_ws.restype = I
+    lib.amd_strix_halo_kernels_launch_gemm_noalloc.argtypes = [I, I, U, P, P, P, P, P, I32, I32, I32, I32, I32,
+                                                               I32]
+    lib.amd_strix_halo_kernels_launch_gemm_noalloc.restype = I
     lib.amd_strix_halo_kernels_gemm_convert.argtypes = [I, I, U, I32, P, I32, I32, I32, P, ctypes.c_uint64]
     lib.amd_strix_halo_kernels_gemm_convert.restype = I
     lib.amd_strix_halo_kernels_launch_gemm_converted.argtypes = [I, I, U, P, P, P, I32, I32, I32, I32, I32, P,

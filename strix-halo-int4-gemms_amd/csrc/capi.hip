@@ -128,6 +128,38 @@ class DeviceGuard {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+}  // namespace
+
+// Scratch of amd_strix_halo_kernels_launch_gemm_noalloc: the fp6 operand
+// workspace of callers that cannot allocate device memory.  Each device the
+// library runs on holds its own copy from the code object's load until the
+// process ends.  In host code `scratch` names a host-side stand-in, never the
+// device array: kernels and copies get the per-device address from
+// scratch_address() instead.
+static __device__ __align__(256) uint8_t scratch[SHK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Device address of `scratch` on the current device (`device`), looked up
+// once per device with hipGetSymbolAddress and cached.
+int scratch_address(int device, void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex lock;
+  static void* cache[kMaxDevices] = {};
+  if (device < 0 || device >= kMaxDevices)
+    return fail("device index " + std::to_string(device) + " is out of range for the scratch table");
+  std::lock_guard<std::mutex> g(lock);
+  if (cache[device] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return fail_hip("hipGetSymbolAddress(scratch)", err);
+    if (p == nullptr || !aligned(p, 256)) return fail("the scratch array has no usable device address");
+    cache[device] = p;
+  }
+  *ptr = cache[device];
+  return 0;
+}
+
 int lookup(int index, int family, const Entry** out) {
   const auto& t = table();
   if (index < 0 || index >= (int)t.size()) {
@@ -172,6 +204,11 @@ uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, i
 // Largest K for which the x16-widened int4 products of one int32 accumulator
 // cannot overflow: 128 * 128 * K < 2^31.
 constexpr int kMaxInt4AccK = 131072;
+
+// Workspace argument of prepare_dense for a call that runs in the library's
+// scratch array: validated against the array's size; the caller sets the
+// workspace pointer (p.work) to the array's device address afterwards.
+void* const kScratchPending = reinterpret_cast<void*>(static_cast<uintptr_t>(256));
 
 // A validated dense call.  PHASE_ALL is a whole launch; the other phases are
 // the separately launched parts of a fp6 entry: converting A, converting B,
@@ -242,7 +279,15 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
   if (!fp6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
                 std::to_string(k));
-  if (fp6) {
+  if (fp6 && workspace == kScratchPending) {
+    // the no-allocation entry point: the library's scratch array, whose
+    // device address the caller fills in after validation
+    const uint64_t need = dense_workspace_bytes(d, m, n, k);
+    if (need > workspace_bytes)
+      return fail("kernel " + std::to_string(kernel_index) + " needs " + std::to_string(need) +
+                  " bytes of scratch for this shape; the no-allocation entry point's scratch holds at most " +
+                  std::to_string(workspace_bytes) + " bytes (use amd_strix_halo_kernels_launch_gemm_ws)");
+  } else if (fp6) {
     const uint64_t need = dense_workspace_bytes(d, m, n, k);
     if (workspace == nullptr || workspace_bytes < need)
       return fail("kernel " + std::to_string(kernel_index) + " converts its operands into a workspace of " +
@@ -407,6 +452,30 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
     return 1;
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  const unsigned split = c.e->d.split_k > 1 ? (unsigned)c.e->d.split_k : 1u;
+  const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles, split), reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail_hip("kernel launch", err);
+  return 0;
+}
+
+int amd_strix_halo_kernels_launch_gemm_noalloc(int kernel_index, int device_index, uintptr_t stream, const void* a,
+                                               const void* b, const void* a_scale, const void* b_scale, void* out,
+                                               int32_t m, int32_t n, int32_t k, int32_t subchannel,
+                                               int32_t epilogue, int32_t out_mode) {
+  g_last_error.clear();
+  DenseCall c;
+  if (prepare_dense(c, kernel_index, PHASE_ALL, a, b, a_scale, b_scale, out, m, n, k, subchannel, epilogue,
+                    out_mode, kScratchPending, SHK_NOALLOC_SCRATCH_BYTES))
+    return 1;
+  DeviceGuard guard(device_index);
+  if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+  if (c.e->d.operand_format == SHK_OPERANDS_FP6) {
+    void* ptr = nullptr;
+    if (scratch_address(device_index, &ptr)) return 1;
+    c.p.work = static_cast<uint8_t*>(ptr);
+  } else {
+    c.p.work = nullptr;
+  }
   const unsigned split = c.e->d.split_k > 1 ? (unsigned)c.e->d.split_k : 1u;
   const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles, split), reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail_hip("kernel launch", err);

@@ -101,6 +101,22 @@ def test_gemm_tile_multiple_messages_follow_the_reference(lib):
     assert "must be positive" in _err(lib)
 
 
+def test_noalloc_validates_before_touching_the_device(lib):
+    f6 = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, scale_mode=0, epilogue_kind=0,
+                      operand_format=kt.OPERANDS_FP6, schedule=0, split_k=1)
+    noalloc = lib.amd_strix_halo_kernels_launch_gemm_noalloc
+    # 0.75 * (16384 * 16384 * 2) bytes of fp6 operands do not fit the scratch
+    assert noalloc(f6, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, 16384, 16384, 16384, 0, 0, 0) == 1
+    assert f"scratch holds at most {kt.NOALLOC_SCRATCH_BYTES} bytes" in _err(lib)
+    need = ctypes.c_uint64(0)
+    assert lib.amd_strix_halo_kernels_gemm_workspace_bytes(f6, 8192, 8192, 8192, ctypes.byref(need)) == 0
+    assert need.value <= kt.NOALLOC_SCRATCH_BYTES  # C2 fits
+    assert noalloc(f6, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, 100, 256, 128, 0, 0, 0) == 1
+    assert "M=100 is not divisible by BLOCK_M=256" in _err(lib)
+    assert noalloc(f6, 0, 0, 0, FAKE, FAKE, FAKE, FAKE, 256, 256, 128, 0, 0, 0) == 1
+    assert "non-null" in _err(lib)
+
+
 def test_gemm_rejects_mismatched_modes(lib):
     pc = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=0, epilogue_kind=0)
     sc = _dense_index(dtype_bits=4, layout=0, block_m=64, block_n=64, scale_mode=1, epilogue_kind=0,
