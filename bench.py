@@ -9,6 +9,7 @@ K-ragged backward, G=8, M=8192, K=2048, N=1408), and the device
 quantize-and-pack of a C2-sized bf16 operand (GB/s against HBM).
 
     python bench.py [--steps K] [--warmup W] [--no-secondary] [--no-cpu-baseline]
+                    [--only c2|c3|c4|c5|c2p|quant]
 
 A step is one API call over operands already resident in HBM; the timed region
 is exactly K steps bracketed by a device synchronisation on both sides.
@@ -327,18 +328,44 @@ def bench_c5(torch, shk, steps, warmup):
         raise RuntimeError("ragged backward: direct launch differs from the API call")
 
     wall_b, kern_b, _ = _time_steps(torch, bwd, steps, warmup)
+
+    # The public calls, as the reference's ragged benchmark times them
+    # (autotune.py:746-777): host validation of group_sizes (one device-to-host
+    # copy and sync per call) plus the same device work.
+    def api_fwd():
+        return shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb, out=out_f)
+
+    def api_bwd():
+        return shk.ragged_dot_int4_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, out=out_b)
+
+    api_wall_f, api_kern_f, _ = _time_steps(torch, api_fwd, steps, warmup)
+    api_wall_b, api_kern_b, _ = _time_steps(torch, api_bwd, steps, warmup)
     ops_b = 2 * 2048 * n * rows
     bytes_b = groups * 2048 * cap // 2 + groups * cap * n // 2 + 2 * groups * (2048 + n) + 4 * groups * 2048 * n
     return {
         "group_sizes": sizes.tolist(),
         "fwd": {"kernel_ms": kern_f, "wall_ms": wall_f, "tops": ops / (kern_f * 1e-3) / 1e12,
+                "api_wall_ms": api_wall_f, "api_event_ms": api_kern_f,
                 "gbs": bytes_f / (kern_f * 1e-3) / 1e9,
                 "frac_hbm": bytes_f / (kern_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
                 "frac_int8_peak": ops / (kern_f * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS},
         "bwd": {"kernel_ms": kern_b, "wall_ms": wall_b, "tops": ops_b / (kern_b * 1e-3) / 1e12,
+                "api_wall_ms": api_wall_b, "api_event_ms": api_kern_b,
                 "gbs": bytes_b / (kern_b * 1e-3) / 1e9,
                 "frac_hbm": bytes_b / (kern_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(torch, host, target_s: float = 12.0):
@@ -370,8 +397,19 @@ def cpu_baseline(torch, host, target_s: float = 12.0):
         rows = min(m, max(rows * 2, int(rows * target_s / max(secs, 1e-3) * 1.1)))
     ops = 2 * rows * n * k
     return {"value": ops / secs / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(), "torch": torch.__version__,
             "sample": f"C2 rows 0..{rows - 1} of 8192 (N=K=8192, full unpack->int32 matmul->scale->bf16), "
                       f"{secs:.1f} s"}
+
+
+# single configurations of --only: (name, runner)
+_ONLY = {
+    "c3": ("c3_int4_sc256_relu2_4096x16384x4096", bench_c3),
+    "c4": ("c4_int8_swiglu_4096x11008x4096", bench_c4),
+    "c5": ("c5_ragged_g8_m8192_k2048_n1408", bench_c5),
+    "c2p": ("c2_persistent_schedule_8192_cubed", bench_c2_persistent),
+    "quant": ("quantize_pack_int4_8192x8192_bf16", bench_quant),
+}
 
 
 def main(argv=None) -> int:
@@ -381,6 +419,8 @@ def main(argv=None) -> int:
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", choices=sorted(_ONLY) + ["c2"],
+                   help="run one configuration and print its figures (for profiler runs)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a 256 MiB device-to-device copy 5 times (HBM counter calibration)")
     args = p.parse_args(argv)
@@ -404,6 +444,14 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": COPY_BYTES, "launches": 5}), flush=True)
         return 0
+    if args.only and args.only != "c2":
+        name, fn = _ONLY[args.only]
+        _log(f"bench: {name} only")
+        res = fn(torch, shk, args.steps, args.warmup)
+        print(json.dumps({"only": name, "steps": args.steps, "warmup": args.warmup, "result": res}), flush=True)
+        return 0
+    if args.only == "c2":
+        args.no_secondary = args.no_cpu_baseline = True
     _log("bench: C2 int4 per-channel 8192^3")
     c2 = bench_c2(torch, shk, args.steps, args.warmup)
     tops_kernel = c2["ops"] / (c2["kernel_ms"] * 1e-3) / 1e12
