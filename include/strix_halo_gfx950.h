@@ -69,7 +69,12 @@ extern "C" {
  * FP6 kernels (int4 only) first convert both operands into a caller
  * workspace of amd_strix_halo_kernels_gemm_workspace_bytes() bytes: every
  * int4 value v is exact as v/8 in the 6-bit float e2m3, whose MFMA runs at
- * twice the int8 rate; the fp32 accumulation is exact for K <= 262144. */
+ * twice the int8 rate; one fp32 pass is exact for K <= 262144, and
+ * per-channel calls with a longer K (up to 2^24) run in exact K slices of
+ * 262144 whose int32 sums add in the workspace before one pass applies the
+ * scales and the epilogue.  The int8 engines' int4 per-channel entries hold
+ * x16-widened products and need K < 131072 per int32 accumulator (per K
+ * slice for split-K entries). */
 #define SHK_OPERANDS_PACKED 0
 #define SHK_OPERANDS_FP6 1
 
@@ -112,7 +117,10 @@ typedef struct shk_kernel_desc {
   int32_t operand_format;  /* SHK_OPERANDS_* */
   int32_t schedule;        /* SHK_SCHEDULE_* */
   int32_t split_k;         /* K slices per output tile (dense); > 1: float32 output that the
-                              slices add into with atomics, so `out` must hold zeros */
+                              slices add into with hardware float atomics, so `out` must hold
+                              zeros and be coarse-grained device memory (hipMalloc, torch's
+                              allocator); the slices add in a run-dependent order, so the last
+                              bits of a result may differ from run to run */
 } shk_kernel_desc;
 
 /* ---- status (reference dispatch.cpp:206-222) ---------------------------- */

@@ -2,7 +2,8 @@
 
 ``kernel_supports_shape`` is the reference's rule: the shape is a multiple
 of the tile (and of the subchannel), the kernel has no K tail, and fused
-RELU2 / SwiGLU epilogues never run split-K.  ``estimate_kernel_score`` ranks
+RELU2 / SwiGLU epilogues never run split-K; K must also be within the
+kernel's gfx950 bound.  ``estimate_kernel_score`` ranks
 a kernel by a benchmark database record for the exact shape when there is
 one, otherwise by the kernel's measured MI355X throughput divided by its
 split-K factor.  The reference's extra weight for its 64x512x64 Triton tile
@@ -12,6 +13,7 @@ MI355X.
 
 from __future__ import annotations
 
+from . import kernel_table as kt
 from .benchmarking import BenchmarkDatabase, BenchmarkShape
 from .metadata import Epilogue, GemmLayout, KernelMetadata, KernelSchedule, OperandDType, ScaleSpec
 from .registry import KernelRegistry, default_registry
@@ -19,9 +21,12 @@ from .template_config import LaunchShape, is_tile_multiple_shape
 
 
 def kernel_supports_shape(kernel: KernelMetadata, *, m: int, n: int, k: int) -> bool:
+    """The reference's rule, plus the K bound of the kernel's gfx950 table
+    entry (its int32 accumulators and buffer offsets)."""
     if kernel.epilogue in {Epilogue.RELU2, Epilogue.SWIGLU} and kernel.tile.split_k != 1:
         return False
-    return kernel.tile.even_k and is_tile_multiple_shape(kernel, LaunchShape(m, n, k))
+    return (kernel.tile.even_k and is_tile_multiple_shape(kernel, LaunchShape(m, n, k))
+            and (kernel.table_index is None or kt.TABLE[kernel.table_index].supports_k(k)))
 
 
 def estimate_kernel_score(

@@ -45,6 +45,14 @@ OUT_I32 = 2
 OPERANDS_PACKED = 0
 OPERANDS_FP6 = 1
 FP6_MAX_K = 262144
+# Largest K of the fp6 entries (32-bit buffer offsets of a tile's panels);
+# per-channel calls with K > FP6_MAX_K run in exact K slices of FP6_MAX_K
+# whose int32 sums add into the workspace, except on the persistent tile.
+FP6_MAX_K_SLICED = 1 << 24
+# Largest K per int32 accumulator of the int8 engines' int4 per-channel
+# entries: products are widened x16, so |sum| <= 128 * 128 * K < 2^31 needs
+# K < 131072 (K = 131072 overflows when every product is (-8) * (-8)).
+INT4_ACC_MAX_K = 131071
 # Bytes of the library's static scratch array (SHK_NOALLOC_SCRATCH_BYTES): the
 # largest fp6 workspace amd_strix_halo_kernels_launch_gemm_noalloc accepts.
 NOALLOC_SCRATCH_BYTES = 128 * 1024 * 1024
@@ -92,11 +100,33 @@ class KernelDesc:
         return self.operand_format == OPERANDS_FP6
 
     def workspace_bytes(self, m: int, n: int, k: int) -> int:
-        """Bytes of the operand workspace for shape (m, n, k) (0 for PACKED)."""
+        """Bytes of the operand workspace for shape (m, n, k) (0 for PACKED);
+        per-channel calls with K > FP6_MAX_K add [m, b_cols] int32 sums."""
         if not self.needs_workspace:
             return 0
         b_cols = 2 * n if self.epilogue_kind == EPI_KIND_SWIGLU else n
-        return (m * k * 3) // 4 + (b_cols * k * 3) // 4
+        nbytes = (m * k * 3) // 4 + (b_cols * k * 3) // 4
+        if self.scale_mode == SCALE_PER_CHANNEL and k > FP6_MAX_K:
+            nbytes += 4 * m * b_cols
+        return nbytes
+
+    @property
+    def max_k(self) -> int | None:
+        """Largest logical K a dense entry runs (None: no bound), as the
+        library checks it (capi.hip dense_max_k)."""
+        if self.family != FAMILY_DENSE:
+            return None
+        if self.operand_format == OPERANDS_FP6:
+            if self.scale_mode == SCALE_PER_CHANNEL and self.schedule == SCHEDULE_PERSISTENT:
+                return FP6_MAX_K
+            return FP6_MAX_K_SLICED
+        if self.dtype_bits == 4 and self.scale_mode == SCALE_PER_CHANNEL:
+            return INT4_ACC_MAX_K * max(1, self.split_k)
+        return None
+
+    def supports_k(self, k: int) -> bool:
+        bound = self.max_k
+        return bound is None or k <= bound
 
     def ragged_workspace_bytes(self, m: int, n: int, k_packed: int, groups: int) -> int:
         """Bytes of the operand workspace of a ragged call (0 for PACKED):

@@ -121,6 +121,14 @@ def _matches(kernel: KernelMetadata, dtype, scale, epilogue, layout, schedule, s
     )
 
 
+def _runs_k(kernel: KernelMetadata, k: int) -> bool:
+    """The library's K bound of the kernel's table entry (gfx950 accumulators
+    and buffer offsets); kernels without a table entry have none."""
+    if kernel.table_index is None:
+        return True
+    return kt.TABLE[kernel.table_index].supports_k(k)
+
+
 class KernelRegistry:
     def __init__(self, kernels: Iterable[KernelMetadata] = ()) -> None:
         self._kernels: dict[str, KernelMetadata] = {}
@@ -158,6 +166,7 @@ class KernelRegistry:
             for kernel in self._kernels.values()
             if _matches(kernel, dtype, scale, epilogue, layout, schedule, split_k)
             and is_tile_multiple_shape(kernel, shape)
+            and _runs_k(kernel, k)
         ]
         if require_compiled:
             candidates = [c for c in candidates if c.status in {KernelStatus.COMPILED, KernelStatus.BENCHMARKED}]

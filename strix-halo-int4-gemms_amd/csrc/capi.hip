@@ -194,16 +194,34 @@ int check_out_mode(int out_mode) {
 }
 
 // Workspace of a dense entry: both operands in fp6 block format for FP6
-// entries, nothing otherwise.
+// entries (and for per-channel calls with K > F6_MAX_K, the [m, b_cols]
+// int32 sums of their K slices past the operands), nothing otherwise.
 uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k) {
   if (d.operand_format != SHK_OPERANDS_FP6) return 0;
   const long b_cols = d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2L * n : (long)n;
-  return shk::f6_operand_bytes(m, k) + shk::f6_operand_bytes(b_cols, k);
+  uint64_t bytes = shk::f6_operand_bytes(m, k) + shk::f6_operand_bytes(b_cols, k);
+  if (d.scale_mode == SHK_SCALE_PER_CHANNEL && k > shk::F6_MAX_K) bytes += 4ull * (uint64_t)m * (uint64_t)b_cols;
+  return bytes;
 }
 
 // Largest K for which the x16-widened int4 products of one int32 accumulator
-// cannot overflow: 128 * 128 * K < 2^31.
-constexpr int kMaxInt4AccK = 131072;
+// cannot overflow: |sum| <= 128 * 128 * K < 2^31, so K < 131072 (at K =
+// 131072 a row and column of -8 sum to exactly 2^31).  A split-K entry's
+// accumulator holds one slice of K / split values.
+constexpr int kMaxInt4AccK = 131071;
+
+// Largest K a dense entry runs: fp6 entries up to F6_MAX_K_SLICED, except
+// the persistent per-channel tile, which multiplies whole K in one pass
+// (F6_MAX_K); int4 per-channel entries of the int8 engines kMaxInt4AccK per
+// K slice; no bound otherwise.
+long dense_max_k(const shk_kernel_desc& d) {
+  if (d.operand_format == SHK_OPERANDS_FP6)
+    return (d.scale_mode == SHK_SCALE_PER_CHANNEL && d.schedule == SHK_SCHEDULE_PERSISTENT) ? shk::F6_MAX_K
+                                                                                            : shk::F6_MAX_K_SLICED;
+  if (d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL)
+    return (long)kMaxInt4AccK * (d.split_k > 1 ? d.split_k : 1);
+  return 0x7FFFFFFFL;
+}
 
 // Workspace argument of prepare_dense for a call that runs in the library's
 // scratch array: validated against the array's size; the caller sets the
@@ -274,11 +292,13 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
     if (swiglu ? epilogue != SHK_EPILOGUE_SWIGLU : (epilogue != SHK_EPILOGUE_NONE && epilogue != SHK_EPILOGUE_RELU2))
       return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
   }
-  if (fp6 && k > shk::F6_MAX_K)
-    return fail("fp6 kernels support K <= " + std::to_string(shk::F6_MAX_K) + "; got " + std::to_string(k));
-  if (!fp6 && d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
-    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) + "; got " +
-                std::to_string(k));
+  if (k > dense_max_k(d)) {
+    if (fp6) return fail("kernel " + std::to_string(kernel_index) + " supports K <= " +
+                         std::to_string(dense_max_k(d)) + "; got " + std::to_string(k));
+    return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) +
+                (split > 1 ? " per K slice (K/SPLIT_K); got K/SPLIT_K=" + std::to_string(k / split)
+                           : "; got " + std::to_string(k)));
+  }
   if (fp6 && workspace == kScratchPending) {
     // the no-allocation entry point: the library's scratch array, whose
     // device address the caller fills in after validation

@@ -50,6 +50,11 @@ typedef _Float16 f6_h32 __attribute__((ext_vector_type(32)));
 
 constexpr int F6_BLOCK = 1536;     // bytes of a 32-row x 64-K fp6 block
 constexpr int F6_MAX_K = 262144;   // 64 * K <= 2^24: fp32 partial sums stay exact
+// Largest K of the fp6 entries.  Per-channel calls with K > F6_MAX_K run in
+// K slices of F6_MAX_K, each exact, whose int32 sums add into an int32
+// workspace (exact while |sum| < 2^31, i.e. K < 2^25); the bound here comes
+// from the 32-bit buffer offsets of one tile's 8 panels (8 * 24 * K < 2^32).
+constexpr int F6_MAX_K_SLICED = 1 << 24;
 constexpr int F6_TILE = 256;       // packed rows per GEMM tile (A rows, B columns)
 // Each operand holds v/8, so the accumulator is sum / 64; multiplying by 64
 // is exact.
@@ -157,8 +162,10 @@ struct F6Engine {
 
   // a6 / b6: block-format operands; the tile's first panels are m0 / 32 and
   // 8 * bt (bt: B tile index).
+  // kb0: first 64-K block of the K range this workgroup multiplies (a K
+  // slice of a large-K launch; 0 otherwise).
   __device__ __forceinline__ void setup(uint8_t* smem, const uint8_t* a6, const uint8_t* b6, int m0, int bt, int kb,
-                                        unsigned long long a_bytes, unsigned long long b_bytes) {
+                                        unsigned long long a_bytes, unsigned long long b_bytes, int kb0 = 0) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     wm = wave % 2;
@@ -167,7 +174,8 @@ struct F6Engine {
     const unsigned long long panel_bytes = (unsigned long long)kb * F6_BLOCK;
     const bool is_a = wave < 2;
     const unsigned long long first =
-        (is_a ? (unsigned long long)(m0 / 32) : (unsigned long long)bt * 8) * panel_bytes;
+        (is_a ? (unsigned long long)(m0 / 32) : (unsigned long long)bt * 8) * panel_bytes +
+        (unsigned long long)kb0 * F6_BLOCK;
     rs = buffer_words((is_a ? a6 : b6) + first, (is_a ? a_bytes : b_bytes) - first);
     // DMA load c of this wave fills stage bytes [1024 * (DPW*wave + c), +1024):
     // panel o / PANEL of the operand, byte o % PANEL of its two blocks
@@ -656,27 +664,61 @@ __device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint
   }
 }
 
+// Adds a wave's exact integer sums into the int32 buffer out ([M, ld],
+// SwiGLU: up columns, then the gate's at +n), as a K slice of a large-K
+// launch does.  Integer adds commute, so the total is exact and the same in
+// every order.
+template <class C, class E>
+__device__ __forceinline__ void f6_add_i32(const E& e, int32_t* out, int ld, int n, int m0, int n0) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int32_t* row = out + (long)(m0 + e.out_row(i)) * ld + n0;
+#pragma unroll
+    for (int j = 0; j < E::FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int c = e.out_col(j, q) + t;
+          __hip_atomic_fetch_add(row + c, e.acc_int(i, j, 4 * q + t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if constexpr (C::SWIGLU)
+            __hip_atomic_fetch_add(row + n + c, e.acc_int(i, j + 2, 4 * q + t), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+  }
+}
+
 // One output tile of the fp6 GEMM: tile index `tile` in the XCD-aware order
-// of dense_tile_coords.
+// of dense_tile_coords.  OUT_I32_ADD: K slice blockIdx.y of F6_MAX_K values
+// (the last one shorter), added into the int32 buffer p.out ([M, b_cols]).
 template <class C, int MODE, int EPI, bool PERSIST = false>
 __device__ __forceinline__ void f6_gemm_tile(const DenseArgs& p, uint8_t* smem, int tile) {
   using E = F6Engine<C>;
+  constexpr bool RAW = MODE == OUT_I32 || MODE == OUT_I32_ADD;
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
   dense_tile_coords(tile, tiles_m, tiles_n, p.group_m, tm, tn);
   const int m0 = tm * C::BM;
   const int n0 = tn * C::BN;
+  int k0 = 0, klen = p.K;
+  if constexpr (MODE == OUT_I32_ADD) {
+    k0 = (int)blockIdx.y * F6_MAX_K;
+    klen = min(F6_MAX_K, p.K - k0);
+  }
   E e;
-  e.setup(smem, p.a, p.b, m0, tn, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.b_cols, p.K));
+  e.setup(smem, p.a, p.b, m0, tn, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.b_cols, p.K), k0 / 64);
   if constexpr (PERSIST) e.mfma_clear();
   float sa[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
-  const OutView o = dense_view<C, MODE>(p);
-  mfma32_prefetch_b_scales<C, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
-  e.run(p.K / 128);
-  mfma32_finish<C, MODE, EPI>(e, o, smem, m0, n0, sa);
+  for (int i = 0; i < 4; ++i) sa[i] = RAW ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
+  const OutView o = dense_view<C, RAW ? OUT_I32 : MODE>(p);
+  if constexpr (!RAW) mfma32_prefetch_b_scales<C, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
+  e.run(klen / 128);
+  if constexpr (MODE == OUT_I32_ADD)
+    f6_add_i32<C>(e, static_cast<int32_t*>(p.out), p.b_cols, p.N, m0, n0);
+  else
+    mfma32_finish<C, MODE, EPI>(e, o, smem, m0, n0, sa);
 }
 
 // One kernel per output mode and epilogue (chosen by the host), so that

@@ -28,8 +28,10 @@
 
 namespace shk {
 
-// OUT_F32_ADD is internal: a split-K slice adds its fp32 partial into out.
-enum OutMode : int { OUT_BF16 = 0, OUT_F32 = 1, OUT_I32 = 2, OUT_F32_ADD = 3 };
+// OUT_F32_ADD and OUT_I32_ADD are internal: a split-K slice adds its fp32
+// partial into out; a K slice of a large-K fp6 launch adds its exact int32
+// sums into an int32 workspace.
+enum OutMode : int { OUT_BF16 = 0, OUT_F32 = 1, OUT_I32 = 2, OUT_F32_ADD = 3, OUT_I32_ADD = 4 };
 enum EpiKind : int { EPI_NONE = 0, EPI_RELU2 = 1 };
 
 template <int BITS_, bool A_KMAJOR_, bool B_KMAJOR_, int BM_, int BN_, int BK_, int WM_, int WN_,

@@ -44,11 +44,31 @@ inline bool f6_mn_major(const DenseArgs& a, int operand) {
 inline hipError_t f6_convert_operand(const DenseArgs& a, int operand, bool swiglu, hipStream_t s) {
   return launch_f6_pack(f6_pack_args(a, operand, swiglu), f6_mn_major(a, operand), s);
 }
+// Large-K per-channel fp6 calls (K > F6_MAX_K): the int32 sums of the K
+// slices go to the workspace past both converted operands, [M, b_cols]
+// int32, which f6_large_k_begin clears and f6_large_k_end turns into the
+// output (scales and epilogue, or the raw sums) (k_f6.hip).
+inline int32_t* f6_large_k_acc(const DenseArgs& a) {
+  return reinterpret_cast<int32_t*>(a.work + f6_operand_bytes(a.M, a.K) + f6_operand_bytes(a.b_cols, a.K));
+}
+hipError_t f6_large_k_begin(const DenseArgs& a, hipStream_t s);
+hipError_t f6_large_k_end(const DenseArgs& a, bool swiglu, hipStream_t s);
+
 template <class C>
 hipError_t launch_f6_gemm_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   DenseArgs g = a;
   g.a = a.work;
   g.b = a.work + f6_operand_bytes(a.M, a.K);
+  if (a.K > F6_MAX_K) {
+    hipError_t err = f6_large_k_begin(a, s);
+    if (err != hipSuccess) return err;
+    g.out = f6_large_k_acc(a);
+    const unsigned slices = (unsigned)((a.K + F6_MAX_K - 1) / F6_MAX_K);
+    hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_I32_ADD, EPI_NONE>), dim3(grid.x, slices), dim3(256), 0, s, g);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return f6_large_k_end(a, C::SWIGLU, s);
+  }
   if (a.out_mode == OUT_I32) {
     hipLaunchKernelGGL((f6_gemm_kernel<C, OUT_I32, EPI_NONE>), grid, dim3(256), 0, s, g);
   } else if (a.out_mode == OUT_F32) {

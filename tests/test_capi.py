@@ -130,7 +130,9 @@ def test_gemm_rejects_mismatched_modes(lib):
     assert _gemm(lib, pc, 64, 64, 64, mode=7) == 1
     assert "output mode" in _err(lib)
     assert _gemm(lib, pc, 64, 64, 262144) == 1
-    assert "K <= 131072" in _err(lib)
+    assert "K <= 131071" in _err(lib)
+    assert _gemm(lib, pc, 64, 64, 131072) == 1  # a -8 row times a -8 column would sum to 2^31
+    assert "K <= 131071" in _err(lib)
     assert _gemm(lib, pc, 64, 64, 64, out=FAKE + 4) == 1
     assert "aligned" in _err(lib)
 
@@ -229,12 +231,36 @@ def test_fp6_launch_needs_a_workspace(lib):
     assert "16-byte aligned" in _err(lib)
 
 
-def test_fp6_k_limit_keeps_fp32_sums_exact(lib):
-    # |sum| <= 64 * K must stay <= 2^24 for the fp32 accumulation to be exact
-    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_FP6)
+def test_fp6_k_bounds(lib):
+    # one fp32 pass is exact while |sum| <= 64 * K <= 2^24; a longer K runs in
+    # slices of FP6_MAX_K whose int32 sums add into the workspace, up to
+    # FP6_MAX_K_SLICED; the persistent tile multiplies K in one pass
+    idx = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_FP6,
+                       schedule=kt.SCHEDULE_STANDARD, scale_mode=0, epilogue_kind=0)
+    per = _dense_index(dtype_bits=4, layout=0, block_m=256, block_n=256, operand_format=kt.OPERANDS_FP6,
+                       schedule=kt.SCHEDULE_PERSISTENT, scale_mode=0)
     assert kt.FP6_MAX_K * 64 == 1 << 24
-    assert _gemm_ws(lib, idx, 256, 256, kt.FP6_MAX_K + 128, work=FAKE, work_bytes=1 << 40) == 1
-    assert "K <= 262144" in _err(lib)
+    m = n = 256
+    k = kt.FP6_MAX_K + 128
+    need = (m + n) * k * 3 // 4 + 4 * m * n
+    assert _ws(lib, idx, m, n, k) == (0, need) and kt.TABLE[idx].workspace_bytes(m, n, k) == need
+    assert _gemm_ws(lib, idx, m, n, k, work=FAKE, work_bytes=need - 1) == 1
+    assert f"workspace of {need} bytes" in _err(lib)
+    assert _gemm_ws(lib, per, m, n, k, work=FAKE, work_bytes=1 << 40) == 1
+    assert f"supports K <= {kt.FP6_MAX_K}" in _err(lib)
+    assert _gemm_ws(lib, idx, m, n, kt.FP6_MAX_K_SLICED + 128, work=FAKE, work_bytes=1 << 62) == 1
+    assert f"supports K <= {kt.FP6_MAX_K_SLICED}" in _err(lib)
+    assert kt.TABLE[idx].max_k == kt.FP6_MAX_K_SLICED and kt.TABLE[per].max_k == kt.FP6_MAX_K
+
+
+def test_split_k_bound_is_per_slice(lib):
+    # each slice's int32 accumulator holds K / SPLIT_K x16-widened products
+    sk2 = _dense_index(dtype_bits=4, layout=0, block_m=128, block_n=128, scale_mode=0, epilogue_kind=0, split_k=2)
+    assert kt.TABLE[sk2].max_k == 2 * kt.INT4_ACC_MAX_K and kt.TABLE[sk2].supports_k(2 * kt.INT4_ACC_MAX_K)
+    k = 2 * 131072  # slices of 131072: one too many for an exact accumulator
+    assert lib.amd_strix_halo_kernels_launch_gemm(sk2, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, 128, 128, k, 0, 0,
+                                                  kt.OUT_F32) == 1
+    assert f"K <= {kt.INT4_ACC_MAX_K} per K slice (K/SPLIT_K); got K/SPLIT_K={k // 2}" in _err(lib)
 
 
 def test_split_fp6_phases_validate_their_arguments(lib):

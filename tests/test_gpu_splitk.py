@@ -55,15 +55,19 @@ def test_split_entries_cover_the_reference_families():
 
 
 @pytest.mark.parametrize("kernel", _SPLIT, ids=lambda k: k.kernel_id)
-def test_split_k_matches_oracle(kernel, device):
+@pytest.mark.parametrize("blocks", [1, 3])
+def test_split_k_matches_oracle(kernel, blocks, device):
+    """`blocks` K blocks (or scale groups) per slice; one is the shortest
+    slice a split entry accepts (K = BLOCK_K * SPLIT_K), where each slice's
+    pipeline runs a single stage."""
     bits = 4 if kernel.a_dtype is shk.OperandDType.INT4 else 8
     sub = _sub_of(kernel)
     m, n = 2 * kernel.tile.block_m, 2 * kernel.tile.block_n
-    # three slice lengths' worth of K blocks per slice, whole groups per slice
-    k = 3 * kernel.tile.block_k * kernel.tile.split_k
+    # whole groups per slice
+    k = blocks * kernel.tile.block_k * kernel.tile.split_k
     if sub:
-        k = 3 * kernel.tile.split_k * max(sub, kernel.tile.block_k)
-    seed = stable_seed("splitk", kernel.kernel_id)
+        k = blocks * kernel.tile.split_k * max(sub, kernel.tile.block_k)
+    seed = stable_seed("splitk", kernel.kernel_id, blocks)
     a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=kernel.layout.value, m=m, n=n, k=k,
                                                  subchannel=sub, swiglu=False)
     print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
@@ -77,6 +81,42 @@ def test_split_k_matches_oracle(kernel, device):
     got = _run(kernel, a_arg, b_arg, sa, sb, device)
     want = ref.scaled_mm(a_q, b_q, sa, sb, subchannel=sub)
     bound = ref.scaled_mm(np.abs(a_q.astype(np.int32)), np.abs(b_q.astype(np.int32)), sa & 0x7FFF, sb & 0x7FFF, subchannel=sub)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * bound.astype(np.float64) + 1e-30)
+
+
+@pytest.mark.parametrize("split", [2, 8])
+def test_split_k_large_k(split, device):
+    """int4 per-channel K of about 2^18, twice what one unsplit accumulator
+    of the int8 engines holds: each slice's int32 sum stays exact (K /
+    SPLIT_K < 131072; split 2: K = 262016, split 8: K = 262144).  Row 0 of A
+    and column 0 of B hold -8, so out[0, 0] = 64 * K, up to 2^24.
+    Unit scales give the exact integer product (every partial sum of the
+    slices is an integer of magnitude <= 2^24); random scales stay within the
+    fp32 bound of the other split tests.  The order of the slices' atomic
+    adds varies from run to run, so those results may differ in the last
+    bits between runs (the tolerance covers it)."""
+    kernel = next(k for k in _SPLIT if k.tile.split_k == split and k.scale.mode is shk.ScaleMode.PER_CHANNEL
+                  and k.a_dtype is shk.OperandDType.INT4 and k.layout is shk.GemmLayout.NN)
+    m, n = kernel.tile.block_m, kernel.tile.block_n
+    k = 262144 if split == 8 else 2 * (131072 - 64)
+    r = ref.rng(stable_seed("splitk-large", split))
+    a_q = ref.randint4(r, (m, k))
+    b_q = ref.randint4(r, (k, n))
+    a_q[0, :] = -8
+    b_q[:, 0] = -8
+    a_arg, b_arg = ref.pack_operands(a_q, b_q, bits=4, layout="nn")
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    ones_a = np.full((m,), ONE_BF16, dtype=np.uint16)
+    ones_b = np.full((n,), ONE_BF16, dtype=np.uint16)
+    exact = _run(kernel, a_arg, b_arg, ones_a, ones_b, device)
+    prod = ref.int_matmul(a_q, b_q)
+    assert prod[0, 0] == 64 * k
+    assert np.array_equal(exact, prod.astype(np.float32))
+    sa = ref.uniform_bf16(r, (m,), 0.005, 0.02)
+    sb = ref.uniform_bf16(r, (n,), 0.005, 0.02)
+    got = _run(kernel, a_arg, b_arg, sa, sb, device)
+    want = ref.scaled_mm(a_q, b_q, sa, sb, subchannel=None)
+    bound = ref.scaled_mm(np.abs(a_q.astype(np.int32)), np.abs(b_q.astype(np.int32)), sa, sb, subchannel=None)
     assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * bound.astype(np.float64) + 1e-30)
 
 

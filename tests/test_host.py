@@ -91,6 +91,34 @@ def test_select_raises_for_shapes_no_kernel_accepts():
                                     m=64, n=64, k=64, schedule=shk.KernelSchedule.PERSISTENT)
 
 
+def test_select_knows_each_entry_k_bound():
+    """K past an entry's gfx950 bound is never selected: int4 per-channel K
+    of 131072 and above skips the int8 engines' unsplit tiles (x16-widened int32
+    accumulators) for a split-K or fp6 entry, K above 262144 runs on the fp6
+    tile in K slices, and past 2^24 no kernel fits (LookupError, the
+    registry's contract for an unserved shape)."""
+    pc = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL)
+    for m, n, k in ((128, 128, 196608), (256, 256, 524288), (256, 256, kt.FP6_MAX_K_SLICED)):
+        kern = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=m, n=n,
+                                           k=k)
+        assert kt.TABLE[kern.table_index].supports_k(k), kern.kernel_id
+    kern = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=128,
+                                       n=128, k=196608)
+    assert kern.tile.split_k > 1
+    kern = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256,
+                                       n=256, k=524288)
+    assert kt.TABLE[kern.table_index].operand_format == kt.OPERANDS_FP6
+    with pytest.raises(LookupError):
+        shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256, n=256,
+                                    k=kt.FP6_MAX_K_SLICED + 128)
+    with pytest.raises(LookupError):
+        shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256, n=256,
+                                    k=524288, schedule=shk.KernelSchedule.PERSISTENT)
+    assert not shk.kernel_supports_shape(
+        next(k for k in shk.default_registry.all() if k.table_index is not None
+             and kt.TABLE[k.table_index].max_k == kt.INT4_ACC_MAX_K), m=256, n=256, k=262144)
+
+
 def test_select_reference_ignores_shape():
     k = shk.default_registry.select_reference(dtype=shk.OperandDType.INT8, scale=PC, epilogue=shk.Epilogue.RELU2)
     assert k.epilogue is shk.Epilogue.RELU2 and k.tile.split_k == 1

@@ -275,6 +275,110 @@ def test_ragged_bwd_empty_and_full_groups():
     assert np.array_equal(out[0], ref.scaled_mm(a[0, :, :5], b[0, :5], sa[0], sb[0], subchannel=None))
 
 
+def _f32(x) -> np.float32:
+    return np.float32(x)
+
+
+def _bf(bits) -> np.float32:
+    return ref.bf16_to_f32(np.uint16(bits))[()] if np.ndim(bits) == 0 else ref.bf16_to_f32(bits)
+
+
+@pytest.mark.parametrize("subchannel", [None, 4])
+def test_ragged_fwd_reference_brute_force_over_groups(subchannel):
+    """Element by element over five groups, one empty and one of a single
+    row: row i belongs to the group whose cumulative row span holds it, and
+    out[i, j] is (float(sum_k a[i,k] b[g,k,j]) * a_scale[i]) * b_scale[g, j]
+    (per-channel) or the K-ordered fp32 sum of the per-group products with
+    the last group partial (subchannel S = 4, K = 10), as the reference's
+    grouped references compute them (tests/test_ragged_dot.py:19-51)."""
+    r = ref.rng(41)
+    sizes = np.array([3, 0, 5, 1, 4])
+    m, k, n, groups = int(sizes.sum()), 10, 5, sizes.size
+    a_q = ref.randint4(r, (m, k))
+    b_q = ref.randint4(r, (groups, k, n))
+    if subchannel:
+        cols = -(-k // subchannel)
+        sa = ref.uniform_bf16(r, (m, cols), 0.01, 1.0)
+        sb = ref.uniform_bf16(r, (groups, cols, n), 0.01, 1.0)
+    else:
+        sa = ref.uniform_bf16(r, (m,), 0.01, 1.0)
+        sb = ref.uniform_bf16(r, (groups, n), 0.01, 1.0)
+    got = ref.ragged_fwd_reference(a_q, b_q, sizes, sa, sb, subchannel=subchannel)
+    owner = []
+    for g, sz in enumerate(sizes.tolist()):
+        owner += [g] * sz
+    for i in range(m):
+        g = owner[i]
+        for j in range(n):
+            if not subchannel:
+                acc = sum(int(a_q[i, kk]) * int(b_q[g, kk, j]) for kk in range(k))
+                v = _f32(_f32(acc) * _bf(sa[i]))
+                v = _f32(v * _bf(sb[g, j]))
+            else:
+                v = _f32(0.0)
+                for s, k0 in enumerate(range(0, k, subchannel)):
+                    acc = sum(int(a_q[i, kk]) * int(b_q[g, kk, j]) for kk in range(k0, min(k0 + subchannel, k)))
+                    p = _f32(_f32(acc) * _bf(sa[i, s]))
+                    p = _f32(p * _bf(sb[g, s, j]))
+                    v = _f32(v + p)
+            assert got[i, j].view(np.uint32) == v.view(np.uint32), (i, j, g)
+
+
+def test_ragged_bwd_reference_subchannel():
+    """Subchannel backward: a full-length group equals the dense subchannel
+    product (scaled_mm, pinned by the reference's golden vectors); a group
+    truncated inside a scale group sums only the scale groups that start
+    below its length, the last one cut at the length; an empty group is zero
+    (tests/test_ragged_dot.py:99-117)."""
+    r = ref.rng(42)
+    groups, rows, kcap, cols, sub = 3, 6, 24, 7, 8
+    a_q = ref.randint4(r, (groups, rows, kcap))
+    b_q = ref.randint4(r, (groups, kcap, cols))
+    sa = ref.uniform_bf16(r, (groups, rows, kcap // sub), 0.01, 1.0)
+    sb = ref.uniform_bf16(r, (groups, kcap // sub, cols), 0.01, 1.0)
+    sizes = np.array([kcap, 13, 0])
+    got = ref.ragged_bwd_reference(a_q, b_q, sizes, sa, sb, subchannel=sub)
+    assert np.array_equal(got[0], ref.scaled_mm(a_q[0], b_q[0], sa[0], sb[0], subchannel=sub))
+    assert (got[2] == 0).all()
+    gk = int(sizes[1])
+    for i in range(rows):
+        for j in range(cols):
+            v = _f32(0.0)
+            for s, k0 in enumerate(range(0, kcap, sub)):
+                k1 = min(k0 + sub, gk)
+                if k1 <= k0:
+                    continue
+                acc = sum(int(a_q[1, i, kk]) * int(b_q[1, kk, j]) for kk in range(k0, k1))
+                p = _f32(_f32(acc) * _bf(sa[1, i, s]))
+                p = _f32(p * _bf(sb[1, s, j]))
+                v = _f32(v + p)
+            assert got[1, i, j].view(np.uint32) == v.view(np.uint32), (i, j)
+    # the second scale group is cut at 13: K values 13..15 must not count
+    cut = a_q.copy()
+    cut[1, :, 13:] = 0
+    assert np.array_equal(got[1], ref.scaled_mm(cut[1], b_q[1], sa[1], sb[1], subchannel=sub))
+
+
+def test_bf16_ulp_diff_closed_forms():
+    """Distances on the bf16 line: adjacent values are 1 apart on either
+    side of zero, +0 and -0 coincide, a pair straddling zero is the sum of
+    the magnitudes' distances from zero, a binade holds 128 steps, and the
+    distance is symmetric."""
+    d = ref.bf16_ulp_diff
+    assert d(np.uint16(0x3F80), np.uint16(0x3F81)) == 1      # 1.0, next bf16
+    assert d(np.uint16(0xBF80), np.uint16(0xBF81)) == 1      # -1.0, next below
+    assert d(np.uint16(0x007F), np.uint16(0x0080)) == 1      # largest subnormal, smallest normal
+    assert d(np.uint16(0x0000), np.uint16(0x8000)) == 0      # +0, -0
+    assert d(np.uint16(0x0003), np.uint16(0x8002)) == 5      # 3 ulps above zero, 2 below
+    assert d(np.uint16(0x3F80), np.uint16(0x4000)) == 128    # 1.0 to 2.0
+    assert d(np.uint16(0x3F80), np.uint16(0xBF80)) == 2 * 0x3F80
+    a = np.array([0x1234, 0x8001, 0x7F7F], dtype=np.uint16)
+    b = np.array([0x1236, 0x0001, 0x7F7E], dtype=np.uint16)
+    assert d(a, b).tolist() == [2, 2, 1]
+    assert np.array_equal(d(a, b), d(b, a))
+    assert (d(a, a) == 0).all()
+
+
 # ---------------------------------------------------------------------------
 # C restatement vs numpy restatement
 
