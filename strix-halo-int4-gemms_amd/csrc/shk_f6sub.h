@@ -6,8 +6,9 @@
 //
 // Each group's partial products must be scaled on their own, so every S K
 // values the accumulators are folded into fp32 totals with VALU work; that
-// fold, not the MFMA, bounds this kernel.  The design keeps it at four VALU
-// operations per value and lets other waves' MFMAs run meanwhile:
+// fold, not the MFMA, bounds this kernel.  The design keeps it at two VALU
+// operations per value (a multiply by a * b from a rank-1 MFMA, and the add;
+// see fold()) and lets other waves' MFMAs run meanwhile:
 //  * the MFMA is the scaled form (v_mfma_scale_f32_32x32x64_f8f6f4) with a
 //    scale of 2^3 on both v/8 operands, so the accumulators hold the exact
 //    integer partial sums (no x64 pass), and the first MFMA of a group takes
@@ -72,6 +73,9 @@ struct F6SubEngine {
   int sb_row;    // bytes of one b_scale row (N * 2)
   uint32_t lds0;
   int lane, wave, wm, wn, m0;
+  // every group so far took the fast fold: all totals are sums of finite
+  // products below 2^110 in magnitude, so none is NaN
+  bool all_fast;
 
   __device__ __forceinline__ int out_row(int i) const { return wm * 64 + 32 * i + (lane & 31); }
   __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
@@ -116,6 +120,7 @@ struct F6SubEngine {
           acc[i][j][r] = 0.0f;
           tot[i][j][r] = 0.0f;
         }
+    all_fast = true;
   }
 
   // byte offset of this lane's scale dword for group g
@@ -263,16 +268,64 @@ struct F6SubEngine {
 
   // Folds group g's partial sums into the totals:
   // tot += (float(part) * a_scale[row, g]) * b_scale[g, col].
+  //
+  // Fast form, two VALU operations per value: tot += part * ab with
+  // ab = a_scale * b_scale from one rank-1 bf16 MFMA per 32 x 32 block.  It
+  // gives the same bits as the reference's order whenever every scale of the
+  // group is zero or a normal number of magnitude in [2^-60, 2^48): part is
+  // an integer of at most 15 significant bits (|part| <= 64 * 256) and a has
+  // 8, so part * a is exact, and a * b (16 bits, within the normal range) is
+  // exact too; both orders therefore round the same real product part*a*b
+  // once.  (A zero product's sign may differ, which changes no sum: the
+  // totals start at +0, and x + -0 = x + +0 for every x.)  A wave whose
+  // scales fall outside that range folds in the reference's order.
   __device__ __forceinline__ void fold(const uint8_t* smem, int g) {
     const uint8_t* sl = smem + RING + (g & 3) * SCALE_SLOT;
-    float sa[2];
+    uint32_t sa_bits[2], sb_bits[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int row = out_row(i);
       const uint32_t w = *reinterpret_cast<const uint32_t*>(sl + 4 * row);
       const int e = (m0 + row) * groups + g;
-      sa[i] = (e & 1) ? f6_bf16_hi(w) : f6_bf16_lo(w);
+      sa_bits[i] = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      sb_bits[j] = *reinterpret_cast<const uint16_t*>(sl + 512 + 2 * (wn * TN + 32 * j + (lane & 31)));
+    auto in_range = [](uint32_t b) {
+      return (b & 0x7FFFu) == 0u || (((b >> 7) & 0xFFu) - (127u - 60u)) < 108u;
+    };
+    const bool ok = in_range(sa_bits[0]) && in_range(sa_bits[1]) && in_range(sb_bits[0]) && in_range(sb_bits[1]);
+    if (__all(ok)) {
+      // second MFMA operand: a_scale of the block's 32 rows at K = 0 (lanes
+      // 0-31, first element); first operand: b_scale of its 32 columns
+      f6_bf8 ya[2], xb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ya[i] = f6_bf8{};
+        xb[i] = f6_bf8{};
+        if (lane < 32) {
+          ya[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sa_bits[i]);
+          xb[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sb_bits[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v16f ab = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[j], ya[i], v16f{}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float x = acc[i][j][r] * ab[r];
+            tot[i][j][r] = tot[i][j][r] + x;
+          }
+        }
+      return;
+    }
+    all_fast = false;
+    float sa[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sa[i] = __uint_as_float(sa_bits[i] << 16);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -366,7 +419,10 @@ struct F6SubEngine {
 // through its own 8 KiB region of the idle ring: unit u = 4j + q (columns
 // 8u .. 8u+7) of row r at r * 128 + 16 * (u ^ ((r / 2) % 8)), read back one
 // 128-byte row segment per 8 lanes.
-template <class E, class V>
+// NO_NAN: no value is NaN, so the hardware conversion (round to nearest
+// even, which keeps a NaN's payload where torch writes 0x7FC0) gives torch's
+// bits.
+template <bool NO_NAN, class E, class V>
 __device__ __forceinline__ void f6sub_store_bf16(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                                  V v) {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -381,8 +437,14 @@ __device__ __forceinline__ void f6sub_store_bf16(const E& e, const OutView& o, u
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int x = 4 * q;
-        const uint32_t lo = f32_to_bf16_rne(v(i, j, x)) | (f32_to_bf16_rne(v(i, j, x + 1)) << 16);
-        const uint32_t hi = f32_to_bf16_rne(v(i, j, x + 2)) | (f32_to_bf16_rne(v(i, j, x + 3)) << 16);
+        uint32_t lo, hi;
+        if constexpr (NO_NAN) {
+          lo = pack_bf16x2_nonan(v(i, j, x), v(i, j, x + 1));
+          hi = pack_bf16x2_nonan(v(i, j, x + 2), v(i, j, x + 3));
+        } else {
+          lo = f32_to_bf16_rne(v(i, j, x)) | (f32_to_bf16_rne(v(i, j, x + 1)) << 16);
+          hi = f32_to_bf16_rne(v(i, j, x + 2)) | (f32_to_bf16_rne(v(i, j, x + 3)) << 16);
+        }
         const int r = 32 * i + (lane & 31);
         *reinterpret_cast<uint2*>(region + r * 128 + 16 * (u ^ ((r >> 1) & 7)) + half) = make_uint2(lo, hi);
       }
@@ -442,7 +504,9 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
     f6sub_store_words(e, o, m0, n0,
                       [&](int i, int j, int x) { return __float_as_int(apply_epi(e.tot[i][j][x], EPI)); });
   } else {
-    f6sub_store_bf16(e, o, smem, m0, n0, [&](int i, int j, int x) { return apply_epi(e.tot[i][j][x], EPI); });
+    auto val = [&](int i, int j, int x) { return apply_epi(e.tot[i][j][x], EPI); };
+    if (e.all_fast) f6sub_store_bf16<true>(e, o, smem, m0, n0, val);
+    else f6sub_store_bf16<false>(e, o, smem, m0, n0, val);
   }
 }
 

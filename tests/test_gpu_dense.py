@@ -348,6 +348,32 @@ def test_fp6_subchannel_every_group_count(kernel, groups, device):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("kernel", _FP6_SUB, ids=lambda k: k.kernel_id)
+def test_fp6_subchannel_special_scales(kernel, device):
+    """The subchannel fold takes its two-operation form (a * b from a rank-1
+    MFMA) only for waves whose group scales are all zero or normal within
+    [2^-60, 2^60], and the reference's three-operation order otherwise.
+    Scales sprinkled with subnormals, huge finite values, infinities, NaN
+    and zeros put waves on both paths in every group; every output is
+    bit-identical to the oracle (NaN as the canonical 0x7FC0)."""
+    _, layout, sub, epi = _kernel_params(kernel)
+    m, n, k = 256, 256, 3 * sub
+    seed = stable_seed("sub-special", kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=sub,
+                                                 swiglu=False, scale_lo=0.001, scale_hi=0.1)
+    sa = _sprinkle(sa, seed, 37)
+    sb = _sprinkle(sb, seed + 1, 53)
+    big = ref.bf16_from_f32(np.float32(2.0 ** 61))
+    sa[200:, 1] = big  # the lower waves' second group: finite but outside the fast range
+    print(f"case {kernel.kernel_id} special scales shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, ref.int_matmul(a_q, b_q))
+    with np.errstate(over="ignore", invalid="ignore", under="ignore"):
+        want = ref.reference_gemm_bf16(a_arg, b_arg, bits=4, layout=layout, a_scale=sa, b_scale=sb, subchannel=sub,
+                                       epilogue=epi)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
 def test_fp6_exact_at_the_k_bound(layout, device):
     """K = 262144 with rows of A and columns of B constant: every output is
