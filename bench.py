@@ -298,7 +298,7 @@ def bench_c5(torch, shk, steps, warmup):
         return native.launch_ragged_fwd(lhs, rhs, gs, a_scale=sa, b_scale=sb, out=out_f,
                                         layout=shk.GemmLayout.NN, subchannel=None, block_m=kt.RAGGED_FP6_BLOCK_M,
                                         align_tile=kt.RAGGED_FP6_ALIGN, rows=rows, cols=n, k_packed=k // 2,
-                                        out_mode=kt.OUT_BF16)
+                                        out_mode=kt.OUT_BF16, fp6=True)
 
     ref_out = shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb)
     fwd()

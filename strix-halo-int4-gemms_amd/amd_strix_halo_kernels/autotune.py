@@ -17,10 +17,10 @@ Differences that follow from the MI355X build:
   * timing uses HIP events (``benchmarking.device_event_samples``) in place
     of triton's do_bench; the records say so in ``timing_backend``;
   * the default ragged candidates are the configs that select distinct
-    gfx950 kernels: one forward config per compiled row-tile height (the
-    256-row fp6 kernel included; block_m 64, the default config, also takes
-    the fp6 kernel where that kernel applies) and one backward config per
-    split-K factor.
+    gfx950 kernels: one forward config per compiled row-tile height of the
+    packed kernels, plus block_m 256, which asks for the fp6 kernel (block_m
+    64, the default config, also takes the fp6 kernel where that kernel
+    applies), and one backward config per split-K factor.
     Configs that differ only in fields the gfx950 launch ignores (block_n,
     block_k, warps, stages) would time the same kernel twice.
 Operands are synthetic, seeded from the kernel id and shape: uniform int4
@@ -218,7 +218,7 @@ def default_ragged_dot_candidates(
     layout = _check_layout(layout)
     split_ks = tuple(split_ks)
     if mode is RaggedDotMode.FWD:
-        heights = sorted(set(kt.RAGGED_FWD_BLOCK_M) | {kt.RAGGED_FP6_BLOCK_M})
+        heights = sorted(set(kt.RAGGED_FWD_BLOCK_M) | {kt.RAGGED_FP6_CONFIG_BLOCK_M})
         configs = [RaggedDotConfig(block_m=bm, align_tile=min(8, bm)) for bm in heights]
     else:
         configs = [RaggedBwdDotConfig(split_k=int(sk)) for sk in split_ks]

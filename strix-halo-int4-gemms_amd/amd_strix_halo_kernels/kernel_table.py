@@ -153,14 +153,20 @@ MFMA32_SCALE_BYTES = 4 * 256
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
-          fp6=False, fp6_sub=False, schedule=SCHEDULE_STANDARD, split_k=1):
+          fp6=False, fp6_sub=False, fp6_small=False, schedule=SCHEDULE_STANDARD, split_k=1):
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
     # fp6_sub: six stages of 128 + 128 rows x 64 K in fp6 (48 bytes) and a
     # four-group scale ring of 768 bytes per group (shk_f6sub.h).
+    # fp6_small: three stages of 128 A rows + 128 B rows x 128 K in fp6 (96
+    # bytes), then the B-scale slots (shk_f6small.h).
     brows = 2 * bn if swiglu else bn
-    if fp6_sub:
+    if fp6_small:
+        fp6 = True
+        pipe = 3
+        lds = pipe * (bm + bn) * 96 + MFMA32_SCALE_BYTES
+    elif fp6_sub:
         fp6 = True
         pipe = 6
         lds = pipe * (bm + bn) * 48 + 4 * 768
@@ -220,14 +226,16 @@ def _build() -> tuple[KernelDesc, ...]:
             add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, swiglu=True, subch=True, mk=32)
     for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN, LAYOUT_TT):
         # fp6 entries lead each family (k_ragged.hip)
-        add(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, group_m=1, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
+        add(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, group_m=1, bm=128, bn=128, bk=128, wm=2, wn=2,
+            fp6_small=True)
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             f = dict(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1)
             add(**f, bm=16, bn=128, bk=128, wm=1, wn=4)
             add(**f, bm=32, bn=128, bk=128, wm=2, wn=2)
             add(**f, bm=64, bn=128, bk=128, wm=2, wn=2)
             add(**f, bm=128, bn=128, bk=128, wm=2, wn=2)
-        add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, group_m=1, bm=256, bn=256, bk=128, wm=2, wn=2, fp6=True)
+        add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, group_m=1, bm=128, bn=128, bk=128, wm=2, wn=2,
+            fp6_small=True)
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1, bm=128, bn=128,
                 bk=128, wm=2, wn=2)
@@ -308,5 +316,8 @@ def ragged_fp6_eligible(family: int, *, subchannel: int | None, m: int, n: int, 
 # Task rows of the forward kernels that read packed operands, and of the fp6
 # forward (whose task list is built with align_tile 32).
 RAGGED_FWD_BLOCK_M = tuple(sorted({d.block_m for d in entries(FAMILY_RAGGED_FWD) if not d.needs_workspace}))
-RAGGED_FP6_BLOCK_M = 256
+RAGGED_FP6_BLOCK_M = 128
+# RaggedDotConfig.block_m that asks for the fp6 forward (as does the default,
+# 64, where the fp6 kernel applies); the other heights pick the packed kernels.
+RAGGED_FP6_CONFIG_BLOCK_M = 256
 RAGGED_FP6_ALIGN = 32

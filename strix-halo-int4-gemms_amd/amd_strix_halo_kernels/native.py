@@ -583,18 +583,20 @@ def launch_ragged_fwd(
     cols: int,
     k_packed: int,
     out_mode: int,
+    fp6: bool = False,
     library_path: str | Path | None = None,
     stream: Any | None = None,
 ) -> Any:
     """Device task list + grouped forward (replaces launch_ragged_fwd_kernel,
-    native.py:533-600).  No host synchronisation.  block_m 256
-    (kt.RAGGED_FP6_BLOCK_M) selects the fp6 entry, whose operands are
-    converted into a workspace and whose tasks need align_tile a multiple
-    of 32.  The task list, its count and the workspace share one
-    allocation."""
+    native.py:533-600).  No host synchronisation.  fp6: run the fp6 entry
+    (per-channel; block_m must be its task tile, kt.RAGGED_FP6_BLOCK_M),
+    whose operands are converted into a workspace and whose tasks need
+    align_tile a multiple of 32.  The task list, its count and the
+    workspace share one allocation."""
     torch = _torch()
     lib = _verified_library(library_path)
-    fp6 = block_m == kt.RAGGED_FP6_BLOCK_M
+    if fp6 and block_m != kt.RAGGED_FP6_BLOCK_M:
+        raise ValueError(f"the fp6 ragged forward takes tasks of {kt.RAGGED_FP6_BLOCK_M} rows; got block_m={block_m}")
     desc = kt.find_ragged(kt.FAMILY_RAGGED_FWD, layout=kt.LAYOUT_CODES[layout.value], subchannel=subchannel,
                           block_m=block_m, fp6=fp6)
     if fp6 and align_tile % 32:

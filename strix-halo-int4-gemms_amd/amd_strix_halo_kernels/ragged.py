@@ -13,7 +13,7 @@ ragged.py (ragged.py:11-72, 201-366, 834-1402).  What differs is underneath:
 * per-channel calls with N a multiple of 8 (and a 16-byte aligned output,
   an 8-byte aligned b_scale) run the fp6 kernels, which convert both int4
   operands into a workspace and use the fp6 MFMA at twice the int8 rate; the
-  forward's task tile is then 256 rows with align_tile 32;
+  forward's task tile is then 128 rows with align_tile 32;
 * otherwise ``RaggedDotConfig.block_m`` / ``align_tile`` set the task tiling
   when the table has that block_m (16, 32, 64, 128), else 64 is used (block_m
   64, the default, and 256 leave the choice of the fp6 kernel to the
@@ -476,9 +476,10 @@ def ragged_dot_int4(
     a_shape = (rows,) if subchannel is None else (rows, scale_cols)
     b_shape = (groups, cols) if subchannel is None else (groups, scale_cols, cols)
     a_scale, b_scale = _scales_or_ones(torch, a_scale, b_scale, a_shape, b_shape, lhs.device)
-    if (config.block_m in (64, kt.RAGGED_FP6_BLOCK_M)
+    fp6 = (config.block_m in (64, kt.RAGGED_FP6_CONFIG_BLOCK_M)
             and kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_FWD, subchannel=subchannel, m=rows, n=cols, k_packed=k_packed)
-            and _fp6_buffers_ok(out, b_scale)):
+           and _fp6_buffers_ok(out, b_scale))
+    if fp6:
         block_m, align = kt.RAGGED_FP6_BLOCK_M, kt.RAGGED_FP6_ALIGN
     else:
         block_m = config.block_m if config.block_m in kt.RAGGED_FWD_BLOCK_M else 64
@@ -489,7 +490,7 @@ def ragged_dot_int4(
     return launch_ragged_fwd(
         lhs, rhs, gs, a_scale=a_scale, b_scale=b_scale, out=out, layout=layout, subchannel=subchannel,
         block_m=block_m, align_tile=align, rows=rows, cols=cols, k_packed=k_packed,
-        out_mode=kt.OUT_BF16 if output_dtype == torch.bfloat16 else kt.OUT_F32,
+        out_mode=kt.OUT_BF16 if output_dtype == torch.bfloat16 else kt.OUT_F32, fp6=fp6,
         library_path=native_library_path if native_library_path is not None else (
             None if native_root is None else f"{native_root}/libamd_strix_halo_kernels_gfx950.so"),
     )

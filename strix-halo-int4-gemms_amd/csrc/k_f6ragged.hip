@@ -1,14 +1,18 @@
-// Ragged forward and K-ragged backward on the fp6 engine (shk_f6.h).
+// Ragged forward and K-ragged backward on the fp6 MFMA.
 //
 // Both convert their int4 operands into fp6 blocks in a caller workspace
-// first (one f6_pack_two launch for both operands), then run the 256 x 256
-// fp6 tile over the converted blocks.  The conversion absorbs the operand
-// layouts, so one GEMM kernel per output mode serves every layout.
+// first (one f6_pack_two launch for both operands), then run the 128 x 128
+// fp6 tile of shk_f6small.h over the converted blocks, two workgroups per
+// CU: the ragged grids are small (the MoE forward of G=8, M=8192, N=1408
+// makes ~900 of these tiles against ~220 of 256 x 256), so the finer tile
+// fills the CUs and lets one workgroup's prologue and epilogue overlap
+// another's MFMAs.  The conversion absorbs the operand layouts, so one
+// GEMM kernel per output mode serves every layout.
 //
 // Forward (ragged.py:1008-1229 semantics): out[rows of group g] =
-// lhs[rows] @ rhs[g].  Workgroup (task, tn) takes the task's 256 rows from
+// lhs[rows] @ rhs[g].  Workgroup (task, tn) takes the task's 128 rows from
 // block_start (a multiple of 32: the task list is built with align_tile a
-// multiple of 32) against group g's 256-column tile tn, and writes rows
+// multiple of 32) against group g's 128-column tile tn, and writes rows
 // [actual_start, actual_end) and columns below N.  K is zero-padded to Kw,
 // a multiple of 128.  Workspace: A as round32(M) rows x Kw, then per group
 // B as round32(N) rows x Kw.
@@ -18,14 +22,16 @@
 // that length, so group g runs ceil(len / 128) whole 128-K stages.
 // Workspace: per group A (round32(M) rows x Kw), then per group B
 // (round32(N) rows x Kw), Kw = K capacity rounded up to 128.
+#include "shk_f6small.h"
 #include "shk_table.h"
 
 namespace shk {
 namespace {
 
-// 256 A rows x 256 B rows, 2 x 2 waves, plain epilogue.
-using F6R = Cfg<4, true, true, 256, 256, 128, 2, 2, false, false, 64, false, 0>;
-constexpr int kTile = 256;
+// 128 A rows x 128 B rows, 2 x 2 waves, plain epilogue.
+using F6R = Cfg<4, true, true, 128, 128, 128, 2, 2, false, false, 64, false, 0>;
+using F6RE = F6SmallEngine<F6R>;
+constexpr int kTile = 128;
 
 __host__ __device__ inline int round32(int x) { return (x + 31) & ~31; }
 __host__ __device__ inline int round128(int x) { return (x + 127) & ~127; }
@@ -40,8 +46,8 @@ __device__ __forceinline__ int xcd_contiguous(int w, int total) {
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
-  using E = F6Engine<F6R>;
+__global__ __launch_bounds__(256, 2) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
+  using E = F6RE;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_n = (p.N + kTile - 1) / kTile;
   const int ntasks = *p.num_tasks;
@@ -59,22 +65,23 @@ __global__ __launch_bounds__(256) void f6_ragged_fwd_kernel(const RaggedFwdArgs 
   const unsigned long long a_bytes = f6_operand_bytes(round32(p.M), kw);
   const unsigned long long b_bytes = f6_operand_bytes(round32(p.N), kw);
   E e;
-  e.setup(smem, p.work, p.work + a_bytes + (unsigned long long)g * b_bytes, m0, tn, kw / 64, a_bytes, b_bytes);
-  float sa[4];
+  e.setup(smem, p.work, p.work + a_bytes + (unsigned long long)g * b_bytes, m0, tn * kTile, kw / 64, a_bytes,
+          b_bytes);
+  float sa[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
     const int m = m0 + e.out_row(i);
     sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + (m < p.M ? m : p.M - 1));
   }
   const OutView o{p.out, p.b_scale + (long)g * p.N, p.N, p.M, p.N, t.z, t.w, p.N};
   mfma32_prefetch_b_scales<F6R, MODE, true>(e, o, tn * kTile, e.lds0 + E::LDS_BYTES + 256u * e.wave);
   e.run(kw / 128);
-  mfma32_finish<F6R, MODE, EPI_NONE, true>(e, o, smem, m0, tn * kTile, sa);
+  f6s_finish<MODE, true>(e, o, smem, m0, tn * kTile, sa);
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
-  using E = F6Engine<F6R>;
+__global__ __launch_bounds__(256, 2) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
+  using E = F6RE;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = (p.M + kTile - 1) / kTile;
   const int tiles_n = (p.N + kTile - 1) / kTile;
@@ -111,19 +118,20 @@ __global__ __launch_bounds__(256) void f6_ragged_bwd_kernel(const RaggedBwdArgs 
   const uint8_t* a6 = p.work + (unsigned long long)g * a_bytes;
   const uint8_t* b6 = p.work + (unsigned long long)p.groups * a_bytes + (unsigned long long)g * b_bytes;
   E e;
-  e.setup(smem, a6, b6, m0, tn, kw / 64, a_bytes, b_bytes);
+  e.setup(smem, a6, b6, m0, tn * kTile, kw / 64, a_bytes, b_bytes);
   const uint16_t* sa_g = p.a_scale + (long)g * p.M;
-  float sa[4];
+  float sa[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
     const int m = m0 + e.out_row(i);
     sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(sa_g + (m < p.M ? m : p.M - 1));
   }
   const OutView o{static_cast<float*>(p.out) + (long)g * p.M * p.N, p.b_scale + (long)g * p.N, p.N, p.M, p.N, 0,
                   p.M, p.N};
   mfma32_prefetch_b_scales<F6R, MODE, true>(e, o, tn * kTile, e.lds0 + E::LDS_BYTES + 256u * e.wave);
+  // whole 128-K stages: the conversion writes no block past the last one
   e.run((len + 127) / 128);
-  mfma32_finish<F6R, MODE, EPI_NONE, true>(e, o, smem, m0, tn * kTile, sa);
+  f6s_finish<MODE, true>(e, o, smem, m0, tn * kTile, sa);
 }
 
 bool lhs_mn_major(int layout) { return layout == SHK_LAYOUT_TN || layout == SHK_LAYOUT_TT; }
@@ -178,8 +186,8 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
 
 shk_kernel_desc f6_ragged_desc(int family, int layout) {
   shk_kernel_desc d = desc_of<F6R>(family, layout, 1);
-  d.num_stages = F6Engine<F6R>::P;
-  d.lds_bytes = F6Engine<F6R>::LDS_BYTES + MFMA32_SCALE_BYTES;
+  d.num_stages = F6RE::P;
+  d.lds_bytes = F6RE::LDS_BYTES + MFMA32_SCALE_BYTES;
   d.operand_format = SHK_OPERANDS_FP6;
   return d;
 }

@@ -47,6 +47,7 @@ typedef int v6i __attribute__((ext_vector_type(6)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 f6_h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f6_h32 __attribute__((ext_vector_type(32)));
+typedef __bf16 f6_bf8 __attribute__((ext_vector_type(8)));
 
 constexpr int F6_BLOCK = 1536;     // bytes of a 32-row x 64-K fp6 block
 constexpr int F6_MAX_K = 262144;   // 64 * K <= 2^24: fp32 partial sums stay exact

@@ -160,14 +160,14 @@ def test_ragged_fwd_even_k_and_larger(scale, device):
 
 
 # fp6 forward (k_f6ragged.hip): every layout and output mode, through the
-# native entry (block_m 256), on shapes that exercise the row and column
+# native entry (128-row tasks), on shapes that exercise the row and column
 # masks, K padded to 128 and the byte-wise operand loads (K/2 or M not a
 # multiple of 16)
 FP6_FWD_SHAPES = [(17, 64, 24, [5, 0, 12]), (300, 200, 40, [100, 0, 37, 163]),
                   (640, 384, 264, [1, 300, 0, 339]), (96, 256, 8, [96])]
 
 
-def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode):
+def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode, fp6=False):
     from amd_strix_halo_kernels import kernel_table as kt
     from amd_strix_halo_kernels import native
     lhs, rhs = _pack_fwd(a_q, b_q, layout)
@@ -177,8 +177,8 @@ def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode):
     native.launch_ragged_fwd(
         to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
         a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), out=out, layout=layout, subchannel=None,
-        block_m=block_m, align_tile=32 if block_m == 256 else 8, rows=m, cols=n, k_packed=a_q.shape[1] // 2,
-        out_mode=out_mode)
+        block_m=block_m, align_tile=32 if fp6 else 8, rows=m, cols=n, k_packed=a_q.shape[1] // 2,
+        out_mode=out_mode, fp6=fp6)
     torch.cuda.synchronize()
     return out
 
@@ -200,11 +200,11 @@ def test_ragged_fwd_fp6_all_layouts_and_modes(layout, shape, device):
     a_q, b_q, sa, sb = _fwd_case(stable_seed("fp6fwd", layout.value, m), m, k, n, sizes, SCALES[0])
     print(f"case fp6 fwd {layout.value} {shape}", flush=True)
     want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb)
-    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, 256, kt.OUT_F32)
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, kt.RAGGED_FP6_BLOCK_M, kt.OUT_F32, fp6=True)
     assert np.array_equal(got.cpu().numpy(), want)
-    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, 256, kt.OUT_BF16)
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, kt.RAGGED_FP6_BLOCK_M, kt.OUT_BF16, fp6=True)
     assert np.array_equal(bf16_bits(torch, got), ref.bf16_round(want))
-    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, 256, kt.OUT_I32)
+    got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, kt.RAGGED_FP6_BLOCK_M, kt.OUT_I32, fp6=True)
     assert np.array_equal(got.cpu().numpy().astype(np.int64), _ragged_int_reference(a_q, b_q, sizes))
 
 
