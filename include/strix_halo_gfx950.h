@@ -285,13 +285,13 @@ int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index,
  * the fp6 block format in a caller workspace of
  * amd_strix_halo_kernels_ragged_workspace_bytes bytes (0 for PACKED
  * entries; sizes as passed to the launch), 16-byte aligned, then run the
- * 256 x 256 fp6 GEMM.  They are per-channel, need 16-byte aligned lhs and
- * rhs, M and N multiples of 16, out 16-byte and b_scale 8-byte aligned.
- * Forward: K a multiple of 128, task list built with tile 256 and an
- * align_tile that is a multiple of 32.  Backward: K capacity a multiple of
- * 32; split_k has no effect (each output is computed whole and written, the
- * result of split_k = 1).  Otherwise the _ws calls equal the calls above,
- * which they replace for every entry. */
+ * 128 x 128 fp6 GEMM.  They are per-channel and take N a multiple of 8,
+ * K <= 262144, out 16-byte and b_scale 8-byte aligned (lhs and rhs in any
+ * alignment).  Forward: task list built with tile 128 (the entry's block_m)
+ * and an align_tile that is a multiple of 32.  Backward: split_k has no
+ * effect (each output is computed whole and written, the result of
+ * split_k = 1).  Otherwise the _ws calls equal the calls above, which they
+ * replace for every entry. */
 int amd_strix_halo_kernels_ragged_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k_packed,
                                                   int32_t groups, uint64_t* bytes);
 int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_index, uintptr_t stream,
@@ -301,6 +301,22 @@ int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_ind
                                                 void* out, int32_t m, int32_t n, int32_t k_packed,
                                                 int32_t groups, int32_t subchannel, int32_t out_mode,
                                                 void* workspace, uint64_t workspace_bytes);
+
+/* The task list and the forward in one call: the same as
+ * amd_strix_halo_kernels_ragged_group_info(group_sizes, groups, tile = the
+ * entry's block_m, align_tile, capacity, tasks_i32, num_tasks_i32, NULL)
+ * followed by amd_strix_halo_kernels_launch_ragged_fwd_ws with that list.
+ * No counterpart in the reference, whose forward takes the list from
+ * calculate_group_info (ragged.py:201-323) as a separate step: the fp6
+ * entries build it inside their conversion launch (up to 1024 groups), so
+ * a call is two launches with no host work between them. */
+int amd_strix_halo_kernels_launch_ragged_fwd_grouped(int kernel_index, int device_index, uintptr_t stream,
+                                                     const void* lhs, const void* rhs, const void* a_scale,
+                                                     const void* b_scale, const int32_t* group_sizes,
+                                                     int32_t align_tile, int32_t* tasks_i32, int32_t* num_tasks_i32,
+                                                     int32_t capacity, void* out, int32_t m, int32_t n,
+                                                     int32_t k_packed, int32_t groups, int32_t subchannel,
+                                                     int32_t out_mode, void* workspace, uint64_t workspace_bytes);
 
 /* ---- ragged backward --------------------------------------------------------
  * Replaces amd_strix_halo_kernels_launch_ragged_bwd_hsaco (dispatch.cpp:391-457)

@@ -286,6 +286,16 @@ def entries(family: int) -> tuple[KernelDesc, ...]:
 
 
 @functools.lru_cache(maxsize=None)
+def ragged_task_capacity(rows: int, groups: int, tile: int) -> int:
+    """Upper bound on the row tasks of `rows` rows in `groups` groups with
+    tasks of `tile` rows (amd_strix_halo_kernels_ragged_task_capacity): every
+    group adds at most one partial task at each end."""
+    if rows < 0 or groups < 0 or tile <= 0:
+        return 0
+    return min(rows // tile + 2 * groups + 1, 0x7FFFFFFF)
+
+
+@functools.lru_cache(maxsize=None)
 def find_ragged(family: int, *, layout: int, subchannel: int | None, block_m: int | None = None,
                 fp6: bool = False) -> KernelDesc:
     """Ragged kernel for a layout and scale mode (and task rows for the

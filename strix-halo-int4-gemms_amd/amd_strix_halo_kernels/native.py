@@ -106,6 +106,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_launch_ragged_fwd_ws.argtypes = [I, I, U, P, P, P, P, P, P, I32, P, I32, I32, I32,
                                                                 I32, I32, I32, P, ctypes.c_uint64]
     lib.amd_strix_halo_kernels_launch_ragged_fwd_ws.restype = I
+    lib.amd_strix_halo_kernels_launch_ragged_fwd_grouped.argtypes = [I, I, U, P, P, P, P, P, I32, P, P, I32, P, I32,
+                                                                     I32, I32, I32, I32, I32, P, ctypes.c_uint64]
+    lib.amd_strix_halo_kernels_launch_ragged_fwd_grouped.restype = I
     lib.amd_strix_halo_kernels_launch_ragged_bwd_ws.argtypes = [I, I, U, P, P, P, P, P, P, I32, I32, I32, I32, I32,
                                                                 I32, I32, P, ctypes.c_uint64]
     lib.amd_strix_halo_kernels_launch_ragged_bwd_ws.restype = I
@@ -587,7 +590,8 @@ def launch_ragged_fwd(
     library_path: str | Path | None = None,
     stream: Any | None = None,
 ) -> Any:
-    """Device task list + grouped forward (replaces launch_ragged_fwd_kernel,
+    """Device task list + grouped forward in one library call (replaces
+    calculate_group_info + launch_ragged_fwd_kernel, ragged.py:201-323 and
     native.py:533-600).  No host synchronisation.  fp6: run the fp6 entry
     (per-channel; block_m must be its task tile, kt.RAGGED_FP6_BLOCK_M),
     whose operands are converted into a workspace and whose tasks need
@@ -602,24 +606,23 @@ def launch_ragged_fwd(
     if fp6 and align_tile % 32:
         raise ValueError(f"the fp6 ragged forward needs align_tile a multiple of 32; got {align_tile}")
     groups = int(group_sizes_i32.shape[0])
-    capacity = int(lib.amd_strix_halo_kernels_ragged_task_capacity(rows, groups, block_m, align_tile))
+    capacity = kt.ragged_task_capacity(rows, groups, block_m)
     # tasks [capacity, 4] int32, then num_tasks (16 bytes), then the workspace
     head = 16 * max(capacity, 1) + 16
     buf, nbytes = _ragged_workspace(torch, desc, lhs, rows, cols, k_packed, groups, stream, head)
     base = buf.data_ptr()
-    device = _device_index(lhs)
-    handle = _stream_handle(torch, lhs, stream)
-    _check(lib, lib.amd_strix_halo_kernels_ragged_group_info(
-        device, handle, group_sizes_i32.data_ptr(), groups, block_m, align_tile, capacity, base,
-        base + head - 16, None))
-    rc = lib.amd_strix_halo_kernels_launch_ragged_fwd_ws(
+    # the task list and the forward in one library call (one launch fewer for
+    # the fp6 entries, whose conversion launch builds the list)
+    rc = lib.amd_strix_halo_kernels_launch_ragged_fwd_grouped(
         desc.index,
-        device,
-        handle,
+        _device_index(lhs),
+        _stream_handle(torch, lhs, stream),
         lhs.data_ptr(),
         rhs.data_ptr(),
         a_scale.data_ptr(),
         b_scale.data_ptr(),
+        group_sizes_i32.data_ptr(),
+        align_tile,
         base,
         base + head - 16,
         capacity,

@@ -593,13 +593,16 @@ int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index,
                                                      k_packed, groups, subchannel, out_mode, nullptr, 0);
 }
 
-int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_index, uintptr_t stream,
-                                                const void* lhs, const void* rhs, const void* a_scale,
-                                                const void* b_scale, const int32_t* tasks_i32,
-                                                const int32_t* num_tasks_i32, int32_t capacity, void* out,
-                                                int32_t m, int32_t n, int32_t k_packed, int32_t groups,
-                                                int32_t subchannel, int32_t out_mode, void* workspace,
-                                                uint64_t workspace_bytes) {
+namespace {
+
+// The ragged forward; job: a task list for it to build first (in the fp6
+// conversion launch where that holds the groups, else in its own launch),
+// already validated.
+int ragged_fwd(int kernel_index, int device_index, uintptr_t stream, const void* lhs, const void* rhs,
+               const void* a_scale, const void* b_scale, const int32_t* tasks_i32, const int32_t* num_tasks_i32,
+               int32_t capacity, void* out, int32_t m, int32_t n, int32_t k_packed, int32_t groups,
+               int32_t subchannel, int32_t out_mode, void* workspace, uint64_t workspace_bytes,
+               const shk::TaskJob* job) {
   g_last_error.clear();
   const Entry* e = nullptr;
   if (lookup(kernel_index, SHK_FAMILY_RAGGED_FWD, &e)) return 1;
@@ -616,7 +619,17 @@ int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_ind
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
   if (!aligned(tasks_i32, 16)) return fail("tasks buffer must be 16-byte aligned");
   if (fp6 && check_f6_ragged(d, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
-  if (m == 0 || n == 0 || capacity == 0) return 0;
+  if (m == 0 || n == 0 || capacity == 0) {
+    // nothing to multiply; a requested task list is still built
+    if (job == nullptr) return 0;
+    DeviceGuard guard(device_index);
+    if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
+    const hipError_t err = shk::launch_group_info(job->sizes, job->groups, job->tile, job->align, job->capacity,
+                                                  job->tasks, job->num_tasks, nullptr,
+                                                  reinterpret_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail_hip("group info launch", err);
+    return 0;
+  }
   shk::RaggedFwdArgs p{};
   p.lhs = static_cast<const uint8_t*>(lhs);
   p.rhs = static_cast<const uint8_t*>(rhs);
@@ -647,9 +660,58 @@ int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_ind
   if (grid > 0x7FFFFFFFL) return fail("ragged forward grid is too large");
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
-  const hipError_t err = e->fwd(p, dim3((unsigned)grid), reinterpret_cast<hipStream_t>(stream));
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (job != nullptr) {
+    if (fp6 && groups <= shk::kFusedTaskGroups) {
+      p.job = *job;
+    } else {
+      const hipError_t err = shk::launch_group_info(job->sizes, job->groups, job->tile, job->align, job->capacity,
+                                                    job->tasks, job->num_tasks, nullptr, s);
+      if (err != hipSuccess) return fail_hip("group info launch", err);
+    }
+  }
+  const hipError_t err = e->fwd(p, dim3((unsigned)grid), s);
   if (err != hipSuccess) return fail_hip("ragged forward launch", err);
   return 0;
+}
+
+}  // namespace
+
+int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_index, uintptr_t stream,
+                                                const void* lhs, const void* rhs, const void* a_scale,
+                                                const void* b_scale, const int32_t* tasks_i32,
+                                                const int32_t* num_tasks_i32, int32_t capacity, void* out,
+                                                int32_t m, int32_t n, int32_t k_packed, int32_t groups,
+                                                int32_t subchannel, int32_t out_mode, void* workspace,
+                                                uint64_t workspace_bytes) {
+  return ragged_fwd(kernel_index, device_index, stream, lhs, rhs, a_scale, b_scale, tasks_i32, num_tasks_i32,
+                    capacity, out, m, n, k_packed, groups, subchannel, out_mode, workspace, workspace_bytes, nullptr);
+}
+
+int amd_strix_halo_kernels_launch_ragged_fwd_grouped(int kernel_index, int device_index, uintptr_t stream,
+                                                     const void* lhs, const void* rhs, const void* a_scale,
+                                                     const void* b_scale, const int32_t* group_sizes,
+                                                     int32_t align_tile, int32_t* tasks_i32, int32_t* num_tasks_i32,
+                                                     int32_t capacity, void* out, int32_t m, int32_t n,
+                                                     int32_t k_packed, int32_t groups, int32_t subchannel,
+                                                     int32_t out_mode, void* workspace, uint64_t workspace_bytes) {
+  g_last_error.clear();
+  const Entry* e = nullptr;
+  if (lookup(kernel_index, SHK_FAMILY_RAGGED_FWD, &e)) return 1;
+  const int tile = e->d.block_m;
+  if (groups < 0) return fail("groups must be non-negative");
+  if (groups > shk::max_info_groups())
+    return fail("at most " + std::to_string(shk::max_info_groups()) + " groups are supported");
+  if (align_tile <= 0) return fail("align_tile must be positive");
+  if (tile % align_tile != 0) return fail("the entry's task tile must be a multiple of align_tile");
+  if (e->d.operand_format == SHK_OPERANDS_FP6 && align_tile % 32 != 0)
+    return fail("fp6 ragged entries need align_tile a multiple of 32 (tasks start on a 32-row panel)");
+  if (capacity < 0) return fail("capacity must be non-negative");
+  if (num_tasks_i32 == nullptr || tasks_i32 == nullptr) return fail("task list pointers must be non-null");
+  if (groups > 0 && group_sizes == nullptr) return fail("group_sizes pointer must be non-null");
+  const shk::TaskJob job{group_sizes, groups, tile, align_tile, capacity, tasks_i32, num_tasks_i32, nullptr};
+  return ragged_fwd(kernel_index, device_index, stream, lhs, rhs, a_scale, b_scale, tasks_i32, num_tasks_i32,
+                    capacity, out, m, n, k_packed, groups, subchannel, out_mode, workspace, workspace_bytes, &job);
 }
 
 int amd_strix_halo_kernels_launch_ragged_bwd(int kernel_index, int device_index, uintptr_t stream,

@@ -221,11 +221,21 @@ __global__ __launch_bounds__(256) void f6_pack_one(const F6PackArgs p, int mn_ma
 }
 
 // Both operands of a call in one launch: workgroups [0, a_groups) convert
-// A, the rest B.
+// A, the rest B.  With a task job, workgroup 0 (dispatched first) builds the
+// task list in the tile's LDS and the conversion shifts up by one.
 __global__ __launch_bounds__(256) void f6_pack_two(const F6PackArgs a, const F6PackArgs b, int a_mn, int b_mn,
-                                                   int a_groups) {
+                                                   int a_groups, const TaskJob job) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kKW * F6_KTILE];
-  const int wg = blockIdx.x;
+  static_assert(sizeof(int) * (2 * (kFusedTaskGroups + 1) + 4) <= sizeof(tile), "task arrays fit the tile");
+  int wg = blockIdx.x;
+  if (job.sizes != nullptr) {
+    if (wg == 0) {
+      int* starts = reinterpret_cast<int*>(tile);
+      build_task_list<256>(job, starts, starts + kFusedTaskGroups + 1, starts + 2 * (kFusedTaskGroups + 1));
+      return;
+    }
+    --wg;
+  }
   if (wg < a_groups) {
     if (a_mn) pack_mnmajor(a, wg, tile);
     else pack_kmajor(a, wg);
@@ -245,11 +255,17 @@ hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s) {
+hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s,
+                           const TaskJob* job) {
   const long ga = pack_groups(a, a_mn), gb = pack_groups(b, b_mn);
-  if (ga + gb <= 0) return hipSuccess;
-  if (ga + gb > 0x7FFFFFFFL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(f6_pack_two, dim3((unsigned)(ga + gb)), dim3(256), 0, s, a, b, (int)a_mn, (int)b_mn, (int)ga);
+  const bool with_job = job != nullptr && job->sizes != nullptr;
+  if (with_job && (job->groups > kFusedTaskGroups || job->groups < 0)) return hipErrorInvalidValue;
+  const long total = ga + gb + (with_job ? 1 : 0);
+  if (total <= 0) return hipSuccess;
+  if (total > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  const TaskJob none{nullptr, 0, 1, 1, 0, nullptr, nullptr, nullptr};
+  hipLaunchKernelGGL(f6_pack_two, dim3((unsigned)total), dim3(256), 0, s, a, b, (int)a_mn, (int)b_mn, (int)ga,
+                     with_job ? *job : none);
   return hipGetLastError();
 }
 

@@ -151,7 +151,8 @@ hipError_t launch_f6_ragged_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s
   const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda)};
   const F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
                       f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb)};
-  hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
+  hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s,
+                                   a.job.sizes != nullptr ? &a.job : nullptr);
   if (err != hipSuccess) return err;
   if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_fwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);
   else if (a.out_mode == OUT_F32) hipLaunchKernelGGL(f6_ragged_fwd_kernel<OUT_F32>, grid, dim3(256), 0, s, a);

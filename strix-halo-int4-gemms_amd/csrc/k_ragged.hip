@@ -48,104 +48,17 @@ void SHK_APPEND_NAME(SHK_LAYOUT)(std::vector<Entry>& t) { append_all(t); }
 #if SHK_LAYOUT == 0
 
 // ---------------------------------------------------------------------------
-// Task list (calculate_group_info, ragged.py:201-323).  One workgroup: a
-// blocked exclusive scan over the groups gives each group's first row and
-// first task; every task slot then binary-searches its group.
+// Task list (calculate_group_info, ragged.py:201-323): one workgroup of
+// kInfoThreads threads runs build_task_list (shk_tasks.h).
 
 constexpr int kInfoThreads = 1024;
 constexpr int kMaxInfoGroups = 16384;
 
-__device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int& total) {
-  // Inclusive scan of one value per thread (kInfoThreads threads).
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) scratch[wave] = x;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < kInfoThreads / 64 ? scratch[lane] : 0;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(w, off, 64);
-      if (lane >= off) w += y;
-    }
-    if (lane < kInfoThreads / 64) scratch[lane] = w;
-  }
-  __syncthreads();
-  const int prefix = wave > 0 ? scratch[wave - 1] : 0;
-  total = scratch[kInfoThreads / 64 - 1];
-  __syncthreads();
-  return prefix + x - v;
-}
-
-__global__ __launch_bounds__(kInfoThreads) void group_info_kernel(const int32_t* sizes, int groups, int tile,
-                                                                  int align, int capacity, int32_t* tasks,
-                                                                  int32_t* num_tasks, int64_t* info) {
+__global__ __launch_bounds__(kInfoThreads) void group_info_kernel(const TaskJob job) {
   __shared__ int starts[kMaxInfoGroups + 1];       // first row of each group
   __shared__ int task_starts[kMaxInfoGroups + 1];  // first task of each group
   __shared__ int scratch[kInfoThreads / 64];
-  const int tid = threadIdx.x;
-  int row_carry = 0, task_carry = 0;
-  for (int base = 0; base < groups; base += kInfoThreads) {
-    const int g = base + tid;
-    int sz = g < groups ? sizes[g] : 0;
-    sz = sz < 0 ? 0 : sz;
-    int row_total;
-    const int row_ex = block_exclusive_scan(sz, scratch, row_total);
-    const int start = row_carry + row_ex;
-    const int aligned = (start / align) * align;
-    const int blocks = sz == 0 ? 0 : (start + sz - aligned + tile - 1) / tile;
-    int task_total;
-    const int task_ex = block_exclusive_scan(blocks, scratch, task_total);
-    if (g < groups) {
-      starts[g] = start;
-      task_starts[g] = task_carry + task_ex;
-    }
-    row_carry += row_total;
-    task_carry += task_total;
-  }
-  if (tid == 0) {
-    starts[groups] = row_carry;
-    task_starts[groups] = task_carry;
-    *num_tasks = task_carry;
-  }
-  __syncthreads();
-  const int ntasks = task_carry;
-  for (int t = tid; t < capacity; t += kInfoThreads) {
-    int gid = 0, bstart = 0, astart = 0, aend = 0;
-    if (t < ntasks) {
-      // Largest g with task_starts[g] <= t and a non-empty group:
-      // upper_bound over task_starts[1..groups].
-      int lo = 0, hi = groups;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (task_starts[mid + 1] <= t) lo = mid + 1; else hi = mid;
-      }
-      gid = lo < groups ? lo : groups - 1;
-      const int gstart = starts[gid];
-      const int gend = starts[gid + 1];
-      const int aligned = (gstart / align) * align;
-      bstart = aligned + (t - task_starts[gid]) * tile;
-      astart = bstart > gstart ? bstart : gstart;
-      aend = (bstart + tile) < gend ? (bstart + tile) : gend;
-    }
-    *reinterpret_cast<int4*>(tasks + 4 * t) = make_int4(gid, bstart, astart, aend);
-    if (info != nullptr) {
-      const int size = aend > astart ? aend - astart : 0;
-      info[t] = gid;
-      info[(long)capacity + t] = bstart;
-      info[2L * capacity + t] = astart;
-      info[3L * capacity + t] = aend;
-      info[4L * capacity + t] = astart - bstart;
-      info[5L * capacity + t] = size;
-    }
-  }
+  build_task_list<kInfoThreads>(job, starts, task_starts, scratch);
 }
 
 // out[g, m, n] (int32 bits of the exact split-K sum) -> (float(sum) * a_scale[g, m]) * b_scale[g, n].
@@ -171,8 +84,8 @@ namespace shk {
 
 hipError_t launch_group_info(const int32_t* sizes, int groups, int tile, int align, int capacity,
                              int32_t* tasks, int32_t* num_tasks, int64_t* info, hipStream_t s) {
-  hipLaunchKernelGGL(group_info_kernel, dim3(1), dim3(kInfoThreads), 0, s, sizes, groups, tile, align,
-                     capacity, tasks, num_tasks, info);
+  const TaskJob job{sizes, groups, tile, align, capacity, tasks, num_tasks, info};
+  hipLaunchKernelGGL(group_info_kernel, dim3(1), dim3(kInfoThreads), 0, s, job);
   return hipGetLastError();
 }
 

@@ -529,6 +529,25 @@ struct DmaEngine {
     }
   }
 
+  // The refill reads are asm statements, so the compiler does not know that
+  // their registers are written later than the statement.  The last step's
+  // refills are never widened: without this wait, with each packed register
+  // an operand, their registers could be reused while the reads are in
+  // flight.
+  template <class T>
+  static __device__ __forceinline__ void hold_until_landed(T& x) {
+    typedef int nv __attribute__((ext_vector_type(sizeof(T) / 4)));
+    nv v = __builtin_bit_cast(nv, x);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v)::"memory");
+    x = __builtin_bit_cast(T, v);
+  }
+  __device__ __forceinline__ void drain_refills() {
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) hold_until_landed(pa[i]);
+#pragma unroll
+    for (int j = 0; j < C::FN2; ++j) hold_until_landed(pb[j]);
+  }
+
   // Stage and ring slot of the loads issued during the current stage.
   int dma_st, dma_slot;
 
@@ -749,6 +768,7 @@ struct DmaEngine {
         step<0, 0, OnStep, false>(smem, 2 * k, on_step);
         step<1, 1, OnStep, false>(smem, 2 * k + 1, on_step);
       }
+      drain_refills();
       acc_fence<7>(acc);
     } else {
 #pragma unroll

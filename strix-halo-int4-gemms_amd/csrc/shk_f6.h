@@ -40,6 +40,7 @@
 #include <utility>
 
 #include "shk_dense.h"
+#include "shk_tasks.h"
 
 namespace shk {
 
@@ -96,8 +97,11 @@ __host__ __device__ constexpr int f6_panels(int rows) { return (rows + 31) / 32;
 // Converts one operand into block format (k_f6pack.hip).  mn_major: the
 // source is stored K-row by K-row (two K values per byte of every row).
 hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s);
-// Both operands in one launch.
-hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s);
+// Both operands in one launch; with a job (sizes non-null, at most
+// kFusedTaskGroups groups) an extra first workgroup builds a ragged task
+// list beside the conversion.
+hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s,
+                           const TaskJob* job = nullptr);
 
 // ---------------------------------------------------------------------------
 // GEMM engine.  Four waves in 2 x 2, each owning 128 rows x 128 packed B
@@ -295,6 +299,17 @@ struct F6Engine {
 #undef SHK_F6_ACC
   }
 
+  // This wave's LDS reads into set S (step ST) have landed.  The reads are
+  // asm statements, so the compiler does not know that their registers are
+  // written later than the statement: every register of the set is an
+  // operand here, so none is copied before the data is in.
+  template <int S, int ST>
+  __device__ __forceinline__ void frag_fence() {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[S][ST][0]), "+v"(fa[S][ST][1]), "+v"(fa[S][ST][2]), "+v"(fa[S][ST][3]),
+                   "+v"(fb[S][ST][0]), "+v"(fb[S][ST][1]), "+v"(fb[S][ST][2]), "+v"(fb[S][ST][3])::"memory");
+  }
+
   // Stage k on set S.  Top: this wave's DMA of stage k+1 has landed (that
   // of k+2 may be outstanding), its LDS reads are done, then the barrier.
   // Then the MFMAs of stage k, the reads of stage k+1 (slot `r`) and the DMA
@@ -305,7 +320,9 @@ struct F6Engine {
   template <int S>
   __device__ __forceinline__ void stage(const Reads& r, int k, int nst, int slot, const v4i& rs_end) {
     wait_vmcnt<DPW>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    frag_fence<S, 0>();
+    frag_fence<S, 1>();
+    asm volatile("s_barrier" ::: "memory");
     const bool live = k + 3 < nst;
     const v4i rs_st = live ? rs : rs_end;
     const uint32_t so = live ? (uint32_t)(k + 3) * PANEL : 0u;
@@ -318,8 +335,12 @@ struct F6Engine {
     slot = slot == 2 ? 0 : slot + 1;
   }
 
-  // nst: 128-K stages.
+  // nst: 128-K stages (at least one; none leaves the sums at zero).
   __device__ __forceinline__ void run(int nst) {
+    if (nst <= 0) {
+      wait_vmcnt<0>();  // loads issued before the call (the B scales)
+      return;
+    }
     const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
     // stages 0..2 (zeros past the last stage), then stage 0 into set 0
 #pragma unroll
@@ -342,11 +363,19 @@ struct F6Engine {
       stage<1>(r, k + 1, nst, slot, rs_end);
       advance(r, slot);
     }
-    // Wait states after the last MFMA wherever paths merge, so that a copy
-    // the register allocator places on a merge reads finished accumulators.
+    // The last stage's reads fetch a stale slot into the set that no MFMA
+    // uses.  They land before the paths merge and before the set's
+    // registers could be reused: the fences name every register of the set
+    // (set 0 after the pairs, set 1 after an odd last stage).  Wait states
+    // after the last MFMA likewise, so that a copy the register allocator
+    // places on a merge reads finished accumulators.
+    frag_fence<0, 0>();
+    frag_fence<0, 1>();
     fence<7>();
     if (k < nst) {
       stage<0>(r, k, nst, slot, rs_end);
+      frag_fence<1, 0>();
+      frag_fence<1, 1>();
       fence<7>();
     }
     fence<7>();

@@ -180,8 +180,10 @@ struct F6SmallEngine {
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
                    : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
   }
-  // This wave's LDS reads into set S have landed; every register of the set
-  // is an operand, so no copy of it is placed before this point.
+  // This wave's LDS reads into set S have landed.  The reads are asm
+  // statements, so the compiler does not know that their registers are
+  // written later than the statement: every register of the set is an
+  // operand here, so none is copied before the data is in.
   template <int S>
   __device__ __forceinline__ void frag_fence() {
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -215,6 +217,10 @@ struct F6SmallEngine {
 
   // nst: 128-K stages (0 leaves the sums at zero).
   __device__ __forceinline__ void run(int nst) {
+    if (nst <= 0) {
+      wait_vmcnt<0>();  // loads issued before the call (the B scales)
+      return;
+    }
     const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
     const int s8 = 130;  // E8M0 2^3: both operands hold v/8
     // stages 0..2 (zeros past the last stage), then stage 0 into set 0
@@ -238,17 +244,22 @@ struct F6SmallEngine {
       stage<1>(r, k + 1, nst, slot, rs_end, s8);
       advance(r, slot);
     }
-    // wait states after the last MFMA wherever paths merge, so that a copy
-    // the register allocator places on a merge reads finished accumulators
+    // The last stage's reads fetch a stale slot into the set that no MFMA
+    // uses.  They land before the paths merge and before the set's
+    // registers could be reused: the fences name every register of the set
+    // (set 0 after the pairs, set 1 after an odd last stage).  Wait states
+    // after the last MFMA likewise, so that a copy the register allocator
+    // places on a merge reads finished accumulators.
+    frag_fence<0>();
     fence<7>();
     if (k < nst) {
       stage<0>(r, k, nst, slot, rs_end, s8);
+      frag_fence<1>();
       fence<7>();
     }
     fence<7>();
-    // the reads and loads past the last stage land before the workgroup's
-    // LDS is freed or reused
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // the loads past the last stage land before the workgroup's LDS is
+    // freed or reused
     wait_vmcnt<0>();
   }
 };

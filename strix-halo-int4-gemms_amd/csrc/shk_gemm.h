@@ -24,6 +24,7 @@
 // the x256 domain and multiplies by 2^-8 once, which is exact.
 #pragma once
 
+#include "shk_tasks.h"
 #include "shk_stage.h"
 
 namespace shk {
@@ -410,6 +411,9 @@ struct RaggedFwdArgs {
   int a_aligned, b_aligned, out_vec;
   int layout;     // SHK_LAYOUT_* (fp6 entries convert either layout)
   uint8_t* work;  // fp6 entries: operand workspace
+  // fp6 entries: a task list to build in the conversion launch, before the
+  // GEMM reads it (job.sizes == nullptr: the list is already built)
+  TaskJob job;
 };
 
 template <class C>

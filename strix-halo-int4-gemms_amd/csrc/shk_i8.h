@@ -226,10 +226,22 @@ struct I8Engine {
   // may stay outstanding), then the barrier; MFMAs of stage k, reads of
   // stage k+1, DMA of stage k+4 into slot `slot` (k's), through zero-record
   // resources past the last stage.
+  // This wave's LDS reads into set S (step ST) have landed.  The reads are
+  // asm statements, so the compiler does not know that their registers are
+  // written later than the statement: every register of the set is an
+  // operand here, so none is copied before the data is in.
+  template <int S, int ST>
+  __device__ __forceinline__ void frag_fence() {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[S][ST][0]), "+v"(fa[S][ST][1]), "+v"(fa[S][ST][2]), "+v"(fa[S][ST][3]),
+                   "+v"(fb[S][ST][0]), "+v"(fb[S][ST][1]), "+v"(fb[S][ST][2]), "+v"(fb[S][ST][3])::"memory");
+  }
   template <int S>
   __device__ __forceinline__ void stage(int k, int nst, int slot, const v4i& rsa_end, const v4i& rsb_end) {
     wait_vmcnt<2 * DPW>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    frag_fence<S, 0>();
+    frag_fence<S, 1>();
+    asm volatile("s_barrier" ::: "memory");
     const bool live = k + 4 < nst;
     const v4i rsa_st = live ? rsa : rsa_end;
     const v4i rsb_st = live ? rsb : rsb_end;
@@ -244,8 +256,12 @@ struct I8Engine {
     slot = slot == P - 1 ? 0 : slot + 1;
   }
 
-  // nst: 64-K stages.
+  // nst: 64-K stages (at least one; none leaves the sums at zero).
   __device__ __forceinline__ void run(int nst) {
+    if (nst <= 0) {
+      wait_vmcnt<0>();  // loads issued before the call (the B scales)
+      return;
+    }
     const v4i rsa_end = v4i{rsa.x, rsa.y, 0, rsa.w};
     const v4i rsb_end = v4i{rsb.x, rsb.y, 0, rsb.w};
     // stages 0..3 (zeros past the last stage), then stage 0 into set 0
@@ -276,10 +292,15 @@ struct I8Engine {
       stage<1>(k + 1, nst, slot, rsa_end, rsb_end);
       advance(slot);
     }
-    // wait states after the last MFMA wherever paths merge (see shk_f6.h)
+    // the last stage's reads land before the paths merge and before their
+    // registers could be reused, and the MFMAs finish (see shk_f6.h)
+    frag_fence<0, 0>();
+    frag_fence<0, 1>();
     fence<7>();
     if (k < nst) {
       stage<0>(k, nst, slot, rsa_end, rsb_end);
+      frag_fence<1, 0>();
+      frag_fence<1, 1>();
       fence<7>();
     }
     fence<7>();

@@ -271,7 +271,7 @@ void append_ragged_2(std::vector<Entry>& t);
 void append_ragged_3(std::vector<Entry>& t);
 int max_info_groups();
 // fp6 ragged entries of one layout (k_f6ragged.hip): the forward (task
-// tile 256) and the K-ragged backward, both per-channel.
+// tile 128) and the K-ragged backward, both per-channel.
 Entry f6_ragged_fwd_entry(int layout);
 Entry f6_ragged_bwd_entry(int layout);
 // Workspace bytes of the fp6 ragged paths.

@@ -1,0 +1,72 @@
+"""The hand-scheduled K loops never let the compiler touch a register of an
+LDS read that is still in flight (tests/_asm_check.py).
+
+A late LDS return into a register the compiler had already handed to
+another value corrupted the ragged fp6 forward's B-scale address for 16
+lanes of a wave, in a few tiles per call; the engines now name every
+fragment register in their waits.  This test compiles each translation unit
+that holds such a loop to gfx950 assembly (hipcc -S, as build.py compiles
+it) and scans it.  CPU only; about a minute."""
+
+from __future__ import annotations
+
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+import pytest
+
+from tests._asm_check import inflight_lds_hazards
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT / "strix-halo-int4-gemms_amd"))
+
+UNITS = ("dense_f6", "ragged_f6", "dense_dma_4_0", "dense_dma_4_1", "dense_dma_4_2", "dense_dma_8_0", "dense_dma_8_1",
+         "dense_dma_8_2")
+
+
+@pytest.fixture(scope="module")
+def assembly(tmp_path_factory):
+    import build
+
+    if shutil.which(build.hipcc()) is None and not Path(build.hipcc()).exists():
+        pytest.skip("hipcc is not available")
+    out = tmp_path_factory.mktemp("asm")
+    units = {name: (src, extra) for name, src, extra in build.translation_units() if name in UNITS}
+    assert set(units) == set(UNITS)
+
+    def one(name):
+        src, extra = units[name]
+        dst = out / f"{name}.s"
+        cmd = [build.hipcc(), *build.HIP_FLAGS, *extra, "--offload-device-only", "-S", str(src), "-o", str(dst)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-2000:]
+        return name, dst.read_text()
+
+    with ThreadPoolExecutor(4) as ex:
+        return dict(ex.map(one, UNITS))
+
+
+@pytest.mark.parametrize("unit", UNITS)
+def test_no_register_of_an_inflight_lds_read_is_touched(assembly, unit):
+    found = inflight_lds_hazards(assembly[unit])
+    assert not found, "\n".join(found[:10])
+
+
+def test_the_scan_finds_a_reuse_and_a_copy():
+    asm = "\n".join([
+        "_Zkern:",
+        ";;#ASMSTART", "ds_read_b128 v[10:13], v1 offset:0", ";;#ASMEND",
+        "v_mov_b32_e32 v20, v11",       # copy before the wait: stale
+        "v_lshrrev_b32_e32 v12, 2, v0",  # reuse before the wait: clobbered
+        "s_waitcnt lgkmcnt(0)",
+        "v_mov_b32_e32 v21, v10",       # after the wait: fine
+    ])
+    found = inflight_lds_hazards(asm)
+    assert len(found) == 2 and "v[11]" in found[0] and "v[12]" in found[1]
+    # a counted wait that leaves the read outstanding does not retire it
+    asm2 = "\n".join(["_Zk:", ";;#ASMSTART", "ds_read_b64 v[4:5], v1", ";;#ASMEND", "ds_read_b64 v[6:7], v1",
+                      "s_waitcnt lgkmcnt(2)", "v_mov_b32_e32 v9, v4", "s_waitcnt lgkmcnt(1)", "v_mov_b32_e32 v9, v4"])
+    assert len(inflight_lds_hazards(asm2)) == 1

@@ -153,6 +153,21 @@ def test_ragged_entry_points_validate_before_launch(lib):
     F = lib.amd_strix_halo_kernels_launch_ragged_fwd
     assert F(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 16, 16, 16, 2, 32, 0) == 1
     assert "subchannel = 0" in _err(lib)
+    # the one-call forward checks the task-list arguments against the entry's tile
+    G = lib.amd_strix_halo_kernels_launch_ragged_fwd_grouped
+    fp6 = kt.find_ragged(kt.FAMILY_RAGGED_FWD, layout=kt.LAYOUT_NN, subchannel=None, fp6=True)
+    args = (FAKE, FAKE, FAKE, FAKE, FAKE)
+    assert G(fp6.index, 0, 0, *args, 96, FAKE, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 1 << 20) == 1
+    assert "multiple of align_tile" in _err(lib)
+    assert G(fp6.index, 0, 0, *args, 16, FAKE, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 1 << 20) == 1
+    assert "multiple of 32" in _err(lib)
+    assert G(fp6.index, 0, 0, *args, 32, FAKE, FAKE, 8, FAKE, 16, 16, 64, 1 << 20, 0, 0, FAKE, 1 << 20) == 1
+    assert "groups are supported" in _err(lib)
+    assert G(fp6.index, 0, 0, *args, 32, None, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 1 << 20) == 1
+    assert "task list pointers" in _err(lib)
+    assert G(fp6.index, 0, 0, *args, 32, FAKE, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 16) == 1
+    assert "workspace" in _err(lib)
+    assert G(bwd, 0, 0, *args, 32, FAKE, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 1 << 20) == 1
 
 
 @pytest.mark.parametrize("rows,groups,tile,align", [(8192, 8, 64, 8), (0, 3, 16, 8), (17, 40, 16, 16), (1, 1, 128, 8)])
@@ -160,7 +175,7 @@ def test_task_capacity_bounds_the_task_list(lib, rows, groups, tile, align):
     from oracle import ref
 
     cap = lib.amd_strix_halo_kernels_ragged_task_capacity(rows, groups, tile, align)
-    assert cap == rows // tile + 2 * groups + 1
+    assert cap == rows // tile + 2 * groups + 1 == kt.ragged_task_capacity(rows, groups, tile)
     # worst case: every group starts one row past an aligned boundary
     r = ref.rng(rows + groups)
     for _ in range(20):

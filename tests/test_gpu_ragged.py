@@ -192,6 +192,54 @@ def _ragged_int_reference(a_q, b_q, sizes):
     return out
 
 
+@pytest.mark.parametrize("groups,align", [(5, 32), (37, 64), (1100, 32)])
+@pytest.mark.parametrize("fp6", [True, False], ids=["fp6", "packed"])
+def test_grouped_forward_builds_the_oracle_task_list(groups, align, fp6, device):
+    """amd_strix_halo_kernels_launch_ragged_fwd_grouped: the task list it
+    leaves in the caller's buffer (built inside the fp6 conversion launch for
+    up to 1024 groups, by the stand-alone launch otherwise) is the oracle's
+    calculate_group_info, and the output is the oracle's forward."""
+    import ctypes
+
+    from amd_strix_halo_kernels import kernel_table as kt
+    from amd_strix_halo_kernels import native
+    r = ref.rng(stable_seed("grouped", groups, align, fp6))
+    sizes = r.integers(0, 90, size=groups)
+    sizes[r.integers(0, groups)] = 0
+    m, k, n = int(sizes.sum()) + 3, 128, 64
+    a_q, b_q, sa, sb = _fwd_case(stable_seed("grouped-op", groups), m, k, n, list(sizes), SCALES[0])
+    tile = kt.RAGGED_FP6_BLOCK_M if fp6 else 64
+    desc = kt.find_ragged(kt.FAMILY_RAGGED_FWD, layout=kt.LAYOUT_NN, subchannel=None, block_m=tile, fp6=fp6)
+    lib = native.load_dispatch_library()
+    lhs, rhs = _pack_fwd(a_q, b_q, shk.GemmLayout.NN)
+    lhs_d, rhs_d = to_dev(torch, lhs, device), to_dev(torch, rhs, device)
+    sa_d, sb_d = to_dev(torch, sa, device), to_dev(torch, sb, device)
+    gs = torch.tensor(sizes, dtype=torch.int32, device=device)
+    cap = kt.ragged_task_capacity(m, groups, tile)
+    tasks = torch.full((cap, 4), -5, dtype=torch.int32, device=device)
+    count = torch.full((4,), -5, dtype=torch.int32, device=device)
+    nbytes = desc.ragged_workspace_bytes(m, n, k // 2, groups)
+    work = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+    out = torch.full((m, n), 7, dtype=torch.float32, device=device)
+    print(f"case grouped fwd groups={groups} align={align} fp6={fp6} m={m}", flush=True)
+    rc = lib.amd_strix_halo_kernels_launch_ragged_fwd_grouped(
+        desc.index, 0, torch.cuda.current_stream().cuda_stream, lhs_d.data_ptr(), rhs_d.data_ptr(), sa_d.data_ptr(),
+        sb_d.data_ptr(), gs.data_ptr(), align, tasks.data_ptr(), count.data_ptr(), cap, out.data_ptr(), m, n, k // 2,
+        groups, 0, kt.OUT_F32, work.data_ptr() if nbytes else None, ctypes.c_uint64(nbytes))
+    assert rc == 0, native._library_last_error(lib)
+    torch.cuda.synchronize()
+    want = ref.calculate_group_info(sizes, tile, align_tile=align)
+    got = tasks.cpu().numpy()
+    assert int(count[0]) == want.num_tasks
+    t = want.num_tasks
+    for col, f in enumerate(("group_id", "block_start", "actual_start", "actual_end")):
+        assert np.array_equal(got[:t, col], getattr(want, f)[:t]), f
+    assert not got[t:].any()
+    res = out.cpu().numpy()
+    assert np.array_equal(res[:m - 3], ref.ragged_fwd_reference(a_q, b_q, sizes, sa, sb)[:m - 3])
+    assert (res[m - 3:] == 7).all()  # rows past the groups are not written
+
+
 @pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
 @pytest.mark.parametrize("shape", FP6_FWD_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}x{s[2]}")
 def test_ragged_fwd_fp6_all_layouts_and_modes(layout, shape, device):
