@@ -1,5 +1,6 @@
 """The hand-scheduled K loops never let the compiler touch a register of an
-LDS read that is still in flight (tests/_asm_check.py).
+LDS read that is still in flight, or an asm MFMA's result before it has
+arrived (tests/_asm_check.py).
 
 A late LDS return into a register the compiler had already handed to
 another value corrupted the ragged fp6 forward's B-scale address for 16
@@ -70,3 +71,10 @@ def test_the_scan_finds_a_reuse_and_a_copy():
     asm2 = "\n".join(["_Zk:", ";;#ASMSTART", "ds_read_b64 v[4:5], v1", ";;#ASMEND", "ds_read_b64 v[6:7], v1",
                       "s_waitcnt lgkmcnt(2)", "v_mov_b32_e32 v9, v4", "s_waitcnt lgkmcnt(1)", "v_mov_b32_e32 v9, v4"])
     assert len(inflight_lds_hazards(asm2)) == 1
+    # an asm MFMA's result read 6 wait states later, then after 21
+    asm3 = "\n".join(["_Zm:", ";;#ASMSTART",
+                       "v_mfma_f32_32x32x64_f8f6f4 v[2:17], v[20:25], v[30:35], v[2:17] cbsz:2 blgp:2",
+                       ";;#ASMEND", "s_nop 4", "v_mov_b32_e32 v40, v5", "s_nop 7", "s_nop 7",
+                       "v_mov_b32_e32 v41, v6"])
+    found = inflight_lds_hazards(asm3)
+    assert len(found) == 1 and "after 6 wait states" in found[0]
