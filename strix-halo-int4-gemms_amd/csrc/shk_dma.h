@@ -154,8 +154,13 @@ struct DmaOperand {
 
 // Wait states between the accumulators' last non-asm access and the asm
 // MFMAs (before the loop), and between the last asm MFMA and the first
-// accumulator read (after it).  Every accumulator is an operand, so the
-// compiler cannot move an accumulator access across the statement.
+// accumulator read (after it).  acc_fence<4> (5 wait states) covers the 2
+// a VALU or v_accvgpr_write needs before an MFMA reads the register as its
+// C operand; acc_fence<7> (3 x s_nop 7: 24 wait states) covers the 10 that
+// v_mfma_i32_16x16x64_i8, an 8-pass form, needs before a VALU, memory or
+// v_accvgpr_read instruction touches its result (18 for 16 passes).  Every
+// accumulator is an operand, so the compiler cannot move an accumulator
+// access across the statement.
 template <int N>
 __device__ __forceinline__ void acc_fence(v4i (&a)[8][8]) {
   static_assert(N == 4 || N == 7, "wait states");

@@ -221,8 +221,17 @@ struct F6SubEngine {
     }
   }
 
-  // Wait states between the asm MFMAs' accumulator writes and any other
-  // access; every accumulator is an operand, so no access crosses it.
+  // fence<4> (s_nop 4: 5 wait states) stands between VALU writes of the
+  // accumulators (the fold's clears) and the first asm MFMA that reads
+  // them as its C operand: a VALU write followed by an MFMA reading the
+  // register needs 2 wait states.  fence<7> (5 x s_nop 7: 40 wait states)
+  // stands between the last asm MFMA and any other access to its result: an
+  // XDL MFMA of up to 16 passes needs 18 wait states before a VALU, VMEM,
+  // LDS or v_accvgpr_read instruction reads its destination or a VALU
+  // instruction overwrites it (the 8-pass fp6 forms need 10), so 40 covers
+  // every MFMA here with margin.  Every accumulator is an operand of the
+  // fence, so no compiler access (or register-allocator copy on a merge)
+  // crosses it.
   template <int N>
   __device__ __forceinline__ void fence() {
     static_assert(N == 4 || N == 7, "wait states");
