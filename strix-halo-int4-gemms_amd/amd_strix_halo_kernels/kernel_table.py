@@ -157,7 +157,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
-    # fp6_sub: six stages of 128 + 128 rows x 64 K in fp6 (48 bytes) and a
+    # fp6_sub: three stages of 128 + 128 rows x 128 K in fp6 (96 bytes) and a
     # four-group scale ring of 768 bytes per group (shk_f6sub.h).
     # fp6_small: three stages of 128 A rows + 128 B rows x 128 K in fp6 (96
     # bytes), then the B-scale slots (shk_f6small.h).
@@ -168,8 +168,8 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         lds = pipe * (bm + bn) * 96 + MFMA32_SCALE_BYTES
     elif fp6_sub:
         fp6 = True
-        pipe = 6
-        lds = pipe * (bm + bn) * 48 + 4 * 768
+        pipe = 3
+        lds = pipe * (bm + bn) * 96 + 4 * 768
     elif fp6:
         pipe = 3
         lds = pipe * (bm + 256) * 96 + MFMA32_SCALE_BYTES

@@ -11,8 +11,8 @@
 // see fold()) and lets other waves' MFMAs run meanwhile:
 //  * the MFMA is the scaled form (v_mfma_scale_f32_32x32x64_f8f6f4) with a
 //    scale of 2^3 on both v/8 operands, so the accumulators hold the exact
-//    integer partial sums (no x64 pass), and the first MFMA of a group takes
-//    0 as its C operand (no clearing pass);
+//    integer partial sums (no x64 pass), and the first MFMA of each block in
+//    a group takes 0 as its C operand (no clearing pass);
 //  * a wave owns 64 x 64 outputs (4 accumulators of 32 x 32 and 64 fp32
 //    totals), so a wave stays within 256 registers and two 4-wave
 //    workgroups of 128 x 128 share a CU: while one wave folds, the other
@@ -22,30 +22,459 @@
 //  * the scales reach LDS by LDS-DMA in the same stream as the operands,
 //    so no load the compiler tracks sits in the K loop.
 //
-// Pipeline: 64-K stages (one 32 x 64 fp6 block per 32-row panel; 6 KiB of
-// A and 6 KiB of B) in a ring of six slots.  Stage k: wait for this wave's
-// DMA of stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
-// carrying (the first two) the 8 LDS reads of stage k+1's fragments and
-// the 4 DMA loads of stage k+6 into slot k % 6 (3 operand loads and one
-// scale load per wave);
-// then a fence that waits for this stage's LDS reads with every fragment
-// register of the other set as an operand, so no compiler copy of a
-// fragment can precede its data.
+// Pipeline (that of shk_f6small.h): 128-K stages (two 32 x 64 fp6 blocks
+// per 32-row panel; 12 KiB of A and 12 KiB of B) in a ring of three slots.
+// Stage k: wait for this wave's DMA of stage k+1 and its LDS reads of stage
+// k (with every fragment register of that set as an operand), then the
+// barrier; 8 MFMAs on the fragments of stage k (two 64-K steps of 2 x 2
+// blocks), each followed by two of the 16 LDS reads of stage k+1 into the
+// other register set, the first seven carrying the DMA loads of stage k+3
+// into slot k % 3 (six operand loads and one scale load per wave).  A group
+// is one (S = 128) or two (S = 256) stages; after its last stage the wave
+// waits for the reads of the next stage (naming their registers, so no
+// compiler copy of a fragment precedes its data) and folds.  128-K stages
+// halve the barriers and waits of 64-K ones, and give each stage's reads a
+// whole stage of MFMAs to land.
 //
 // Scales of group g sit in slot g % 4 of a small ring: the a_scale dword
 // holding row r's scale (dword-aligned pair (e & ~1, e | 1) of e = row * G +
 // g) at 4 r, and the 128 b_scale values at 512.  Every stage loads the
 // scales of the group of the stage it loads (duplicates rewrite the same
-// bytes), 5 stages before that group's first stage; the ring slot of
-// group g is next written for group g+4, after g has been folded.
+// bytes), three stages before that stage; the slot it writes last held the
+// scales of a group every wave has folded before the stage's barrier.
 #pragma once
+
+#include <type_traits>
 
 #include "shk_f6.h"
 
 namespace shk {
 
-template <class C, int SPG>
+template <class C>
 struct F6SubEngine {
+  static constexpr int P = 3;                       // ring slots
+  static constexpr int NW = 4;
+  static constexpr int PANEL = 2 * F6_BLOCK;        // 32 rows x 128 K: 3 KiB
+  static constexpr int OPB = 4 * PANEL;             // 128 rows x 128 K: 12 KiB
+  static constexpr int STAGE = 2 * OPB;             // 24 KiB
+  static constexpr int RING = P * STAGE;            // 72 KiB
+  static constexpr int SCALE_SLOT = 768;            // 128 a dwords + 128 b halves
+  static constexpr int LDS_BYTES = RING + 4 * SCALE_SLOT;
+  static constexpr int OPW = STAGE / 1024 / NW;     // 6 operand loads per wave per stage
+  static constexpr int DPW = OPW + 1;               // and one scale load
+  static constexpr int TN = 64;                     // output columns per wave
+  static constexpr int FN = 2;
+  static_assert(C::BM == 128 && C::BROWS == 128 && C::WM == 2 && C::WN == 2 && C::SUBCH && !C::SWIGLU,
+                "128 x 128 tiles of 2 x 2 waves, subchannel, plain epilogue");
+  static constexpr int SPG = 2;                     // stages per group of 256 K
+
+  v16f acc[2][2];
+  float tot[2][2][16];
+  v6i fa[2][2][2];  // [set][step][i]
+  v6i fb[2][2][2];  // [set][step][j]
+  uint32_t voff[OPW];
+  v4i rs;        // operand DMA resource (waves 0-1: A, 2-3: B)
+  v4i rss;       // scale DMA resource (waves 0-1: a_scale, 2-3: b_scale)
+  int sbase;     // waves 0-1: element index row * G of the lane's row; 2-3: byte of its b_scale pair
+  int groups;    // G = K / S
+  int sb_row;    // bytes of one b_scale row (N * 2)
+  uint32_t lds0;
+  int lane, wave, wm, wn, m0;
+  // every group so far took the fast fold: all totals are sums of finite
+  // products below 2^110 in magnitude, so none is NaN
+  bool all_fast;
+
+  __device__ __forceinline__ int out_row(int i) const { return wm * 64 + 32 * i + (lane & 31); }
+  __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
+
+  // a6 / b6: block-format operands; tile rows m0 (A) and n0 (B).
+  __device__ __forceinline__ void setup(uint8_t* smem, const uint8_t* a6, const uint8_t* b6, int m0_, int n0,
+                                        int kb, unsigned long long a_bytes, unsigned long long b_bytes,
+                                        const uint16_t* a_scale, const uint16_t* b_scale, int m_rows, int n_cols,
+                                        int g) {
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    wm = wave % 2;
+    wn = wave / 2;
+    m0 = m0_;
+    groups = g;
+    lds0 = lds_address(smem);
+    const unsigned long long panel_bytes = (unsigned long long)kb * F6_BLOCK;
+    const bool is_a = wave < 2;
+    const unsigned long long first = (unsigned long long)((is_a ? m0 : n0) / 32) * panel_bytes;
+    rs = buffer_words((is_a ? a6 : b6) + first, (is_a ? a_bytes : b_bytes) - first);
+    // DMA load c of this wave fills stage bytes [1024 * (OPW*wave + c), +1024):
+    // panel o / PANEL of the operand, byte o % PANEL of its two blocks
+#pragma unroll
+    for (int c = 0; c < OPW; ++c) {
+      const uint32_t o = 1024u * (OPW * wave + c) + 16u * lane - (is_a ? 0u : (uint32_t)OPB);
+      voff[c] = (o / PANEL) * (uint32_t)panel_bytes + o % PANEL;
+    }
+    sb_row = 2 * n_cols;
+    if (is_a) {
+      rss = buffer_words(a_scale, 2ull * (unsigned long long)m_rows * g);
+      sbase = (m0 + 64 * wave + lane) * g;
+    } else {
+      rss = buffer_words(b_scale, 2ull * (unsigned long long)g * n_cols);
+      sbase = 2 * (n0 + 2 * lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          acc[i][j][r] = 0.0f;
+          tot[i][j][r] = 0.0f;
+        }
+    all_fast = true;
+  }
+
+  // byte offset of this lane's scale dword for group g
+  __device__ __forceinline__ uint32_t scale_voff(int g) const {
+    return wave < 2 ? (uint32_t)(2 * (sbase + g)) & ~3u : (uint32_t)(g * sb_row + sbase);
+  }
+  // LDS destination of this wave's scale load for group g
+  __device__ __forceinline__ uint32_t scale_m0(int g) const {
+    return lds0 + (uint32_t)RING + (uint32_t)(g & 3) * SCALE_SLOT + (wave < 2 ? 256u * wave : 512u);
+  }
+
+  struct Reads {
+    uint32_t a16, a8, b16, b8;
+    __device__ __forceinline__ void add(uint32_t d) {
+      a16 += d;
+      a8 += d;
+      b16 += d;
+      b8 += d;
+    }
+  };
+  // this lane's read addresses in a slot: the wave's A panel 0 and B panel 0
+  // (panel i adds PANEL * i, step 1 adds one block)
+  __device__ __forceinline__ Reads reads_of_slot(int slot) const {
+    const uint32_t s = lds0 + (uint32_t)slot * STAGE;
+    const uint32_t a = s + 2u * wm * PANEL, b = s + OPB + 2u * wn * PANEL;
+    return Reads{a + 16u * lane, a + 1024u + 8u * lane, b + 16u * lane, b + 1024u + 8u * lane};
+  }
+
+  // LDS read Q (0..15) of a stage into set S: per step (Q / 8), fragments
+  // A0, B0, B1, A1 (the order of first use), each as its 16-byte then its
+  // 8-byte part.
+  template <int S, int Q>
+  __device__ __forceinline__ void read(const Reads& r) {
+    constexpr int ST = Q / 8;
+    constexpr int F = (Q % 8) / 2;
+    constexpr bool IS_A = F == 0 || F == 3;
+    constexpr int IDX = F == 0 ? 0 : (F == 3 ? 1 : F - 1);
+    constexpr int OFF = IDX * PANEL + ST * F6_BLOCK;
+    v6i& dst = IS_A ? fa[S][ST][IDX] : fb[S][ST][IDX];
+    if constexpr (Q % 2 == 0) {
+      v4i x;
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x) : "v"(IS_A ? r.a16 : r.b16), "i"(OFF));
+      // a whole new value: the fragment's previous contents are dead here
+      dst = __builtin_shufflevector(x, x, 0, 1, 2, 3, -1, -1);
+    } else {
+      v2i y;
+      asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(y) : "v"(IS_A ? r.a8 : r.b8), "i"(OFF));
+      dst.s4 = y.x;
+      dst.s5 = y.y;
+    }
+  }
+  template <int S, int... Q>
+  __device__ __forceinline__ void reads(const Reads& r, std::integer_sequence<int, Q...>) {
+    (read<S, Q>(r), ...);
+  }
+
+  // MFMA T (0..7) of a stage on set S (step T / 4, A fragment (T % 4) / 2,
+  // B fragment T % 2; the step-0 MFMAs of a group's first stage (ZERO) take
+  // 0 as their C operand), fused for T < OPW with operand DMA load T and for
+  // T = OPW with the scale load of the stage loaded now, then (READ) LDS
+  // reads 2T, 2T+1 of the next stage into the other set.  Every stage runs
+  // the same branch-free sequence (see shk_f6.h).
+  template <int S, int T, bool ZERO, bool READ>
+  __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0_st,
+                                       const v4i& rss_st, uint32_t svo, uint32_t sm0, int s8) {
+    constexpr int ST = T / 4, I = (T % 4) / 2, J = T % 2;
+    constexpr bool Z = ZERO && ST == 0;
+    // the compiler writes M0 before each statement; the MFMA is the wait
+    // state the LDS-DMA load needs after that write
+    if constexpr (T < OPW) {
+      if constexpr (Z)
+        asm volatile(
+            "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+            "buffer_load_dwordx4 %4, %5, %6 offen lds"
+            : "+v"(acc[I][J])
+            : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so),
+              "{m0}"(m0_st + 1024u * T)
+            : "memory");
+      else
+        asm volatile(
+            "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+            "buffer_load_dwordx4 %4, %5, %6 offen lds"
+            : "+v"(acc[I][J])
+            : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so),
+              "{m0}"(m0_st + 1024u * T)
+            : "memory");
+    } else if constexpr (T == OPW) {
+      static_assert(!Z, "the scale load rides on a step-1 MFMA");
+      asm volatile(
+          "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
+          "buffer_load_dword %4, %5, 0 offen lds"
+          : "+v"(acc[I][J])
+          : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(s8), "v"(svo), "s"(rss_st), "{m0}"(sm0)
+          : "memory");
+    } else {
+      asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2"
+                   : "+v"(acc[I][J])
+                   : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(s8));
+    }
+    if constexpr (READ) {
+      read<1 - S, 2 * T>(r);
+      read<1 - S, 2 * T + 1>(r);
+    }
+  }
+  template <int S, bool ZERO, bool READ, int... T>
+  __device__ __forceinline__ void ticks(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0_st,
+                                        const v4i& rss_st, uint32_t svo, uint32_t sm0, int s8,
+                                        std::integer_sequence<int, T...>) {
+    (tick<S, T, ZERO, READ>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8), ...);
+  }
+
+  // fence<4> (s_nop 4: 5 wait states) stands between VALU writes of the
+  // accumulators (the clear before the loop) and the first asm MFMA that
+  // writes them: a VALU write followed by an MFMA reading the register
+  // needs 2 wait states.  fence<7> (5 x s_nop 7: 40 wait states) stands
+  // between the last asm MFMA and any other access to its result: an XDL
+  // MFMA of up to 16 passes needs 18 wait states before a VALU, VMEM, LDS or
+  // v_accvgpr_read instruction reads its destination or a VALU instruction
+  // overwrites it (the 8-pass fp6 forms need 10), so 40 covers every MFMA
+  // here with margin.  Every accumulator is an operand of the fence, so no
+  // compiler access (or register-allocator copy on a merge) crosses it.
+  template <int N>
+  __device__ __forceinline__ void fence() {
+    static_assert(N == 4 || N == 7, "wait states");
+    if constexpr (N == 4)
+      asm volatile("s_nop 4" : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
+    else
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                   : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
+  }
+  // This wave's LDS reads into set S have landed.  The reads are asm
+  // statements, so the compiler does not know that their registers are
+  // written later than the statement: every register of the set is an
+  // operand here, so none is copied before the data is in.
+  template <int S>
+  __device__ __forceinline__ void frag_fence() {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[S][0][0]), "+v"(fa[S][0][1]), "+v"(fb[S][0][0]), "+v"(fb[S][0][1]), "+v"(fa[S][1][0]),
+                   "+v"(fa[S][1][1]), "+v"(fb[S][1][0]), "+v"(fb[S][1][1])::"memory");
+  }
+
+  // Stage k (128 K) on set S (ZERO: the first stage of a group; READ: the
+  // next stage's fragments are read here, else after the group's fold, and
+  // the group's scales are read at the top).
+  // Top: this wave's DMA of stage k+1 has landed (that of k+2 may be
+  // outstanding) and its LDS reads of stage k are done, then the barrier:
+  // stage k+1 and the scales it loaded are complete in LDS, no wave still
+  // reads slot k % 3, and every wave has folded the groups before stage k.
+  // Past the last stage the DMA loads go through zero-record resources into
+  // a slot that holds no live data, and the reads fetch a stale slot into
+  // the set no MFMA uses.
+  template <int S, bool ZERO, bool READ>
+  __device__ __forceinline__ void stage(const uint8_t* smem, const Reads& r, int k, int nst, int slot,
+                                        const v4i& rs_end, const v4i& rss_end, int s8) {
+    wait_vmcnt<DPW>();
+    frag_fence<S>();
+    asm volatile("s_barrier" ::: "memory");
+    if constexpr (!READ) load_scales(smem, k / SPG);
+    const int kl = k + P;  // the stage loaded now
+    const bool live = kl < nst;
+    const v4i rs_st = live ? rs : rs_end;
+    const v4i rss_st = live ? rss : rss_end;
+    const int gl = kl / SPG;
+    const uint32_t so = live ? (uint32_t)kl * PANEL : 0u;
+    const uint32_t svo = live ? scale_voff(gl) : 0u;
+    const uint32_t m0_st = lds0 + (uint32_t)slot * STAGE + 1024u * OPW * wave;
+    ticks<S, ZERO, READ>(r, rs_st, so, m0_st, rss_st, svo, scale_m0(gl), s8,
+                         std::make_integer_sequence<int, 8>{});
+  }
+  static __device__ __forceinline__ void advance(Reads& r, int& slot) {
+    r.add(slot == 1 ? (uint32_t)(-2 * STAGE) : (uint32_t)STAGE);
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+
+  // Folds group g's partial sums into the totals:
+  // tot += (float(part) * a_scale[row, g]) * b_scale[g, col].
+  //
+  // Fast form, two VALU operations per value: tot += part * ab with
+  // ab = a_scale * b_scale from one rank-1 bf16 MFMA per 32 x 32 block.  It
+  // gives the same bits as the reference's order whenever every scale of the
+  // group is zero or a normal number of magnitude in [2^-60, 2^48): part is
+  // an integer of at most 15 significant bits (|part| <= 64 * 256) and a has
+  // 8, so part * a is exact, and a * b (16 bits, within the normal range) is
+  // exact too; both orders therefore round the same real product part*a*b
+  // once.  (A zero product's sign may differ, which changes no sum: the
+  // totals start at +0, and x + -0 = x + +0 for every x.)  A wave whose
+  // scales fall outside that range folds in the reference's order.
+  // The scales of group g this lane folds with: a_scale of its rows
+  // out_row(0), out_row(1) and b_scale of columns 32j + lane % 32 of its
+  // window.  Read at the top of the group's last stage (after its barrier,
+  // so the DMA that loaded them is complete and visible), so that their
+  // latency passes under that stage's MFMAs.
+  uint32_t sa_bits[2], sb_bits[2];
+  __device__ __forceinline__ void load_scales(const uint8_t* smem, int g) {
+    const uint8_t* sl = smem + RING + (g & 3) * SCALE_SLOT;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = out_row(i);
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(sl + 4 * row);
+      const int e = (m0 + row) * groups + g;
+      sa_bits[i] = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      sb_bits[j] = *reinterpret_cast<const uint16_t*>(sl + 512 + 2 * (wn * TN + 32 * j + (lane & 31)));
+  }
+
+  __device__ __forceinline__ void fold(const uint8_t* smem, int g) {
+    const uint8_t* sl = smem + RING + (g & 3) * SCALE_SLOT;
+    auto in_range = [](uint32_t b) {
+      return (b & 0x7FFFu) == 0u || (((b >> 7) & 0xFFu) - (127u - 60u)) < 108u;
+    };
+    const bool ok = in_range(sa_bits[0]) && in_range(sa_bits[1]) && in_range(sb_bits[0]) && in_range(sb_bits[1]);
+    if (__all(ok)) {
+      // second MFMA operand: a_scale of the block's 32 rows at K = 0 (lanes
+      // 0-31, first element); first operand: b_scale of its 32 columns
+      f6_bf8 ya[2], xb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ya[i] = f6_bf8{};
+        xb[i] = f6_bf8{};
+        if (lane < 32) {
+          ya[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sa_bits[i]);
+          xb[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sb_bits[i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v16f ab = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[j], ya[i], v16f{}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float x = acc[i][j][r] * ab[r];
+            tot[i][j][r] = tot[i][j][r] + x;
+          }
+        }
+      return;
+    }
+    all_fast = false;
+    float sa[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) sa[i] = __uint_as_float(sa_bits[i] << 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint2 w = *reinterpret_cast<const uint2*>(sl + 512 + 2 * out_col(j, q));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            float x = acc[i][j][4 * q + t] * sa[i];
+            x = x * f6_bf16_at(w, t);
+            tot[i][j][4 * q + t] = tot[i][j][4 * q + t] + x;
+          }
+      }
+  }
+
+  // RAW mode: adds group g's exact integer partial sums into the totals,
+  // which then hold int32 bit patterns.
+  __device__ __forceinline__ void fold_raw() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          tot[i][j][x] = __int_as_float(__float_as_int(tot[i][j][x]) + (int)acc[i][j][x]);
+  }
+
+  // After group g's last stage (on set S, which read nothing): the MFMA
+  // results land, the group folds, then the next stage's fragments are read
+  // into set 1 - S from `r`.  Reading them after the fold rather than during
+  // the stage keeps their 48 registers free while the fold needs its own
+  // beside the totals and accumulators.
+  template <bool RAW, int S>
+  __device__ __forceinline__ void end_group(const uint8_t* smem, int g, const Reads& r) {
+    fence<7>();
+    if constexpr (RAW) fold_raw();
+    else fold(smem, g);
+    // keeps the reads (and their destination registers) after the fold
+    __builtin_amdgcn_sched_barrier(0);
+    reads<1 - S>(r, std::make_integer_sequence<int, 16>{});
+  }
+
+  // nst: 128-K stages (a multiple of 2).  RAW: the totals receive the exact
+  // int32 sum over all K instead of the scaled fp32 sum.  The step-0 MFMAs
+  // of every group's first stage take 0 as their C operand in both modes: no
+  // MFMA reads accumulators that VALU code wrote (between the tiles of a
+  // persistent workgroup, such a read returned stale values).
+  template <bool RAW>
+  __device__ __forceinline__ void run(const uint8_t* smem, int nst) {
+    const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
+    const v4i rss_end = v4i{rss.x, rss.y, 0, rss.w};
+    const int s8 = 130;  // E8M0 2^3: both operands hold v/8
+    // stages 0 .. P-1 (zeros past the last stage) with their groups' scales
+#pragma unroll
+    for (int st = 0; st < P; ++st) {
+      const bool live = st < nst;
+#pragma unroll
+      for (int c = 0; c < OPW; ++c)
+        lds_dma16(live ? rs : rs_end, voff[c], live ? (uint32_t)st * PANEL : 0u,
+                  lds0 + (uint32_t)st * STAGE + 1024u * (OPW * wave + c));
+      // (the nop: the wait state between the M0 write and the LDS-DMA load)
+      asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+                   :
+                   : "v"(live ? scale_voff(st / SPG) : 0u), "s"(live ? rss : rss_end), "{m0}"(scale_m0(st / SPG))
+                   : "memory");
+    }
+    wait_vmcnt<(P - 1) * DPW>();
+    asm volatile("s_barrier" ::: "memory");
+    reads<0>(reads_of_slot(0), std::make_integer_sequence<int, 16>{});
+    fence<4>();
+    Reads r = reads_of_slot(1);
+    int slot = 0;
+    int k = 0;
+    // The reads after the last fold fetch a stale slot into the set no MFMA
+    // uses (set 0); they land, naming their registers, before the registers
+    // could be reused.
+    for (; k < nst; k += 2) {
+      stage<0, true, true>(smem, r, k, nst, slot, rs_end, rss_end, s8);
+      advance(r, slot);
+      stage<1, false, false>(smem, r, k + 1, nst, slot, rs_end, rss_end, s8);
+      end_group<RAW, 1>(smem, k / 2, r);
+      advance(r, slot);
+    }
+    frag_fence<0>();
+    // the loads past the last stage land before the workgroup's LDS is freed
+    wait_vmcnt<0>();
+    fence<7>();
+  }
+};
+
+// The 64-K-stage engine, for groups of 128: one 32 x 64 fp6 block per
+// 32-row panel per stage (6 KiB of A and 6 KiB of B) in a ring of six
+// slots, SPG = 2 stages per group.  Stage k: wait for this wave's DMA of
+// stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
+// carrying (the first two) the 8 LDS reads of stage k+1's fragments and the
+// 4 DMA loads of stage k+6 into slot k % 6 (3 operand loads and one scale
+// load per wave); then a fence that waits for this stage's LDS reads with
+// every fragment register of the other set as an operand.  Scales of group
+// g load 5 stages before its first stage, into slot g % 4 of the scale ring
+// (laid out as for the 128-K engine).  (The 128-K engine does not fit 256
+// registers with a fold after every stage.)
+template <class C, int SPG>
+struct F6SubEngine64 {
   static constexpr int P = 6;                       // ring slots
   static constexpr int NW = 4;
   static constexpr int OPB = 4 * F6_BLOCK;          // 128 rows x 64 K: 6 KiB
@@ -492,10 +921,12 @@ __device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, 
 }
 
 // One 128 x 128 output tile of the subchannel GEMM over fp6 blocks (p.a /
-// p.b point at the converted A and B); SPG = S / 64 stages per scale group.
+// p.b point at the converted A and B); SPG = S / 128 (2: the 128-K-stage
+// engine, 1: the 64-K-stage one).
 template <class C, int MODE, int EPI, int SPG>
 __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, int tile) {
-  using E = F6SubEngine<C, SPG>;
+  using E = std::conditional_t<SPG == 2, F6SubEngine<C>, F6SubEngine64<C, 2>>;
+  static_assert(F6SubEngine<C>::LDS_BYTES == F6SubEngine64<C, 2>::LDS_BYTES, "both engines fill the same LDS");
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
@@ -505,7 +936,7 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
   E e;
   e.setup(smem, p.a, p.b, m0, n0, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.N, p.K), p.a_scale,
           p.b_scale, p.M, p.N, p.K / p.subchannel);
-  e.template run<MODE == OUT_I32>(smem, p.K / 64);
+  e.template run<MODE == OUT_I32>(smem, p.K / (SPG == 2 ? 128 : 64));
   const OutView o{p.out, p.b_scale, p.N, p.M, p.N, 0, p.M, p.N};
   if constexpr (MODE == OUT_I32) {
     f6sub_store_words(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
@@ -523,7 +954,7 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
 // tile, two workgroups per CU.
 template <class C, int MODE, int EPI, int SPG>
 __global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C, SPG>::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C>::LDS_BYTES];
   f6_sub_tile<C, MODE, EPI, SPG>(p, smem, blockIdx.x);
 }
 
@@ -531,7 +962,7 @@ __global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
 // over the tiles, with every LDS read done before the next tile's prologue.
 template <class C, int MODE, int EPI, int SPG>
 __global__ __launch_bounds__(256, 2) void f6_sub_persistent(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C, SPG>::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C>::LDS_BYTES];
   const int tiles = (p.M / C::BM) * (p.N / C::BN);
   for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
     f6_sub_tile<C, MODE, EPI, SPG>(p, smem, t);

@@ -18,7 +18,13 @@ destination within MFMA_WAIT_STATES of it (each instruction counts one
 wait state, s_nop N counts N + 1; 18 covers a 16-pass MFMA's result
 latency for a VALU or memory reader).
 
-The scan follows the text order of each function."""
+Each function is split into basic blocks (labels start one; branches and
+s_endpgm end one) and the in-flight state is propagated along the control
+flow to a fixed point: a read or MFMA result counts as pending at a block's
+entry if it is pending at the end of any predecessor, with the fewest
+retiring operations or wait states of those paths.  So a loop that the
+compiler lays out rotated (its latch blocks placed before its header) is
+judged by its real paths, and every path is covered."""
 
 from __future__ import annotations
 
@@ -85,18 +91,136 @@ def _touched(op: str, ops: list[str], line: str) -> set[int]:
     return out
 
 
+_LABEL = re.compile(r"^(\.LBB\w+):")
+_BRANCH = re.compile(r"^s_(c?branch\w*)\s+(\.LBB\w+)")
+LGKM_MAX = 15  # outstanding LDS/SMEM operations a wave can have
+
+
+def _blocks(lines: list[tuple[int, str, bool]]):
+    """Basic blocks of one function: (label or None, [(line no, text, in asm)], successor labels, falls through)."""
+    blocks, cur, label = [], [], None
+
+    def close(succ, falls):
+        nonlocal cur, label
+        blocks.append((label, cur, succ, falls))
+        cur, label = [], None
+
+    for no, s, in_asm in lines:
+        m = _LABEL.match(s)
+        if m:
+            if cur or label is not None:
+                close([], True)
+            label = m.group(1)
+            continue
+        cur.append((no, s, in_asm))
+        b = _BRANCH.match(s)
+        if b:
+            close([b.group(2)], b.group(1) != "branch")
+        elif s.startswith(("s_endpgm", "s_setpc", "s_trap")):
+            close([], False)
+    if cur or label is not None:
+        close([], False)
+    return blocks
+
+
+def _step(state, no, s, in_asm, fn, found):
+    """Advances (reads, mfmas) over one instruction, recording hazards in found (if not None)."""
+    reads, mfma = state  # reads: {line: (asm, regs, ops issued after)}; mfma: {line: (regs, wait states)}
+    nop = _NOP.match(s)
+    ws = int(nop.group(1)) + 1 if nop else 1
+    op0, ops0 = _operands(s)
+    if op0.startswith("v_mfma"):
+        mfma = {l: (r, w + ws) for l, (r, w) in mfma.items() if w + ws < MFMA_WAIT_STATES + 1}
+        if in_asm:
+            mfma[no] = (_mfma_regs(ops0[0]), 0)
+    else:
+        if not s.startswith("s_") and found is not None:
+            t = _touched(op0, ops0, s)
+            for l, (r, w) in sorted(mfma.items()):
+                if w < MFMA_WAIT_STATES and r & t:
+                    found.append(f"{fn}: line {no} '{s}' touches the asm MFMA result of line {l} "
+                                 f"after {w} wait states")
+                    break
+        mfma = {l: (r, w + ws) for l, (r, w) in mfma.items() if w + ws < MFMA_WAIT_STATES}
+    m = _LGKM.search(s)
+    if s.startswith("s_waitcnt") and m:
+        n = int(m.group(1))
+        return {l: x for l, x in reads.items() if x[2] < n}, mfma
+    op, ops = _operands(s)
+    if found is not None:
+        live = {}
+        for l, (is_asm, regs, _) in reads.items():
+            if is_asm:
+                for r in regs:
+                    live.setdefault(r, l)
+        if live and not op.startswith("ds_"):
+            touched = (_srcs(op, ops) | _dst(op, ops, s)) & set(live)
+            if touched:
+                found.append(f"{fn}: line {no} '{s}' touches v{sorted(touched)} of the asm ds_read at line "
+                             f"{min(live[r] for r in touched)}")
+    if op.startswith(("ds_", "s_load", "s_buffer_load")):
+        reads = {l: (a, r, c + 1) for l, (a, r, c) in reads.items() if c + 1 < LGKM_MAX}
+        reads[no] = (in_asm and op.startswith("ds_read"), _dst(op, ops, s) if op.startswith("ds_read") else set(), 0)
+    return reads, mfma
+
+
+def _merge(a, b):
+    if a is None:
+        return b
+    reads = dict(a[0])
+    for l, (x, r, c) in b[0].items():
+        reads[l] = (x, r, min(c, reads[l][2])) if l in reads else (x, r, c)
+    mfma = dict(a[1])
+    for l, (r, w) in b[1].items():
+        mfma[l] = (r, min(w, mfma[l][1])) if l in mfma else (r, w)
+    return reads, mfma
+
+
+def _function_hazards(fn: str, lines: list[tuple[int, str, bool]]) -> list[str]:
+    blocks = _blocks(lines)
+    index = {lab: i for i, (lab, _, _, _) in enumerate(blocks) if lab is not None}
+    succ = []
+    for i, (_, _, targets, falls) in enumerate(blocks):
+        out = [index[t] for t in targets if t in index]
+        if falls and i + 1 < len(blocks):
+            out.append(i + 1)
+        succ.append(out)
+    entry = [None] * len(blocks)
+    entry[0] = ({}, {})
+    work = [0]
+    while work:
+        i = work.pop()
+        st = entry[i]
+        for no, s, in_asm in blocks[i][1]:
+            st = _step(st, no, s, in_asm, fn, None)
+        for j in succ[i]:
+            merged = _merge(entry[j], st)
+            if merged != entry[j]:
+                entry[j] = merged
+                work.append(j)
+    found: list[str] = []
+    for i, blk in enumerate(blocks):
+        if entry[i] is None:
+            continue
+        st = entry[i]
+        for no, s, in_asm in blk[1]:
+            st = _step(st, no, s, in_asm, fn, found)
+    return found
+
+
 def inflight_lds_hazards(asm: str) -> list[str]:
     """Lines that touch a register of an asm ds_read still in flight, or of
-    an asm MFMA's result within MFMA_WAIT_STATES of it."""
-    found = []
-    fn = "?"
-    queue: list[tuple[bool, set[int], int]] = []  # (asm read, registers, line)
-    mfma: list[tuple[set[int], int, int]] = []    # (destination, wait states since, line)
-    in_asm = False
+    an asm MFMA's result within MFMA_WAIT_STATES of it, on some path."""
+    found: list[str] = []
+    fn, lines, in_asm = None, [], False
     for no, raw in enumerate(asm.splitlines(), 1):
         s = raw.strip()
         if re.match(r"^_Z\S+:", s):
-            fn, queue, mfma = s.split(":")[0], [], []
+            if fn is not None:
+                found += _function_hazards(fn, lines)
+            fn, lines, in_asm = s.split(":")[0], [], False
+            continue
+        if fn is None:
             continue
         if s.startswith(";;#ASMSTART"):
             in_asm = True
@@ -104,44 +228,9 @@ def inflight_lds_hazards(asm: str) -> list[str]:
         if s.startswith(";;#ASMEND"):
             in_asm = False
             continue
-        if not s or s.startswith((";", ".")):
+        if not s or s.startswith(";") or (s.startswith(".") and not _LABEL.match(s)):
             continue
-        nop = _NOP.match(s)
-        ws = int(nop.group(1)) + 1 if nop else 1
-        op0, ops0 = _operands(s)
-        if op0.startswith("v_mfma"):
-            # an MFMA may take another MFMA's result as its accumulator
-            if in_asm:
-                mfma.append((_mfma_regs(ops0[0]), 0, no))
-            mfma = [(r, w + ws, l) for r, w, l in mfma]
-            mfma = [x for x in mfma if x[1] < MFMA_WAIT_STATES + 1]
-        else:
-            pending = [x for x in mfma if x[1] < MFMA_WAIT_STATES]
-            if pending and not s.startswith("s_"):
-                t = _touched(op0, ops0, s)
-                for r, w, l in pending:
-                    if r & t:
-                        found.append(f"{fn}: line {no} '{s}' touches the asm MFMA result of line {l} "
-                                     f"after {w} wait states")
-                        break
-            mfma = [(r, w + ws, l) for r, w, l in mfma if w + ws < MFMA_WAIT_STATES]
-        m = _LGKM.search(s)
-        if s.startswith("s_waitcnt") and m:
-            n = int(m.group(1))
-            queue = queue[len(queue) - n:] if 0 < n < len(queue) else ([] if n == 0 else queue)
-            continue
-        op, ops = _operands(s)
-        live: set[int] = set()
-        for is_asm, regs, _ in queue:
-            if is_asm:
-                live |= regs
-        if live and not op.startswith("ds_"):
-            touched = (_srcs(op, ops) | _dst(op, ops, s)) & live
-            if touched:
-                src = min(q[2] for q in queue if q[0] and q[1] & touched)
-                found.append(f"{fn}: line {no} '{s}' touches v{sorted(touched)} of the asm ds_read at line {src}")
-        if op.startswith(("ds_", "s_load", "s_buffer_load")):
-            queue.append((in_asm and op.startswith("ds_read"), _dst(op, ops, s) if op.startswith("ds_read") else set(),
-                          no))
-            queue = queue[-15:]
+        lines.append((no, s, in_asm))
+    if fn is not None:
+        found += _function_hazards(fn, lines)
     return found

@@ -71,10 +71,25 @@ def test_the_scan_finds_a_reuse_and_a_copy():
     asm2 = "\n".join(["_Zk:", ";;#ASMSTART", "ds_read_b64 v[4:5], v1", ";;#ASMEND", "ds_read_b64 v[6:7], v1",
                       "s_waitcnt lgkmcnt(2)", "v_mov_b32_e32 v9, v4", "s_waitcnt lgkmcnt(1)", "v_mov_b32_e32 v9, v4"])
     assert len(inflight_lds_hazards(asm2)) == 1
-    # an asm MFMA's result read 6 wait states later, then after 21
+    # an asm MFMA's result read 5 wait states later (s_nop 4), then after 22
     asm3 = "\n".join(["_Zm:", ";;#ASMSTART",
                        "v_mfma_f32_32x32x64_f8f6f4 v[2:17], v[20:25], v[30:35], v[2:17] cbsz:2 blgp:2",
                        ";;#ASMEND", "s_nop 4", "v_mov_b32_e32 v40, v5", "s_nop 7", "s_nop 7",
                        "v_mov_b32_e32 v41, v6"])
     found = inflight_lds_hazards(asm3)
-    assert len(found) == 1 and "after 6 wait states" in found[0]
+    assert len(found) == 1 and "after 5 wait states" in found[0]
+    # control flow: a loop laid out with its latch block before its header
+    # (as the compiler rotates loops) waits on every real path
+    asm4 = "\n".join(["_Zl:", ";;#ASMSTART", "ds_read_b128 v[10:13], v1", ";;#ASMEND", "s_branch .LBB0_2",
+                       ".LBB0_1:", "v_mov_b32_e32 v20, v10", "s_cbranch_scc0 .LBB0_3",
+                       ".LBB0_2:", "s_waitcnt lgkmcnt(0)", "s_branch .LBB0_1",
+                       ".LBB0_3:", "s_endpgm"])
+    assert inflight_lds_hazards(asm4) == []
+    # ... while a path that skips the wait is found, whatever the layout
+    asm5 = asm4.replace("s_branch .LBB0_2", "s_cbranch_vccz .LBB0_1\ns_branch .LBB0_2")
+    found = inflight_lds_hazards(asm5)
+    assert len(found) == 1 and "v[10]" in found[0]
+    # a read retired by 15 younger LDS operations
+    asm6 = "\n".join(["_Zq:", ";;#ASMSTART", "ds_read_b32 v10, v1", ";;#ASMEND"] + ["ds_read_b32 v11, v1"] * 15 +
+                      ["v_mov_b32_e32 v20, v10"])
+    assert inflight_lds_hazards(asm6) == []
