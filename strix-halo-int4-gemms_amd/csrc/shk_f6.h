@@ -132,6 +132,8 @@ struct F6Engine {
   static constexpr int DPW = STAGE / 1024 / NW;  // 12 DMA loads per wave per stage
   static constexpr int TN = SWIGLU ? 64 : 128;   // output columns per wave
   static constexpr int FN = SWIGLU ? 2 : 4;      // output column fragments per wave
+  static constexpr int MI = 4;                   // 32-row fragments per wave
+  static constexpr int WROWS = 32 * MI;          // output rows per wave
   static_assert(C::BM == 256 && C::WM == 2 && C::WN == 2 && C::BROWS == 256, "256-row tiles, 2x2 waves");
 
   v16f acc[4][4];
@@ -439,9 +441,9 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const OutView& o, int m0
                              ((unsigned long long)o.rows * ldo - first) * ESZ);
   const uint32_t voff = ((uint32_t)e.out_row(0) * ldo + (uint32_t)e.out_col(0, 0)) * ESZ;
   // rows of this lane inside the written range (MASK)
-  bool row_in[4];
+  bool row_in[E::MI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < E::MI; ++i) {
     const int row = m0 + e.out_row(i);
     row_in[i] = !MASK || (row >= o.row_lo && row < o.row_hi);
   }
@@ -460,7 +462,7 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const OutView& o, int m0
         sg[t] = C::SWIGLU ? f6_bf16_at(sb[j + 2 < 4 ? j + 2 : j][q], t) : 0.0f;
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < E::MI; ++i) {
         const uint32_t soff = (uint32_t)(32 * i) * ldo * ESZ;
         const bool in = !MASK || (row_in[i] && col_in);
         if constexpr (MODE == OUT_I32) {
@@ -515,7 +517,7 @@ __device__ __forceinline__ void f6_epilogue(const E& e, const OutView& o, int m0
   }
 }
 
-// bf16 epilogue through LDS.  Each wave writes its 128-row bf16 results
+// bf16 epilogue through LDS.  Each wave writes its WROWS-row bf16 results
 // into its own region of the (now idle) ring, then reads the region back
 // row-contiguously and writes whole row segments with 16-byte stores,
 // instead of 32 rows x 16 bytes per store instruction.  16-byte unit u
@@ -533,15 +535,15 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
   // With bounded scales (NO_NAN) the engine's power-of-two factor folds into
   // the A scale: UNSCALE * sa is exact below 2^48, so stored * (UNSCALE * sa)
   // is the same real product as (stored * UNSCALE) * sa and rounds alike.
-  float sx[4];
+  float sx[E::MI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sx[i] = NO_NAN ? sa[i] * E::UNSCALE : sa[i];
+  for (int i = 0; i < E::MI; ++i) sx[i] = NO_NAN ? sa[i] * E::UNSCALE : sa[i];
   auto scaled = [&](int i, int j, int x) {
     return (NO_NAN ? e.acc_stored(i, j, x) : e.acc_value(i, j, x)) * sx[i];
   };
   // every wave has finished reading the ring
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  uint8_t* region = smem + (size_t)e.wave * 128 * PITCH;
+  uint8_t* region = smem + (size_t)e.wave * E::WROWS * PITCH;
   const int lane = e.lane;
   const int half = 8 * (lane >> 5);  // columns +4 .. +7 of a unit
 #pragma unroll
@@ -555,12 +557,12 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
         sg[t] = C::SWIGLU ? f6_bf16_at(sb[j + 2 < 4 ? j + 2 : j][q], t) : 0.0f;
       }
       const int u = 4 * j + q;  // columns 32j + 8q .. +7
-      float v[4][4];            // [row i][column t]
+      float v[E::MI][4];        // [row i][column t]
       if constexpr (C::SWIGLU) {
-        float up[4][4], gt[4][4];
+        float up[E::MI][4], gt[E::MI][4];
         float gmax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < E::MI; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             up[i][t] = scaled(i, j, 4 * q + t);
@@ -574,18 +576,18 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
         // gives NaN on either path)
         if (__all(gmax <= SWIGLU_FAST_MAX)) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < E::MI; ++i)
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[i][t] = swiglu_fast(up[i][t], gt[i][t]);
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < E::MI; ++i)
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[i][t] = swiglu(up[i][t], gt[i][t]);
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < E::MI; ++i)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             float x = scaled(i, j, 4 * q + t);
@@ -595,7 +597,7 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
           }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < E::MI; ++i) {
         uint32_t lo, hi;
         if constexpr (NO_NAN) {
           lo = pack_bf16x2_nonan(v[i][0], v[i][1]);
@@ -616,13 +618,13 @@ __device__ __forceinline__ void mfma32_epilogue_lds(const E& e, const OutView& o
   const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(o.out) + first * 2, ((unsigned long long)o.rows * ldo - first) * 2);
   constexpr int ROWS = 64 / UNITS;
   const int rr = lane / UNITS, u = lane % UNITS;
-  const uint32_t voff = ((uint32_t)(e.wm * 128 + rr) * ldo + (uint32_t)(e.wn * E::TN + 8 * u)) * 2u;
+  const uint32_t voff = ((uint32_t)(e.wm * E::WROWS + rr) * ldo + (uint32_t)(e.wn * E::TN + 8 * u)) * 2u;
   const bool col_in = !MASK || n0 + e.wn * E::TN + 8 * u < o.col_hi;
 #pragma unroll
-  for (int t = 0; t < 128 / ROWS; ++t) {
+  for (int t = 0; t < E::WROWS / ROWS; ++t) {
     const int r = ROWS * t + rr;
     const uint4 x = *reinterpret_cast<const uint4*>(region + r * PITCH + 16 * (u ^ swz(r)));
-    const int row = m0 + e.wm * 128 + r;
+    const int row = m0 + e.wm * E::WROWS + r;
     if (!MASK || (col_in && row >= o.row_lo && row < o.row_hi))
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(ROWS * t) * ldo * 2u,
                                              0);
@@ -689,7 +691,7 @@ __device__ __forceinline__ void mfma32_finish(const E& e, const OutView& o, uint
     constexpr uint32_t F32_LIM = (127u + 48u) << 23, BF16_LIM = (127u + 48u) << 7;
     bool bounded = true;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bounded = bounded && (__float_as_uint(sa[i]) & 0x7F800000u) < F32_LIM;
+    for (int i = 0; i < E::MI; ++i) bounded = bounded && (__float_as_uint(sa[i]) & 0x7F800000u) < F32_LIM;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll

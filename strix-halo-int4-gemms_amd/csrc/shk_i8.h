@@ -33,25 +33,29 @@ struct I8Engine {
   static constexpr bool SWIGLU = C::SWIGLU;
   static constexpr int P = 4;
   static constexpr int NW = 4;
-  using OA = DmaOperand<8, C::A_KMAJOR, 256, NW, 256>;
+  static constexpr int MI = C::BM / 64;                // 32-row A fragments per wave: 4 or 2
+  static constexpr int WROWS = 32 * MI;                // output rows per wave
+  using OA = DmaOperand<8, C::A_KMAJOR, C::BM, NW, C::BM>;
   using OB = DmaOperand<8, C::B_KMAJOR, 256, NW, C::BHALF>;
-  static constexpr int OPB = 256 * 64;                 // one operand's stage: 16 KiB
-  static constexpr int STAGE = 2 * OPB;                // 32 KiB
-  static constexpr int LDS_BYTES = P * STAGE;          // 128 KiB
-  static constexpr int DPW = OA::BLK + OB::BLK;        // 8 DMA loads per wave per stage
+  static constexpr int A_BYTES = C::BM * 64;           // A's part of a stage: 16 or 8 KiB
+  static constexpr int STAGE = A_BYTES + 256 * 64;     // then 16 KiB of B
+  static constexpr int LDS_BYTES = P * STAGE;          // 128 or 96 KiB
+  static constexpr int DPW = OA::BLK + OB::BLK;        // 8 or 6 DMA loads per wave per stage
   static constexpr int TN = SWIGLU ? 64 : 128;         // output columns per wave
   static constexpr int FN = SWIGLU ? 2 : 4;            // output column fragments per wave
   static constexpr int NA = C::A_KMAJOR ? 1 : 2;       // LDS reads per A fragment and step
   static constexpr int NB = C::B_KMAJOR ? 1 : 2;
-  static constexpr int RSTEP = 4 * (NA + NB);          // LDS reads per step
-  static constexpr int READS = 2 * RSTEP;              // per stage (<= 32)
-  static_assert(C::BITS == 8 && C::BM == 256 && C::BROWS == 256 && C::WM == 2 && C::WN == 2,
-                "int8, 256-row tiles, 2x2 waves");
-  static_assert(DPW == 8 && READS <= 32, "schedule");
+  static constexpr int RSTEP = MI * NA + 4 * NB;       // LDS reads per step
+  static constexpr int READS = 2 * RSTEP;              // per stage
+  static constexpr int TICKS = 2 * MI * 4;             // MFMAs per stage
+  static_assert(C::BITS == 8 && (C::BM == 256 || (C::BM == 128 && C::A_KMAJOR)) && C::BROWS == 256 &&
+                    C::WM == 2 && C::WN == 2,
+                "int8, 256-row tiles (128-row tiles with a K-major A), 2x2 waves");
+  static_assert(2 * DPW <= TICKS && READS <= 2 * TICKS, "schedule");
 
-  v16i acc[4][4];
-  v4i fa[2][2][4];  // [set][step][i]
-  v4i fb[2][2][4];  // [set][step][j]
+  v16i acc[MI][4];
+  v4i fa[2][2][MI];  // [set][step][i]
+  v4i fb[2][2][4];   // [set][step][j]
   OA oa;
   OB ob;
   v4i rsa, rsb;
@@ -68,7 +72,7 @@ struct I8Engine {
   __device__ __forceinline__ int brow(int j) const {
     return SWIGLU ? (j < 2 ? 64 * wn + 32 * j : 128 + 64 * wn + 32 * (j - 2)) : 128 * wn + 32 * j;
   }
-  __device__ __forceinline__ int out_row(int i) const { return wm * 128 + 32 * i + (lane & 31); }
+  __device__ __forceinline__ int out_row(int i) const { return wm * WROWS + 32 * i + (lane & 31); }
   __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
   __device__ __forceinline__ float acc_value(int i, int j, int x) const { return (float)acc[i][j][x]; }
   static constexpr float UNSCALE = 1.0f;
@@ -111,21 +115,21 @@ struct I8Engine {
     // read bases of slot 1 (stage 1 is read during stage 0)
     const uint32_t s1 = lds0 + (uint32_t)STAGE;
     if constexpr (C::A_KMAJOR) {
-      ra[0] = s1 + kmajor_base(128 * wm, 0);
-      ra[1] = s1 + kmajor_base(128 * wm, 1);
+      ra[0] = s1 + kmajor_base(WROWS * wm, 0);
+      ra[1] = s1 + kmajor_base(WROWS * wm, 1);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) ra[i] = s1 + mnmajor_base(128 * wm + 32 * i);
     }
     if constexpr (C::B_KMAJOR) {
-      rb[0] = s1 + OPB + kmajor_base(brow(0), 0);
-      rb[1] = s1 + OPB + kmajor_base(brow(0), 1);
+      rb[0] = s1 + A_BYTES + kmajor_base(brow(0), 0);
+      rb[1] = s1 + A_BYTES + kmajor_base(brow(0), 1);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) rb[j] = s1 + OPB + mnmajor_base(brow(j));
+      for (int j = 0; j < 4; ++j) rb[j] = s1 + A_BYTES + mnmajor_base(brow(j));
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -141,7 +145,7 @@ struct I8Engine {
   }
 
   // Read Q of a stage into set S.  Per step the fragments in the order of
-  // their first use: A0, B0..B3, A1..A3, each in NA / NB parts.
+  // their first use: A0, B0..B3, A1..A(MI-1), each in NA / NB parts.
   template <int S, int Q>
   __device__ __forceinline__ void read() {
     constexpr int ST = Q / RSTEP;
@@ -174,19 +178,20 @@ struct I8Engine {
     }
   }
 
-  // MFMA T (0..31) of a stage on set S (step T/16, A fragment (T%16)/4, B
-  // fragment T%4), fused with DMA load T/2 (odd T < 16: A blocks, then B
-  // blocks) of the stage being loaded, followed by LDS read T of the next
-  // stage.  No branch surrounds an asm MFMA or LDS read (see shk_f6.h).
+  // MFMA T (0..TICKS-1) of a stage on set S (step T / (4 MI), A fragment
+  // (T % 4 MI) / 4, B fragment T % 4), fused with DMA load T/2 (odd T <
+  // 2 DPW: A blocks, then B blocks) of the stage being loaded, followed by
+  // LDS reads T and T + TICKS (while below READS) of the next stage.  No
+  // branch surrounds an asm MFMA or LDS read (see shk_f6.h).
   template <int S, int T>
   __device__ __forceinline__ void tick(const v4i& rsa_st, const v4i& rsb_st, uint32_t soa, uint32_t sob, uint32_t m0) {
-    constexpr int ST = T / 16, I = (T % 16) / 4, J = T % 4;
+    constexpr int ST = T / (4 * MI), I = (T % (4 * MI)) / 4, J = T % 4;
     if constexpr (T % 2 == 1 && T < 2 * DPW) {
       constexpr int c = T / 2;
       constexpr bool DA = c < OA::BLK;
       const v4i& rs = DA ? rsa_st : rsb_st;
       const uint32_t voff = DA ? oa.voff[c] : ob.voff[c - OA::BLK];
-      const uint32_t dst = m0 + (DA ? 1024u * (OA::BLK * wave + c) : OPB + 1024u * (OB::BLK * wave + c - OA::BLK));
+      const uint32_t dst = m0 + (DA ? 1024u * (OA::BLK * wave + c) : A_BYTES + 1024u * (OB::BLK * wave + c - OA::BLK));
       asm volatile(
           "v_mfma_i32_32x32x32_i8 %0, %1, %2, %0\n\t"
           "buffer_load_dwordx4 %3, %4, %5 offen lds"
@@ -199,6 +204,7 @@ struct I8Engine {
                    : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]));
     }
     if constexpr (T < READS) read<1 - S, T>();
+    if constexpr (T + TICKS < READS) read<1 - S, T + TICKS>();
   }
   template <int S, int... T>
   __device__ __forceinline__ void ticks(const v4i& rsa_st, const v4i& rsb_st, uint32_t soa, uint32_t sob,
@@ -225,11 +231,18 @@ struct I8Engine {
   __device__ __forceinline__ void fence() {
     static_assert(N == 4 || N == 7, "wait states");
 #define SHK_I8_ACC(i) "+a"(acc[i][0]), "+a"(acc[i][1]), "+a"(acc[i][2]), "+a"(acc[i][3])
-    if constexpr (N == 4)
-      asm volatile("s_nop 4" : SHK_I8_ACC(0), SHK_I8_ACC(1), SHK_I8_ACC(2), SHK_I8_ACC(3));
-    else
-      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-                   : SHK_I8_ACC(0), SHK_I8_ACC(1), SHK_I8_ACC(2), SHK_I8_ACC(3));
+    if constexpr (MI == 4) {
+      if constexpr (N == 4)
+        asm volatile("s_nop 4" : SHK_I8_ACC(0), SHK_I8_ACC(1), SHK_I8_ACC(2), SHK_I8_ACC(3));
+      else
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                     : SHK_I8_ACC(0), SHK_I8_ACC(1), SHK_I8_ACC(2), SHK_I8_ACC(3));
+    } else {
+      if constexpr (N == 4)
+        asm volatile("s_nop 4" : SHK_I8_ACC(0), SHK_I8_ACC(1));
+      else
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" : SHK_I8_ACC(0), SHK_I8_ACC(1));
+    }
 #undef SHK_I8_ACC
   }
 
@@ -243,9 +256,14 @@ struct I8Engine {
   // operand here, so none is copied before the data is in.
   template <int S, int ST>
   __device__ __forceinline__ void frag_fence() {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(fa[S][ST][0]), "+v"(fa[S][ST][1]), "+v"(fa[S][ST][2]), "+v"(fa[S][ST][3]),
-                   "+v"(fb[S][ST][0]), "+v"(fb[S][ST][1]), "+v"(fb[S][ST][2]), "+v"(fb[S][ST][3])::"memory");
+    if constexpr (MI == 4)
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fa[S][ST][0]), "+v"(fa[S][ST][1]), "+v"(fa[S][ST][2]), "+v"(fa[S][ST][3]),
+                     "+v"(fb[S][ST][0]), "+v"(fb[S][ST][1]), "+v"(fb[S][ST][2]), "+v"(fb[S][ST][3])::"memory");
+    else
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(fa[S][ST][0]), "+v"(fa[S][ST][1]), "+v"(fb[S][ST][0]), "+v"(fb[S][ST][1]),
+                     "+v"(fb[S][ST][2]), "+v"(fb[S][ST][3])::"memory");
   }
   template <int S>
   __device__ __forceinline__ void stage(int k, int nst, int slot, const v4i& rsa_end, const v4i& rsb_end) {
@@ -258,7 +276,7 @@ struct I8Engine {
     const v4i rsb_st = live ? rsb : rsb_end;
     const uint32_t soa = live ? OA::soff(k + 4, lda) : 0u;
     const uint32_t sob = live ? OB::soff(k + 4, ldb) : 0u;
-    ticks<S>(rsa_st, rsb_st, soa, sob, lds0 + (uint32_t)slot * STAGE, std::make_integer_sequence<int, 32>{});
+    ticks<S>(rsa_st, rsb_st, soa, sob, lds0 + (uint32_t)slot * STAGE, std::make_integer_sequence<int, TICKS>{});
   }
   // Moves the read bases one slot ahead (wrapping after the last) and the
   // stage slot.
@@ -286,7 +304,7 @@ struct I8Engine {
 #pragma unroll
       for (int c = 0; c < OB::BLK; ++c)
         lds_dma16(st < nst ? rsb : rsb_end, ob.voff[c], st < nst ? OB::soff(st, ldb) : 0u,
-                  base + OPB + 1024u * (OB::BLK * wave + c));
+                  base + A_BYTES + 1024u * (OB::BLK * wave + c));
     }
     wait_vmcnt<(P - 1) * DPW>();
     asm volatile("s_barrier" ::: "memory");
@@ -320,26 +338,48 @@ struct I8Engine {
   }
 };
 
-// One kernel per output mode and epilogue (chosen by the host).
+// One int8 tile at (m0, n0) on the engine of configuration T.
+template <class T, int MODE, int EPI>
+__device__ __forceinline__ void i8_tile(const DenseArgs& p, uint8_t* smem, int m0, int n0) {
+  using E = I8Engine<T>;
+  E e;
+  e.setup(smem, p, m0, n0, T::SWIGLU ? p.N : 0);
+  float sa[4] = {};
+#pragma unroll
+  for (int i = 0; i < E::MI; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
+  const OutView o = dense_view<T, MODE>(p);
+  mfma32_prefetch_b_scales<T, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
+  e.run(p.K / 64);
+  mfma32_finish<T, MODE, EPI>(e, o, smem, m0, n0, sa);
+}
+
+// The 128-row tile of a 256-row int8 configuration (K-major A).
+template <class C>
+using I8Half = Cfg<8, C::A_KMAJOR, C::B_KMAJOR, 128, C::BN, C::BK, 2, 2, C::SWIGLU, false, C::MK, false, C::PIPE>;
+
+// One kernel per output mode and epilogue (chosen by the host).  One
+// workgroup per tile.  With p.split_tn > 0 (256-row tiles, K-major A), the
+// column tiles [split_tn, N / BN) run last as twice as many 128-row tiles:
+// the host sets it when those columns would otherwise form a partial last
+// round of workgroups, which then takes about half as long.
 template <class C, int MODE, int EPI>
 __global__ __launch_bounds__(256) void i8_gemm_kernel(const DenseArgs p) {
-  using E = I8Engine<C>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[I8Engine<C>::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
+  const int main_n = p.split_tn > 0 ? p.split_tn : tiles_n;
+  const int main_tiles = tiles_m * main_n;
   int tm, tn;
-  dense_tile_coords(blockIdx.x, tiles_m, tiles_n, p.group_m, tm, tn);
-  const int m0 = tm * C::BM;
-  const int n0 = tn * C::BN;
-  E e;
-  e.setup(smem, p, m0, n0, C::SWIGLU ? p.N : 0);
-  float sa[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) sa[i] = MODE == OUT_I32 ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
-  const OutView o = dense_view<C, MODE>(p);
-  mfma32_prefetch_b_scales<C, MODE>(e, o, n0, e.lds0 + E::LDS_BYTES + 256u * e.wave);
-  e.run(p.K / 64);
-  mfma32_finish<C, MODE, EPI>(e, o, smem, m0, n0, sa);
+  if constexpr (C::BM == 256 && C::A_KMAJOR) {
+    static_assert(I8Engine<I8Half<C>>::LDS_BYTES <= I8Engine<C>::LDS_BYTES, "the half tile fits the LDS");
+    if ((int)blockIdx.x >= main_tiles) {
+      dense_tile_coords((int)blockIdx.x - main_tiles, 2 * tiles_m, tiles_n - main_n, p.group_m, tm, tn);
+      i8_tile<I8Half<C>, MODE, EPI>(p, smem, tm * 128, (main_n + tn) * C::BN);
+      return;
+    }
+  }
+  dense_tile_coords(blockIdx.x, tiles_m, main_n, p.group_m, tm, tn);
+  i8_tile<C, MODE, EPI>(p, smem, tm * C::BM, tn * C::BN);
 }
 
 }  // namespace shk

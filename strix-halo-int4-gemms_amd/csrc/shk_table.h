@@ -129,22 +129,42 @@ template <class C>
 hipError_t launch_dense_persistent_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   return launch_persistent<&dense_gemm_persistent<C>>(a, grid.x, C::NT, s);
 }
-// int8 32x32 engine: one kernel per output mode and epilogue.
+// int8 32x32 engine: one kernel per output mode and epilogue.  A grid of
+// 256-row tiles (K-major A) whose last round of workgroups would be partial
+// runs the column tiles of that round as 128-row tiles, twice as many and
+// half as long, when they fit one round (i8_gemm_kernel).
+template <class C, int MODE, int EPI>
+hipError_t launch_i8_k(const DenseArgs& a, dim3 grid, hipStream_t s) {
+  auto* k = &i8_gemm_kernel<C, MODE, EPI>;
+  DenseArgs g = a;
+  g.split_tn = 0;
+  if constexpr (C::BM == 256 && C::A_KMAJOR) {
+    const long tiles_m = a.M / C::BM, tiles_n = a.N / C::BN;
+    unsigned slots = 0;
+    const hipError_t err = persistent_grid(reinterpret_cast<const void*>(k), 256, 0xFFFFFFFFu, &slots);
+    if (err != hipSuccess) return err;
+    const long tiles = tiles_m * tiles_n;
+    const long rest = slots > 0 ? tiles % slots : 0;
+    if (tiles > (long)slots && rest > 0) {
+      const long c = (rest + tiles_m - 1) / tiles_m;  // trailing column tiles holding the partial round
+      if (2 * tiles_m * c <= (long)slots && c < tiles_n) {
+        g.split_tn = (int)(tiles_n - c);
+        grid = dim3((unsigned)(tiles_m * (tiles_n - c) + 2 * tiles_m * c));
+      }
+    }
+  }
+  hipLaunchKernelGGL(k, grid, dim3(256), 0, s, g);
+  return hipGetLastError();
+}
 template <class C>
 hipError_t launch_i8_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
-  if (a.out_mode == OUT_I32) {
-    hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_I32, EPI_NONE>), grid, dim3(256), 0, s, a);
-  } else if (a.out_mode == OUT_F32) {
-    if (!C::SWIGLU && a.epilogue == EPI_RELU2)
-      hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_F32, EPI_RELU2>), grid, dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_F32, EPI_NONE>), grid, dim3(256), 0, s, a);
-  } else if (!C::SWIGLU && a.epilogue == EPI_RELU2) {
-    hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_BF16, EPI_RELU2>), grid, dim3(256), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((i8_gemm_kernel<C, OUT_BF16, EPI_NONE>), grid, dim3(256), 0, s, a);
+  if (a.out_mode == OUT_I32) return launch_i8_k<C, OUT_I32, EPI_NONE>(a, grid, s);
+  if (a.out_mode == OUT_F32) {
+    if (!C::SWIGLU && a.epilogue == EPI_RELU2) return launch_i8_k<C, OUT_F32, EPI_RELU2>(a, grid, s);
+    return launch_i8_k<C, OUT_F32, EPI_NONE>(a, grid, s);
   }
-  return hipGetLastError();
+  if (!C::SWIGLU && a.epilogue == EPI_RELU2) return launch_i8_k<C, OUT_BF16, EPI_RELU2>(a, grid, s);
+  return launch_i8_k<C, OUT_BF16, EPI_NONE>(a, grid, s);
 }
 template <class C>
 hipError_t launch_fwd_t(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {

@@ -215,6 +215,47 @@ def test_config_c4_int8_swiglu(device):
     assert max_ulp(got, want) <= ULP_TOL
 
 
+# the int8 32x32 engine's 256-row tiles (four-stage ring) with a K-major A
+_I8_BIG = [k for k in _UNSPLIT
+           if kt.TABLE[k.table_index].dtype_bits == 8 and kt.TABLE[k.table_index].num_stages == 4
+           and k.tile.block_m == 256 and k.layout.value in ("nn", "nt")]
+
+
+@pytest.mark.parametrize("kernel", _I8_BIG, ids=lambda k: k.kernel_id)
+def test_int8_partial_last_round_runs_half_height_tiles(kernel, device):
+    """17 column tiles x 16 row tiles = 272 of the 256-row int8 tiles: one
+    full round on the chip's CUs and 16 tiles over.  The launcher then runs
+    the last column tile as 32 tiles of 128 rows (i8_gemm_kernel's split),
+    so both tile heights and the split's column mapping are exercised; every
+    output is checked: int32 exact against the C oracle, bf16 exact (plain)
+    or within 2 ulp (SwiGLU) against the oracle."""
+    from oracle import native as oracle_native
+
+    if not oracle_native.available():
+        from oracle import build as obuild
+
+        obuild.build(verbose=False)
+    bits, layout, sub, epi = _kernel_params(kernel)
+    swiglu = epi == "swiglu"
+    m, n, k = 4096, 17 * kernel.tile.block_n, 256
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles = (m // 256) * 17
+    # a partial last round that one column tile holds, and whose 2 x 16
+    # half-height tiles fit one round
+    assert tiles > cus and 0 < tiles % cus <= m // 256 and 2 * (m // 256) <= cus
+    seed = stable_seed("i8-split", kernel.kernel_id)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=8, layout=layout, m=m, n=n, k=k, subchannel=None,
+                                                 swiglu=swiglu, scale_lo=1e-4, scale_hi=1e-3)
+    print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
+    got, raw = _run_kernel(kernel, a_arg, b_arg, sa, sb, device)
+    assert np.array_equal(raw, oracle_native.matmul_i8(a_q, b_q)), "int32 accumulators differ"
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=8, layout=layout, a_scale=sa, b_scale=sb, epilogue=epi)
+    if swiglu:
+        assert max_ulp(got, want) <= ULP_TOL
+    else:
+        assert np.array_equal(got, want)
+
+
 def test_shape_and_layout_errors(device):
     a = torch.zeros((100, 32), dtype=torch.uint8, device=device)
     b = torch.zeros((32, 64), dtype=torch.uint8, device=device)
