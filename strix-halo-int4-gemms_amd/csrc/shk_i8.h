@@ -19,7 +19,8 @@
 //    [8, 16), which hand lane l the bytes of its column.
 // Stage k waits for its own DMA of stage k+1, then the barrier; its 32 MFMAs
 // (2 steps x 4 x 4) carry the LDS reads of stage k+1 and, on the odd MFMAs
-// 1 .. 15, the DMA loads of stage k+4 into slot k % 4 (three stages ahead).
+// 1 .. 15, the DMA loads of stage k+P into slot k % P (P = 4 ring slots:
+// three stages ahead).
 #pragma once
 
 #include "shk_f6.h"
@@ -31,7 +32,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 template <class C>
 struct I8Engine {
   static constexpr bool SWIGLU = C::SWIGLU;
-  static constexpr int P = 4;
+  static constexpr int P = C::PIPE;                     // ring slots: 4 (one workgroup per CU) or 3
   static constexpr int NW = 4;
   static constexpr int MI = C::BM / 64;                // 32-row A fragments per wave: 4 or 2
   static constexpr int WROWS = 32 * MI;                // output rows per wave
@@ -51,7 +52,7 @@ struct I8Engine {
   static_assert(C::BITS == 8 && (C::BM == 256 || (C::BM == 128 && C::A_KMAJOR)) && C::BROWS == 256 &&
                     C::WM == 2 && C::WN == 2,
                 "int8, 256-row tiles (128-row tiles with a K-major A), 2x2 waves");
-  static_assert(2 * DPW <= TICKS && READS <= 2 * TICKS, "schedule");
+  static_assert(2 * DPW <= TICKS && READS <= 2 * TICKS && (P == 3 || P == 4), "schedule");
 
   v16i acc[MI][4];
   v4i fa[2][2][MI];  // [set][step][i]
@@ -246,9 +247,9 @@ struct I8Engine {
 #undef SHK_I8_ACC
   }
 
-  // Stage k on set S: wait for this wave's DMA of stage k+1 (k+2 and k+3
+  // Stage k on set S: wait for this wave's DMA of stage k+1 (k+2 .. k+P-1
   // may stay outstanding), then the barrier; MFMAs of stage k, reads of
-  // stage k+1, DMA of stage k+4 into slot `slot` (k's), through zero-record
+  // stage k+1, DMA of stage k+P into slot `slot` (k's), through zero-record
   // resources past the last stage.
   // This wave's LDS reads into set S (step ST) have landed.  The reads are
   // asm statements, so the compiler does not know that their registers are
@@ -267,15 +268,15 @@ struct I8Engine {
   }
   template <int S>
   __device__ __forceinline__ void stage(int k, int nst, int slot, const v4i& rsa_end, const v4i& rsb_end) {
-    wait_vmcnt<2 * DPW>();
+    wait_vmcnt<(P - 2) * DPW>();
     frag_fence<S, 0>();
     frag_fence<S, 1>();
     asm volatile("s_barrier" ::: "memory");
-    const bool live = k + 4 < nst;
+    const bool live = k + P < nst;
     const v4i rsa_st = live ? rsa : rsa_end;
     const v4i rsb_st = live ? rsb : rsb_end;
-    const uint32_t soa = live ? OA::soff(k + 4, lda) : 0u;
-    const uint32_t sob = live ? OB::soff(k + 4, ldb) : 0u;
+    const uint32_t soa = live ? OA::soff(k + P, lda) : 0u;
+    const uint32_t sob = live ? OB::soff(k + P, ldb) : 0u;
     ticks<S>(rsa_st, rsb_st, soa, sob, lds0 + (uint32_t)slot * STAGE, std::make_integer_sequence<int, TICKS>{});
   }
   // Moves the read bases one slot ahead (wrapping after the last) and the
