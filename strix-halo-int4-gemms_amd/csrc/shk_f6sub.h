@@ -50,6 +50,33 @@
 
 namespace shk {
 
+// The fast fold of one group for a wave's 2 x 2 blocks of 32 x 32:
+// tot += part * ab, ab[i][j] = a_scale (rows of block i) x b_scale (columns
+// of block j) from one two-block rank-1 MFMA per column block j
+// (v_mfma_f32_32x32x1_2b_f32: block i takes the second operand from lanes
+// 32i .. 32i+31, so lanes 0-31 give the a_scale of block 0's rows and lanes
+// 32-63 that of block 1's; both halves give block j's b_scale as the first
+// operand).  Its output blocks are laid out as the accumulators (lane l: row
+// l % 32 of the block, its 16 columns), and each product of two bf16 values
+// is exact in fp32.  sa_bits / sb_bits: the bf16 bits of the lane's scales
+// (rows out_row(0), out_row(1); columns 32j + lane % 32).
+typedef float f6_v32f __attribute__((ext_vector_type(32)));
+__device__ __forceinline__ void f6sub_fold_fast(const v16f (&acc)[2][2], float (&tot)[2][2][16], int lane,
+                                                const uint32_t (&sa_bits)[2], const uint32_t (&sb_bits)[2]) {
+  const float av = __uint_as_float((lane < 32 ? sa_bits[0] : sa_bits[1]) << 16);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const f6_v32f ab = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(sb_bits[j] << 16), av, f6_v32f{}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = acc[i][j][r] * ab[16 * i + r];
+        tot[i][j][r] = tot[i][j][r] + x;
+      }
+  }
+}
+
 template <class C>
 struct F6SubEngine {
   static constexpr int P = 3;                       // ring slots
@@ -306,7 +333,7 @@ struct F6SubEngine {
   // tot += (float(part) * a_scale[row, g]) * b_scale[g, col].
   //
   // Fast form, two VALU operations per value: tot += part * ab with
-  // ab = a_scale * b_scale from one rank-1 bf16 MFMA per 32 x 32 block.  It
+  // ab = a_scale * b_scale from rank-1 MFMAs (f6sub_fold_fast).  It
   // gives the same bits as the reference's order whenever every scale of the
   // group is zero or a normal number of magnitude in [2^-60, 2^48): part is
   // an integer of at most 15 significant bits (|part| <= 64 * 256) and a has
@@ -342,29 +369,7 @@ struct F6SubEngine {
     };
     const bool ok = in_range(sa_bits[0]) && in_range(sa_bits[1]) && in_range(sb_bits[0]) && in_range(sb_bits[1]);
     if (__all(ok)) {
-      // second MFMA operand: a_scale of the block's 32 rows at K = 0 (lanes
-      // 0-31, first element); first operand: b_scale of its 32 columns
-      f6_bf8 ya[2], xb[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ya[i] = f6_bf8{};
-        xb[i] = f6_bf8{};
-        if (lane < 32) {
-          ya[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sa_bits[i]);
-          xb[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sb_bits[i]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v16f ab = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[j], ya[i], v16f{}, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = acc[i][j][r] * ab[r];
-            tot[i][j][r] = tot[i][j][r] + x;
-          }
-        }
+      f6sub_fold_fast(acc, tot, lane, sa_bits, sb_bits);
       return;
     }
     all_fast = false;
@@ -708,7 +713,7 @@ struct F6SubEngine64 {
   // tot += (float(part) * a_scale[row, g]) * b_scale[g, col].
   //
   // Fast form, two VALU operations per value: tot += part * ab with
-  // ab = a_scale * b_scale from one rank-1 bf16 MFMA per 32 x 32 block.  It
+  // ab = a_scale * b_scale from rank-1 MFMAs (f6sub_fold_fast).  It
   // gives the same bits as the reference's order whenever every scale of the
   // group is zero or a normal number of magnitude in [2^-60, 2^48): part is
   // an integer of at most 15 significant bits (|part| <= 64 * 256) and a has
@@ -735,29 +740,7 @@ struct F6SubEngine64 {
     };
     const bool ok = in_range(sa_bits[0]) && in_range(sa_bits[1]) && in_range(sb_bits[0]) && in_range(sb_bits[1]);
     if (__all(ok)) {
-      // second MFMA operand: a_scale of the block's 32 rows at K = 0 (lanes
-      // 0-31, first element); first operand: b_scale of its 32 columns
-      f6_bf8 ya[2], xb[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ya[i] = f6_bf8{};
-        xb[i] = f6_bf8{};
-        if (lane < 32) {
-          ya[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sa_bits[i]);
-          xb[i][0] = __builtin_bit_cast(__bf16, (uint16_t)sb_bits[i]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v16f ab = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xb[j], ya[i], v16f{}, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float x = acc[i][j][r] * ab[r];
-            tot[i][j][r] = tot[i][j][r] + x;
-          }
-        }
+      f6sub_fold_fast(acc, tot, lane, sa_bits, sb_bits);
       return;
     }
     all_fast = false;
