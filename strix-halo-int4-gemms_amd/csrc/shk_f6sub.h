@@ -38,10 +38,12 @@
 //
 // Scales of group g sit in slot g % 4 of a small ring: the a_scale dword
 // holding row r's scale (dword-aligned pair (e & ~1, e | 1) of e = row * G +
-// g) at 4 r, and the 128 b_scale values at 512.  Every stage loads the
-// scales of the group of the stage it loads (duplicates rewrite the same
-// bytes), three stages before that stage; the slot it writes last held the
-// scales of a group every wave has folded before the stage's barrier.
+// g) at 4 r, and the 128 b_scale values at 512.  With groups of 256 the
+// scales of a group load with its first stage, three stages before that
+// stage (by the previous group's second stage; those of groups 0 and 1 in
+// the prologue); with groups of 128 every stage loads its group's scales.
+// The slot a load writes last held the scales of a group every wave has
+// folded before the stage's barrier.
 #pragma once
 
 #include <type_traits>
@@ -213,10 +215,13 @@ struct F6SubEngine {
 
   // MFMA T (0..7) of a stage on set S (step T / 4, A fragment (T % 4) / 2,
   // B fragment T % 2; the step-0 MFMAs of a group's first stage (ZERO) take
-  // 0 as their C operand), fused for T < OPW with operand DMA load T and for
-  // T = OPW with the scale load of the stage loaded now, then (READ) LDS
-  // reads 2T, 2T+1 of the next stage into the other set.  Every stage runs
-  // the same branch-free sequence (see shk_f6.h).
+  // 0 as their C operand), fused for T < OPW with operand DMA load T and,
+  // in a group's second stage, for T = OPW with the scale load of the stage
+  // loaded now (which is the first stage of its group: the first stage of a
+  // group loads the second stage of a group whose scales are already
+  // loaded), then (READ) LDS reads 2T, 2T+1 of the next stage into the
+  // other set.  Every stage of a kind runs the same branch-free sequence
+  // (see shk_f6.h).
   template <int S, int T, bool ZERO, bool READ>
   __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0_st,
                                        const v4i& rss_st, uint32_t svo, uint32_t sm0, int s8) {
@@ -241,7 +246,7 @@ struct F6SubEngine {
             : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(s8), "v"(voff[T]), "s"(rs_st), "s"(so),
               "{m0}"(m0_st + 1024u * T)
             : "memory");
-    } else if constexpr (T == OPW) {
+    } else if constexpr (T == OPW && !ZERO) {
       static_assert(!Z, "the scale load rides on a step-1 MFMA");
       asm volatile(
           "v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2\n\t"
@@ -299,8 +304,10 @@ struct F6SubEngine {
   // Stage k (128 K) on set S (ZERO: the first stage of a group; READ: the
   // next stage's fragments are read here, else after the group's fold, and
   // the group's scales are read at the top).
-  // Top: this wave's DMA of stage k+1 has landed (that of k+2 may be
-  // outstanding) and its LDS reads of stage k are done, then the barrier:
+  // Top: this wave's DMA of stage k+1 has landed (that of k+2, issued by
+  // the previous stage: DPW loads after a group's second stage or the
+  // prologue, OPW after a first stage, may be outstanding) and its LDS
+  // reads of stage k are done, then the barrier:
   // stage k+1 and the scales it loaded are complete in LDS, no wave still
   // reads slot k % 3, and every wave has folded the groups before stage k.
   // Past the last stage the DMA loads go through zero-record resources into
@@ -309,7 +316,7 @@ struct F6SubEngine {
   template <int S, bool ZERO, bool READ>
   __device__ __forceinline__ void stage(const uint8_t* smem, const Reads& r, int k, int nst, int slot,
                                         const v4i& rs_end, const v4i& rss_end, int s8) {
-    wait_vmcnt<DPW>();
+    wait_vmcnt<ZERO ? DPW : OPW>();
     frag_fence<S>();
     asm volatile("s_barrier" ::: "memory");
     if constexpr (!READ) load_scales(smem, k / SPG);
