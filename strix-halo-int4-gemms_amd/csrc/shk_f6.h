@@ -99,9 +99,11 @@ __host__ __device__ constexpr int f6_panels(int rows) { return (rows + 31) / 32;
 hipError_t launch_f6_pack(const F6PackArgs& a, bool mn_major, hipStream_t s);
 // Both operands in one launch; with a job (sizes non-null, at most
 // kFusedTaskGroups groups) an extra first workgroup builds a ragged task
-// list beside the conversion.
+// list beside the conversion.  interleave: the two operands' workgroups
+// alternate in proportion instead of running A's first (the per-channel
+// dense calls).
 hipError_t launch_f6_pack2(const F6PackArgs& a, bool a_mn, const F6PackArgs& b, bool b_mn, hipStream_t s,
-                           const TaskJob* job = nullptr);
+                           const TaskJob* job = nullptr, bool interleave = false);
 
 // ---------------------------------------------------------------------------
 // GEMM engine.  Four waves in 2 x 2, each owning 128 rows x 128 packed B

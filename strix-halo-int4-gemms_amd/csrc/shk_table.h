@@ -86,7 +86,7 @@ hipError_t launch_f6_gemm_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
 template <class C>
 hipError_t launch_f6_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   hipError_t err = launch_f6_pack2(f6_pack_args(a, 0, C::SWIGLU), f6_mn_major(a, 0), f6_pack_args(a, 1, C::SWIGLU),
-                                   f6_mn_major(a, 1), s);
+                                   f6_mn_major(a, 1), s, nullptr, true);
   if (err == hipSuccess) err = launch_f6_gemm_t<C>(a, grid, s);
   return err;
 }
@@ -121,7 +121,7 @@ hipError_t launch_f6_gemm_persistent_t(const DenseArgs& a, dim3 grid, hipStream_
 template <class C>
 hipError_t launch_f6_persistent_t(const DenseArgs& a, dim3 grid, hipStream_t s) {
   hipError_t err = launch_f6_pack2(f6_pack_args(a, 0, false), f6_mn_major(a, 0), f6_pack_args(a, 1, false),
-                                   f6_mn_major(a, 1), s);
+                                   f6_mn_major(a, 1), s, nullptr, true);
   if (err == hipSuccess) err = launch_f6_gemm_persistent_t<C>(a, grid, s);
   return err;
 }
