@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void f6_pack_one(const F6PackArgs p, int mn_ma
 // tiles) A-then-B took 35 us of workgroup span, the B tiles ~22 us of it at
 // ~3.6 TB/s; interleaved, 29 us (the C2 call 2% faster).  The subchannel
 // and ragged calls keep A then B: interleaved, the C3 call was 0.5-0.8%
-// and the C5 forward 3 us slower.  With a task job, workgroup
+// slower, the C5 forward 3 us and the C5 backward ~1.4 us.  With a task job, workgroup
 // 0 (dispatched first) builds the task list in the tile's LDS and the
 // conversion shifts up by one.
 __global__ __launch_bounds__(256) void f6_pack_two(const F6PackArgs a, const F6PackArgs b, int a_mn, int b_mn,
