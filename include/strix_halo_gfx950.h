@@ -77,6 +77,18 @@ extern "C" {
  * slice for split-K entries). */
 #define SHK_OPERANDS_PACKED 0
 #define SHK_OPERANDS_FP6 1
+/* STREAM entries (block_m 16, 32, 64; block_k 32) read the packed operands
+ * straight from HBM like PACKED ones.  Per-channel calls may split a tile's
+ * K over several workgroups that add exact int32 partials; they do so only
+ * with a workspace of amd_strix_halo_kernels_gemm_workspace_bytes() bytes
+ * (0 when the shape needs no split), whose leading arrival counters must be
+ * zero before the first launch that uses it and are left zero by every
+ * completed launch, so a zero-filled workspace can be reused by launches in
+ * stream order (not by launches that overlap in time).  Without a
+ * workspace (amd_strix_halo_kernels_launch_gemm) the tile's K stays in one
+ * workgroup, which limits int4 per-channel calls to K <= 523776.  Results
+ * are identical either way. */
+#define SHK_OPERANDS_STREAM 2
 
 /* Tile schedules of a dense entry (reference metadata.KernelSchedule,
  * metadata.py:51-53).  STANDARD launches one workgroup per output tile;
@@ -116,11 +128,13 @@ typedef struct shk_kernel_desc {
   int32_t group_size_m;    /* tile-row swizzle width (dense) */
   int32_t operand_format;  /* SHK_OPERANDS_* */
   int32_t schedule;        /* SHK_SCHEDULE_* */
-  int32_t split_k;         /* K slices per output tile (dense); > 1: float32 output that the
-                              slices add into with hardware float atomics, so `out` must hold
-                              zeros and be coarse-grained device memory (hipMalloc, torch's
-                              allocator); the slices add in a run-dependent order, so the last
-                              bits of a result may differ from run to run */
+  int32_t split_k;         /* K slices per output tile (dense); > 1: float32 output.  PACKED
+                              entries add the slices into it with hardware float atomics, so
+                              `out` must hold zeros and be coarse-grained device memory
+                              (hipMalloc, torch's allocator); the slices add in a run-dependent
+                              order, so the last bits of a result may differ from run to run.
+                              STREAM entries compute each output whole (exact int32 sums) and
+                              store it: split_k sets only the K multiple and the output type */
 } shk_kernel_desc;
 
 /* ---- status (reference dispatch.cpp:206-222) ---------------------------- */

@@ -232,7 +232,10 @@ def swiglu(x) -> np.ndarray:
     d = x.shape[-1] // 2
     up = x[..., :d]
     gate = x[..., d:]
-    den = (np.float32(1.0) + np.exp(-gate).astype(np.float32)).astype(np.float32)
+    # exp(-gate) overflows to inf for gates below about -88: the quotient is
+    # then -0 or 0, as torch gives, so the overflow warning is expected
+    with np.errstate(over="ignore"):
+        den = (np.float32(1.0) + np.exp(-gate).astype(np.float32)).astype(np.float32)
     return (up * (gate / den).astype(np.float32)).astype(np.float32)
 
 

@@ -44,6 +44,11 @@ OUT_I32 = 2
 # first (amd_strix_halo_kernels_gemm_workspace_bytes).
 OPERANDS_PACKED = 0
 OPERANDS_FP6 = 1
+# STREAM entries (block_m 16, 32, 64; block_k 32; csrc/shk_skinny.h) read the
+# packed operands directly; per-channel calls split a tile's K over several
+# workgroups when given a workspace whose arrival counters start at zero
+# (every launch leaves them zero): sk_split_count / sk_workspace_bytes.
+OPERANDS_STREAM = 2
 FP6_MAX_K = 262144
 # Largest K of the fp6 entries (32-bit buffer offsets of a tile's panels);
 # per-channel calls with K > FP6_MAX_K run in exact K slices of FP6_MAX_K
@@ -99,9 +104,16 @@ class KernelDesc:
     def needs_workspace(self) -> bool:
         return self.operand_format == OPERANDS_FP6
 
+    @property
+    def is_stream(self) -> bool:
+        return self.operand_format == OPERANDS_STREAM
+
     def workspace_bytes(self, m: int, n: int, k: int) -> int:
-        """Bytes of the operand workspace for shape (m, n, k) (0 for PACKED);
-        per-channel calls with K > FP6_MAX_K add [m, b_cols] int32 sums."""
+        """Bytes of the workspace for shape (m, n, k): fp6 operands (FP6;
+        per-channel calls with K > FP6_MAX_K add [m, b_cols] int32 sums), the
+        split-K counters and partials (STREAM), 0 for PACKED."""
+        if self.is_stream:
+            return sk_workspace_bytes(self, m, n, k)
         if not self.needs_workspace:
             return 0
         b_cols = 2 * n if self.epilogue_kind == EPI_KIND_SWIGLU else n
@@ -116,6 +128,8 @@ class KernelDesc:
         library checks it (capi.hip dense_max_k)."""
         if self.family != FAMILY_DENSE:
             return None
+        if self.is_stream:
+            return FP6_MAX_K_SLICED if (self.dtype_bits == 4 and self.scale_mode == SCALE_PER_CHANNEL) else None
         if self.operand_format == OPERANDS_FP6:
             if self.scale_mode == SCALE_PER_CHANNEL and self.schedule == SCHEDULE_PERSISTENT:
                 return FP6_MAX_K
@@ -150,6 +164,56 @@ class KernelDesc:
 # The 32x32 engines (fp6 per-channel, int8 direct-to-LDS) keep each wave's
 # 256 bytes of B scales in LDS past the stage ring (shk_f6.h).
 MFMA32_SCALE_BYTES = 4 * 256
+
+# Skinny (STREAM) tiles: 4 waves, 64 output columns, wave-private rings of
+# stages of 64 source bytes per row (shk_skinny.h).
+SK_NW = 4
+SK_BN = 64
+SK_TARGET_UNITS = 512
+
+
+def _sk_geometry(r: int, swiglu: bool, subch: bool) -> tuple[int, int]:
+    """(ring depth, LDS bytes) of a skinny tile of r rows (SkCfg)."""
+    bnb = 2 * SK_BN if swiglu else SK_BN
+    wcols = bnb // SK_NW if subch else bnb
+    stage = r * 64 + wcols * 64 + ((r // 16) * 256 + 256 if subch else 0)
+    depth = 4 if SK_NW * 4 * stage <= 79872 else (3 if SK_NW * 3 * stage <= 79872 else 2)
+    ring = SK_NW * depth * stage
+    red = 0 if subch else SK_NW * (wcols // 16) * 1024
+    return depth, max(ring, red)
+
+
+def sk_split_count(desc: "KernelDesc", m: int, n: int, k: int, with_workspace: bool = True) -> int:
+    """Workgroups sharing a skinny per-channel tile's K (shk_table.h
+    sk_split_count): about SK_TARGET_UNITS workgroups with at least two
+    stages per wave, at most 16; for int4 enough to keep every wave within
+    1023 stages of 128 K.  Without a workspace 1, or 0 if K needs a split."""
+    if desc.scale_mode == SCALE_SUBCHANNEL:
+        return 1
+    ks = 128 if desc.dtype_bits == 4 else 64
+    nst = -(-k // ks)
+    need = 1
+    if desc.dtype_bits == 4:
+        while need * 4 * 1023 < nst:
+            need *= 2
+    if not with_workspace:
+        return 1 if need == 1 else 0
+    tiles = (m // desc.block_m) * (n // desc.block_n)
+    s = 1
+    while s * 2 <= 16 and tiles * s * 2 <= SK_TARGET_UNITS and nst >= 16 * s:
+        s *= 2
+    return max(s, need)
+
+
+def sk_workspace_bytes(desc: "KernelDesc", m: int, n: int, k: int) -> int:
+    """Arrival counters (padded to 256 bytes) and exact int32 partials of a
+    split skinny launch; 0 when it runs unsplit (shk_table.h)."""
+    s = sk_split_count(desc, m, n, k, True)
+    if s <= 1:
+        return 0
+    tiles = (m // desc.block_m) * (n // desc.block_n)
+    cf = 2 if desc.epilogue_kind == EPI_KIND_SWIGLU else 1
+    return ((tiles * 4 + 255) & ~255) + tiles * s * 4 * (desc.block_m // 16) * (desc.block_n // 64) * cf * 1024
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,
@@ -199,11 +263,25 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
     )
 
 
+def _sk_desc(index, bits, layout, r, *, swiglu=False, subch=False, schedule=SCHEDULE_STANDARD, split_k=1):
+    depth, lds = _sk_geometry(r, swiglu, subch)
+    return KernelDesc(
+        index=index, family=FAMILY_DENSE, dtype_bits=bits, layout=layout,
+        scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
+        min_subchannel=32 if subch else 0, max_subchannel=256 if subch else 0,
+        epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
+        block_m=r, block_n=SK_BN, block_k=32, num_waves=SK_NW, num_stages=depth, lds_bytes=lds,
+        group_size_m=1, operand_format=OPERANDS_STREAM, schedule=schedule, split_k=split_k)
+
+
 def _build() -> tuple[KernelDesc, ...]:
     out: list[KernelDesc] = []
 
     def add(**kw):
         out.append(_desc(len(out), **kw))
+
+    def add_sk(*args, **kw):
+        out.append(_sk_desc(len(out), *args, **kw))
 
     for bits in (4, 8):
         big_bk = 128 if bits == 4 else 64
@@ -256,6 +334,21 @@ def _build() -> tuple[KernelDesc, ...]:
                 for mk in (64, 32):
                     for split in (2, 4, 8):
                         add(**d, bm=64, bn=64, bk=64, wm=2, wn=2, subch=True, mk=mk, split_k=split)
+    # skinny tiles (k_skinny.hip), per (bits, layout)
+    for bits in (4, 8):
+        for layout in (LAYOUT_NN, LAYOUT_NT, LAYOUT_TN):
+            for r in (16, 32, 64):
+                for swiglu, subch in ((False, False), (True, False), (False, True), (True, True)):
+                    add_sk(bits, layout, r, swiglu=swiglu, subch=subch)
+            if bits == 4:
+                for split in (1, 2, 4, 8):
+                    for r in (16, 32, 64):
+                        for subch in (False, True):
+                            add_sk(bits, layout, r, subch=subch, schedule=SCHEDULE_PERSISTENT, split_k=split)
+            for split in (2, 4, 8):
+                for r in (16, 32, 64):
+                    for subch in (False, True):
+                        add_sk(bits, layout, r, subch=subch, split_k=split)
     return tuple(out)
 
 

@@ -17,6 +17,7 @@ raises otherwise.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import functools
 import threading
@@ -307,21 +308,49 @@ def gemm_workspace_bytes(kernel: KernelMetadata, m: int, n: int, k: int, *, libr
     return int(out.value)
 
 
+_SPLIT_LOCK = threading.Lock()
+_SPLIT_WORKSPACES: dict[tuple[int, int], Any] = {}
+
+
+def _split_workspace(torch, device, stream_handle: int, stream, nbytes: int):
+    """The workspace of the skinny (STREAM) launches on one stream of one
+    device: zero-filled when allocated, on that stream, and left with zero
+    counters by every launch, so launches in stream order share it.  It
+    grows (to a new zero-filled buffer) when a shape needs more."""
+    key = (0 if device.index is None else int(device.index), stream_handle)
+    with _SPLIT_LOCK:
+        buf = _SPLIT_WORKSPACES.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+            ctx = torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+            with ctx:
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _SPLIT_WORKSPACES[key] = buf
+        return buf
+
+
 def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, library_path, stream) -> None:
     lib = _verified_library(library_path)
     sub = kernel.scale.subchannel_size if kernel.scale.mode is ScaleMode.SUBCHANNEL else 0
     # fp6 entries convert both operands into a workspace first; it comes from
     # torch's caching allocator on the launch stream, so a later launch on
-    # the same stream may reuse it.
+    # the same stream may reuse it.  Skinny entries that split K share one
+    # zero-filled workspace per stream (its counters must start at zero).
     # (the table mirror's size, which gemm_workspace_bytes matches)
-    ws_bytes = kt.TABLE[_table_index(kernel)].workspace_bytes(m, n, k)
-    work = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
-    if work is not None and stream is not None:
-        work.record_stream(stream)
+    desc = kt.TABLE[_table_index(kernel)]
+    ws_bytes = desc.workspace_bytes(m, n, k)
+    handle = _stream_handle(torch, a, stream)
+    if desc.is_stream:
+        work = _split_workspace(torch, a.device, handle, stream, ws_bytes) if ws_bytes else None
+        ws_bytes = work.numel() if work is not None else 0
+    else:
+        work = torch.empty(ws_bytes, dtype=torch.uint8, device=a.device) if ws_bytes else None
+        if work is not None and stream is not None:
+            work.record_stream(stream)
     rc = lib.amd_strix_halo_kernels_launch_gemm_ws(
         _table_index(kernel),
         _device_index(a),
-        _stream_handle(torch, a, stream),
+        handle,
         a.data_ptr(),
         b.data_ptr(),
         a_scale.data_ptr(),

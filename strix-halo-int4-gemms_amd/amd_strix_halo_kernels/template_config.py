@@ -8,6 +8,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+from . import kernel_table
 from .metadata import Epilogue, KernelMetadata, OperandDType, ScaleMode
 
 
@@ -39,10 +40,19 @@ def tile_multiple_rejection_reasons(kernel: KernelMetadata, shape: LaunchShape) 
     if kernel.scale.mode is ScaleMode.SUBCHANNEL and sub is not None and shape.k % sub:
         out.append(f"K={shape.k} is not divisible by SUBCHANNEL={sub}")
     elif (kernel.scale.mode is ScaleMode.SUBCHANNEL and sub is not None and tile.split_k > 1
-          and (shape.k // tile.split_k) % sub):
+          and _slices_k(kernel) and (shape.k // tile.split_k) % sub):
         # each K slice of a split-K kernel starts at a scale group boundary
         out.append(f"K/SPLIT_K={shape.k // tile.split_k} is not divisible by SUBCHANNEL={sub}")
     return tuple(out)
+
+
+def _slices_k(kernel: KernelMetadata) -> bool:
+    """Whether a split-K kernel cuts K into SPLIT_K contiguous slices (the
+    gfx950 split tiles); the skinny (STREAM) split tiles fold every scale
+    group of the whole K in one workgroup and need no slice boundary."""
+    if kernel.table_index is None:
+        return True
+    return kernel_table.TABLE[kernel.table_index].operand_format != kernel_table.OPERANDS_STREAM
 
 
 def is_tile_multiple_shape(kernel: KernelMetadata, shape: LaunchShape) -> bool:

@@ -69,6 +69,9 @@ def translation_units() -> list[tuple[str, Path, list[str]]]:
     units.append(("quant", CSRC / "k_quant.hip", []))
     for layout in (0, 1, 2, 3):
         units.append((f"ragged_{layout}", CSRC / "k_ragged.hip", [f"-DSHK_LAYOUT={layout}"]))
+    for bits in (4, 8):
+        for layout in (0, 1, 2):
+            units.append((f"skinny_{bits}_{layout}", CSRC / "k_skinny.hip", [f"-DSHK_BITS={bits}", f"-DSHK_LAYOUT={layout}"]))
     units.append(("capi", CSRC / "capi.hip", []))
     return units
 

@@ -98,6 +98,12 @@ const std::vector<Entry>& table() {
     shk::append_split_8_0(v);
     shk::append_split_8_1(v);
     shk::append_split_8_2(v);
+    shk::append_skinny_4_0(v);
+    shk::append_skinny_4_1(v);
+    shk::append_skinny_4_2(v);
+    shk::append_skinny_8_0(v);
+    shk::append_skinny_8_1(v);
+    shk::append_skinny_8_2(v);
     for (size_t i = 0; i < v.size(); ++i) v[i].d.index = (int32_t)i;
     return v;
   }();
@@ -195,8 +201,11 @@ int check_out_mode(int out_mode) {
 
 // Workspace of a dense entry: both operands in fp6 block format for FP6
 // entries (and for per-channel calls with K > F6_MAX_K, the [m, b_cols]
-// int32 sums of their K slices past the operands), nothing otherwise.
+// int32 sums of their K slices past the operands); for STREAM entries the
+// arrival counters and exact partials of a split K (shk::sk_workspace_bytes);
+// nothing otherwise.
 uint64_t dense_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k) {
+  if (d.operand_format == SHK_OPERANDS_STREAM) return shk::sk_workspace_bytes(d, m, n, k);
   if (d.operand_format != SHK_OPERANDS_FP6) return 0;
   const long b_cols = d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2L * n : (long)n;
   uint64_t bytes = shk::f6_operand_bytes(m, k) + shk::f6_operand_bytes(b_cols, k);
@@ -212,9 +221,13 @@ constexpr int kMaxInt4AccK = 131071;
 
 // Largest K a dense entry runs: fp6 entries up to F6_MAX_K_SLICED, except
 // the persistent per-channel tile, which multiplies whole K in one pass
-// (F6_MAX_K); int4 per-channel entries of the int8 engines kMaxInt4AccK per
-// K slice; no bound otherwise.
+// (F6_MAX_K); int4 per-channel STREAM entries F6_MAX_K_SLICED as well (their
+// x256 int32 sums stay within 1023 stages per wave through the split count);
+// int4 per-channel entries of the int8 engines kMaxInt4AccK per K slice; no
+// bound otherwise.
 long dense_max_k(const shk_kernel_desc& d) {
+  if (d.operand_format == SHK_OPERANDS_STREAM)
+    return (d.dtype_bits == 4 && d.scale_mode == SHK_SCALE_PER_CHANNEL) ? shk::F6_MAX_K_SLICED : 0x7FFFFFFFL;
   if (d.operand_format == SHK_OPERANDS_FP6)
     return (d.scale_mode == SHK_SCALE_PER_CHANNEL && d.schedule == SHK_SCHEDULE_PERSISTENT) ? shk::F6_MAX_K
                                                                                             : shk::F6_MAX_K_SLICED;
@@ -246,6 +259,7 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
   if (lookup(kernel_index, SHK_FAMILY_DENSE, &c.e)) return 1;
   const shk_kernel_desc& d = c.e->d;
   const bool fp6 = d.operand_format == SHK_OPERANDS_FP6;
+  const bool stream = d.operand_format == SHK_OPERANDS_STREAM;
   const bool uses_a = phase == PHASE_ALL || phase == PHASE_CONVERT_A;
   const bool uses_b = phase == PHASE_ALL || phase == PHASE_CONVERT_B;
   const bool gemm = phase == PHASE_ALL || phase == PHASE_GEMM;
@@ -276,7 +290,7 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
     if (!why.empty()) why += "; ";
     why += "K=" + std::to_string(k) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
   }
-  if (split > 1 && d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && (k / split) % subchannel) {
+  if (split > 1 && !stream && d.scale_mode == SHK_SCALE_SUBCHANNEL && subchannel > 0 && (k / split) % subchannel) {
     if (!why.empty()) why += "; ";
     why += "K/SPLIT_K=" + std::to_string(k / split) + " is not divisible by SUBCHANNEL=" + std::to_string(subchannel);
   }
@@ -293,8 +307,8 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
       return fail("epilogue " + std::to_string(epilogue) + " does not match the kernel's epilogue kind");
   }
   if (k > dense_max_k(d)) {
-    if (fp6) return fail("kernel " + std::to_string(kernel_index) + " supports K <= " +
-                         std::to_string(dense_max_k(d)) + "; got " + std::to_string(k));
+    if (fp6 || stream) return fail("kernel " + std::to_string(kernel_index) + " supports K <= " +
+                                   std::to_string(dense_max_k(d)) + "; got " + std::to_string(k));
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK) +
                 (split > 1 ? " per K slice (K/SPLIT_K); got K/SPLIT_K=" + std::to_string(k / split)
                            : "; got " + std::to_string(k)));
@@ -313,6 +327,26 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
       return fail("kernel " + std::to_string(kernel_index) + " converts its operands into a workspace of " +
                   std::to_string(need) + " bytes (amd_strix_halo_kernels_gemm_workspace_bytes)");
     if (!aligned(workspace, 16)) return fail("the workspace must be 16-byte aligned");
+  }
+  if (stream && gemm) {
+    // K split over workgroups only with a (zeroed-counter) workspace
+    const bool with_ws = workspace != nullptr;
+    const uint64_t need = dense_workspace_bytes(d, m, n, k);
+    if (with_ws && workspace != kScratchPending) {
+      if (workspace_bytes < need)
+        return fail("kernel " + std::to_string(kernel_index) + " needs a workspace of " + std::to_string(need) +
+                    " bytes for this shape (amd_strix_halo_kernels_gemm_workspace_bytes)");
+      if (need > 0 && !aligned(workspace, 16)) return fail("the workspace must be 16-byte aligned");
+    } else if (with_ws && need > workspace_bytes) {
+      return fail("kernel " + std::to_string(kernel_index) + " needs " + std::to_string(need) +
+                  " bytes of scratch for this shape; the no-allocation entry point's scratch holds at most " +
+                  std::to_string(workspace_bytes) + " bytes (use amd_strix_halo_kernels_launch_gemm_ws)");
+    }
+    const int splits = shk::sk_split_count(d, m, n, k, with_ws && need > 0);
+    if (splits == 0)
+      return fail("kernel " + std::to_string(kernel_index) + " splits K=" + std::to_string(k) +
+                  " over workgroups, which needs a workspace (amd_strix_halo_kernels_launch_gemm_ws)");
+    c.p.sk_splits = splits;
   }
   if (gemm && (!aligned(out, 16) || !aligned(b_scale, 8) || !aligned(a_scale, 2)))
     return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
@@ -339,7 +373,7 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
   p.out_mode = out_mode;
   // 16-byte pieces for K-major operands and for every operand of the
   // direct-to-LDS and fp6 tiles; 8-byte rows otherwise.
-  const bool dma = d.num_stages > 2 || fp6;
+  const bool dma = d.num_stages > 2 || fp6 || stream;
   const int a_need = (a_km || dma) ? 16 : 8;
   const int b_need = (b_km || dma) ? 16 : 8;
   p.a_aligned = !uses_a || (aligned(a, a_need) && p.lda % a_need == 0);
@@ -347,6 +381,7 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
   p.group_m = d.group_size_m;
   p.layout = d.layout;
   p.work = static_cast<uint8_t*>(workspace);
+  if (stream && p.sk_splits <= 1) p.work = nullptr;
   // Operands are addressed with 32-bit buffer offsets.
   if ((unsigned long long)kbytes * (unsigned long long)m >= (1ull << 32) ||
       (unsigned long long)kbytes * (unsigned long long)b_cols >= (1ull << 32))
@@ -489,7 +524,8 @@ int amd_strix_halo_kernels_launch_gemm_noalloc(int kernel_index, int device_inde
     return 1;
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
-  if (c.e->d.operand_format == SHK_OPERANDS_FP6) {
+  if (c.e->d.operand_format == SHK_OPERANDS_FP6 ||
+      (c.e->d.operand_format == SHK_OPERANDS_STREAM && c.p.sk_splits > 1)) {
     void* ptr = nullptr;
     if (scratch_address(device_index, &ptr)) return 1;
     c.p.work = static_cast<uint8_t*>(ptr);

@@ -74,11 +74,14 @@ __device__ __forceinline__ v4i buffer_words(const void* base, unsigned long long
 // One LDS-DMA load: lane L's 16 bytes at rsrc + voff + soff land at LDS
 // address m0 + 16*L.  The compiler does not know about this write, so the
 // waits for it are explicit (wait_vmcnt) and the asm clobbers memory.
+// The asm opens with the wait states its operands need, which the compiler's
+// hazard recognizer cannot insert because it does not see the load: 1 after
+// the M0 write, and 5 after a VALU write of an SGPR the load reads (the
+// compiler reloads spilled scalars such as the offset with v_readlane_b32,
+// possibly right before the asm).  tests/_asm_check.py scans for the latter.
 __device__ __forceinline__ void lds_dma16(const v4i& rs, uint32_t voff, uint32_t soff, uint32_t m0) {
-  // The compiler sets M0 for the "{m0}" operand; the nop is the wait state
-  // an M0 write needs before an LDS-DMA instruction reads it.
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "buffer_load_dwordx4 %0, %1, %2 offen lds"
       :
       : "v"(voff), "s"(rs), "s"(soff), "{m0}"(m0)
@@ -88,7 +91,7 @@ __device__ __forceinline__ void lds_dma16(const v4i& rs, uint32_t voff, uint32_t
 // The same with 4 bytes per lane: lane L's land at m0 + 4*L.
 __device__ __forceinline__ void lds_dma4(const v4i& rs, uint32_t voff, uint32_t soff, uint32_t m0) {
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "buffer_load_dword %0, %1, %2 offen lds"
       :
       : "v"(voff), "s"(rs), "s"(soff), "{m0}"(m0)

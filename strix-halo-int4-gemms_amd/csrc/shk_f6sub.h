@@ -444,8 +444,9 @@ struct F6SubEngine {
       for (int c = 0; c < OPW; ++c)
         lds_dma16(live ? rs : rs_end, voff[c], live ? (uint32_t)st * PANEL : 0u,
                   lds0 + (uint32_t)st * STAGE + 1024u * (OPW * wave + c));
-      // (the nop: the wait state between the M0 write and the LDS-DMA load)
-      asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+      // (the nops: the wait states after the M0 write and after a VALU write
+      // of the resource's SGPRs, as in lds_dma16)
+      asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds"
                    :
                    : "v"(live ? scale_voff(st / SPG) : 0u), "s"(live ? rss : rss_end), "{m0}"(scale_m0(st / SPG))
                    : "memory");
@@ -800,8 +801,9 @@ struct F6SubEngine64 {
       for (int c = 0; c < OPW; ++c)
         lds_dma16(live ? rs : rs_end, voff[c], live ? (uint32_t)st * F6_BLOCK : 0u,
                   lds0 + (uint32_t)st * STAGE + 1024u * (OPW * wave + c));
-      // (the nop: the wait state between the M0 write and the LDS-DMA load)
-      asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+      // (the nops: the wait states after the M0 write and after a VALU write
+      // of the resource's SGPRs, as in lds_dma16)
+      asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds"
                    :
                    : "v"(live ? scale_voff(st / SPG) : 0u), "s"(live ? rss : rss_end), "{m0}"(scale_m0(st / SPG))
                    : "memory");

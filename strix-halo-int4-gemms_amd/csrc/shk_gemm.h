@@ -371,6 +371,7 @@ struct DenseArgs {
   int layout;        // SHK_LAYOUT_* (read by the fp6 path's operand conversion)
   uint8_t* work;     // fp6 path: caller workspace for the converted operands
   int split_tn;      // int8 256-row tiles: first column tile run as 128-row tiles (0: none)
+  int sk_splits;     // skinny per-channel tiles: workgroups sharing a tile's K (1: none)
 };
 
 // Tile order: workgroups are dispatched round-robin over the 8 XCDs, so the

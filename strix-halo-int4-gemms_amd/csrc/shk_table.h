@@ -253,6 +253,43 @@ Entry bwd_entry(int layout) {
   return Entry{desc_of<C>(SHK_FAMILY_RAGGED_BWD, layout, 1), nullptr, nullptr, &launch_bwd_t<C>, nullptr};
 }
 
+// Skinny entries (SHK_OPERANDS_STREAM, shk_skinny.h).  Workgroups that share
+// a per-channel tile's K: enough to give about kSkTargetUnits workgroups (two
+// per CU of an MI355X) while every wave keeps at least two stages, at most 16;
+// and for int4 at least as many as keep each wave's x256 int32 sum within
+// 1023 stages of 128 K (up to 64 at K = 2^24).  Without a workspace only
+// one, or 0 when K needs more.  Subchannel tiles always use one.
+constexpr int kSkTargetUnits = 512;
+inline int sk_split_count(const shk_kernel_desc& d, long m, long n, long k, bool with_workspace) {
+  if (d.scale_mode == SHK_SCALE_SUBCHANNEL) return 1;
+  const long ks = d.dtype_bits == 4 ? 128 : 64;
+  const long nst = (k + ks - 1) / ks;
+  long need = 1;
+  if (d.dtype_bits == 4)
+    while (need * 4L * 1023L < nst) need *= 2;
+  if (!with_workspace) return need == 1 ? 1 : 0;
+  const long tiles = (m / d.block_m) * (n / d.block_n);
+  long s = 1;
+  while (s * 2 <= 16 && tiles * s * 2 <= kSkTargetUnits && nst >= 16L * s) s *= 2;
+  return (int)(s > need ? s : need);
+}
+// Workspace of a skinny launch with more than one split: the tiles' arrival
+// counters (zero before the first launch, left zero by every launch), padded
+// to 256 bytes, then an exact int32 partial of every (tile, split).
+inline unsigned long long sk_workspace_bytes(const shk_kernel_desc& d, long m, long n, long k) {
+  const int s = sk_split_count(d, m, n, k, true);
+  if (s <= 1) return 0;
+  const long tiles = (m / d.block_m) * (n / d.block_n);
+  const long cf = d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2 : 1;
+  // per (tile, split): 4 waves x (block_m / 16) row tiles x (block_n / 64)
+  // output tiles per wave x (up, gate) x 1 KiB
+  return (unsigned long long)((tiles * 4 + 255) & ~255L) +
+         (unsigned long long)tiles * s * 4 * (d.block_m / 16) * (d.block_n / 64) * cf * 1024;
+}
+inline unsigned long long sk_counter_bytes(const shk_kernel_desc& d, long m, long n) {
+  return (unsigned long long)((((m / d.block_m) * (n / d.block_n)) * 4 + 255) & ~255L);
+}
+
 // Each kernel translation unit appends its entries in a fixed order
 // (append_dense_f6(layout), append_dense_dma_<bits>_<layout>,
 // append_dense_<bits>_<layout>, append_ragged_<layout>).
@@ -285,6 +322,15 @@ void append_split_4_2(std::vector<Entry>& t);
 void append_split_8_0(std::vector<Entry>& t);
 void append_split_8_1(std::vector<Entry>& t);
 void append_split_8_2(std::vector<Entry>& t);
+// Skinny entries per (bits, layout) (k_skinny.hip): for block_m 16, 32, 64
+// the per-channel and subchannel tiles, plain and SwiGLU; for int4 the
+// persistent plain tiles, split-K 1/2/4/8; then split-K 2/4/8 plain tiles.
+void append_skinny_4_0(std::vector<Entry>& t);
+void append_skinny_4_1(std::vector<Entry>& t);
+void append_skinny_4_2(std::vector<Entry>& t);
+void append_skinny_8_0(std::vector<Entry>& t);
+void append_skinny_8_1(std::vector<Entry>& t);
+void append_skinny_8_2(std::vector<Entry>& t);
 void append_ragged_0(std::vector<Entry>& t);
 void append_ragged_1(std::vector<Entry>& t);
 void append_ragged_2(std::vector<Entry>& t);

@@ -234,3 +234,134 @@ def inflight_lds_hazards(asm: str) -> list[str]:
     if fn is not None:
         found += _function_hazards(fn, lines)
     return found
+
+
+# ---------------------------------------------------------------------------
+# SGPR operands of asm vector-memory instructions.  A VALU instruction that
+# writes an SGPR (v_readlane_b32 / v_readfirstlane_b32 reloading a spilled
+# scalar, a v_cmp mask) needs VALU_SGPR_VMEM_WAIT_STATES before a VMEM
+# instruction reads that SGPR as its resource, offset or (LDS-DMA) M0.  The
+# compiler inserts them for its own VMEM instructions but cannot see the
+# operands of inline asm, so an asm load must carry them itself.
+
+VALU_SGPR_VMEM_WAIT_STATES = 5
+_SRANGE = re.compile(r"s\[(\d+):(\d+)\]$")
+_SREG = re.compile(r"s(\d+)$")
+_VCC = {106, 107}
+_M0 = 124
+
+
+def _sgprs(spec: str) -> set[int]:
+    m = _SRANGE.match(spec)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = _SREG.match(spec)
+    if m:
+        return {int(m.group(1))}
+    if spec in ("vcc", "vcc_lo", "vcc_hi"):
+        return set(_VCC)
+    if spec == "m0":
+        return {_M0}
+    return set()
+
+
+def _valu_sgpr_writes(op: str, ops: list[str]) -> set[int]:
+    if not op.startswith("v_") or not ops:
+        return set()
+    out = _sgprs(ops[0])
+    if "_co_" in op and len(ops) > 1:
+        out |= _sgprs(ops[1])
+    if op.endswith("_e32") and (op.startswith("v_cmp") or "_co_" in op):
+        out |= _VCC
+    return out
+
+
+def _vmem_sgpr_reads(op: str, ops: list[str], line: str) -> set[int]:
+    if not op.startswith(("buffer_", "global_", "scratch_")):
+        return set()
+    out: set[int] = set()
+    for o in ops:
+        out |= _sgprs(o)
+    if " lds" in line:
+        out.add(_M0)
+    return out
+
+
+def _sgpr_function_hazards(fn: str, lines: list[tuple[int, str, bool]]) -> list[str]:
+    blocks = _blocks(lines)
+    index = {lab: i for i, (lab, _, _, _) in enumerate(blocks) if lab is not None}
+    succ = []
+    for i, (_, _, targets, falls) in enumerate(blocks):
+        out = [index[t] for t in targets if t in index]
+        if falls and i + 1 < len(blocks):
+            out.append(i + 1)
+        succ.append(out)
+
+    def step(state, no, s, in_asm, found):
+        op, ops = _operands(s)
+        if found is not None and in_asm:
+            for r in sorted(_vmem_sgpr_reads(op, ops, s)):
+                if r in state and state[r][1] < VALU_SGPR_VMEM_WAIT_STATES:
+                    found.append(f"{fn}: line {no} '{s}' reads s{r} {state[r][1]} wait states after the VALU "
+                                 f"write at line {state[r][0]}")
+                    break
+        nop = _NOP.match(s)
+        ws = int(nop.group(1)) + 1 if nop else 1
+        state = {r: (l, w + ws) for r, (l, w) in state.items() if w + ws < VALU_SGPR_VMEM_WAIT_STATES}
+        for r in _valu_sgpr_writes(op, ops):
+            state[r] = (no, 0)
+        return state
+
+    entry: list[dict | None] = [None] * len(blocks)
+    entry[0] = {}
+    work = [0]
+    while work:
+        i = work.pop()
+        st = entry[i]
+        for no, s, in_asm in blocks[i][1]:
+            st = step(st, no, s, in_asm, None)
+        for j in succ[i]:
+            merged = dict(entry[j] or {})
+            for r, (l, w) in st.items():
+                if r not in merged or w < merged[r][1]:
+                    merged[r] = (l, w)
+            if entry[j] is None or merged != entry[j]:
+                entry[j] = merged
+                work.append(j)
+    found: list[str] = []
+    for i, blk in enumerate(blocks):
+        if entry[i] is None:
+            continue
+        st = entry[i]
+        for no, s, in_asm in blk[1]:
+            st = step(st, no, s, in_asm, found)
+    return found
+
+
+def sgpr_vmem_hazards(asm: str) -> list[str]:
+    """Asm vector-memory instructions that read an SGPR (or M0) fewer than
+    VALU_SGPR_VMEM_WAIT_STATES after a VALU instruction wrote it, on some
+    path."""
+    found: list[str] = []
+    fn, lines, in_asm = None, [], False
+    for no, raw in enumerate(asm.splitlines(), 1):
+        s = raw.strip()
+        if re.match(r"^_Z\S+:", s):
+            if fn is not None:
+                found += _sgpr_function_hazards(fn, lines)
+            fn, lines, in_asm = s.split(":")[0], [], False
+            continue
+        if fn is None:
+            continue
+        if s.startswith(";;#ASMSTART"):
+            in_asm = True
+            continue
+        if s.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
+        if not s or s.startswith(";") or (s.startswith(".") and not _LABEL.match(s)):
+            continue
+        lines.append((no, s, in_asm))
+    if fn is not None:
+        found += _sgpr_function_hazards(fn, lines)
+    return found

@@ -51,6 +51,7 @@ def test_split_entries_cover_the_reference_families():
             assert (shk.OperandDType.INT4, shk.ScaleMode.PER_CHANNEL, layout, split) in fams
             assert (shk.OperandDType.INT4, shk.ScaleMode.SUBCHANNEL, layout, split) in fams
             assert (shk.OperandDType.INT8, shk.ScaleMode.PER_CHANNEL, layout, split) in fams
+            assert (shk.OperandDType.INT8, shk.ScaleMode.SUBCHANNEL, layout, split) in fams
     assert all(k.output_dtype == "float32" and k.epilogue is shk.Epilogue.NONE for k in _SPLIT)
 
 

@@ -88,7 +88,10 @@ def test_select_raises_for_shapes_no_kernel_accepts():
                                     m=100, n=64, k=64)
     with pytest.raises(LookupError):
         shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=PC, epilogue=shk.Epilogue.NONE,
-                                    m=64, n=64, k=64, schedule=shk.KernelSchedule.PERSISTENT)
+                                    m=24, n=64, k=64, schedule=shk.KernelSchedule.PERSISTENT)
+    with pytest.raises(LookupError):  # K a multiple of 32 only
+        shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=PC, epilogue=shk.Epilogue.NONE,
+                                    m=16, n=64, k=48)
 
 
 def test_select_knows_each_entry_k_bound():
@@ -111,9 +114,14 @@ def test_select_knows_each_entry_k_bound():
     with pytest.raises(LookupError):
         shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256, n=256,
                                     k=kt.FP6_MAX_K_SLICED + 128)
+    # the persistent fp6 tile multiplies K <= 262144 in one pass; the skinny
+    # persistent tiles take longer K (split over workgroups), up to 2^24
+    kern = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256,
+                                       n=256, k=524288, schedule=shk.KernelSchedule.PERSISTENT)
+    assert kt.TABLE[kern.table_index].operand_format == kt.OPERANDS_STREAM
     with pytest.raises(LookupError):
         shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256, n=256,
-                                    k=524288, schedule=shk.KernelSchedule.PERSISTENT)
+                                    k=kt.FP6_MAX_K_SLICED + 128, schedule=shk.KernelSchedule.PERSISTENT)
     assert not shk.kernel_supports_shape(
         next(k for k in shk.default_registry.all() if k.table_index is not None
              and kt.TABLE[k.table_index].max_k == kt.INT4_ACC_MAX_K), m=256, n=256, k=262144)
