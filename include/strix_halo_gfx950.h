@@ -81,10 +81,11 @@ extern "C" {
  * straight from HBM like PACKED ones.  Per-channel calls may split a tile's
  * K over several workgroups that add exact int32 partials; they do so only
  * with a workspace of amd_strix_halo_kernels_gemm_workspace_bytes() bytes
- * (0 when the shape needs no split), whose leading arrival counters must be
- * zero before the first launch that uses it and are left zero by every
- * completed launch, so a zero-filled workspace can be reused by launches in
- * stream order (not by launches that overlap in time).  Without a
+ * (0 when the shape needs no split), which must be zero before the first
+ * launch that uses it; every completed launch leaves all of it that it used
+ * zero (arrival counters and partials alike), so a zero-filled workspace can
+ * be reused by launches of any shape in stream order (not by launches that
+ * overlap in time).  Without a
  * workspace (amd_strix_halo_kernels_launch_gemm) the tile's K stays in one
  * workgroup, which limits int4 per-channel calls to K <= 523776.  Results
  * are identical either way. */
@@ -218,16 +219,21 @@ int amd_strix_halo_kernels_launch_gemm_ws(int kernel_index, int device_index, ui
  * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
  * the reference.  FP6 entries convert their operands into the library's own
  * static scratch array of SHK_NOALLOC_SCRATCH_BYTES on `device_index`
- * instead of a caller workspace; PACKED entries need none and run as
- * amd_strix_halo_kernels_launch_gemm.  The call allocates and frees nothing
- * (its first call on a device looks the array's address up once).  Shapes
- * whose workspace (amd_strix_halo_kernels_gemm_workspace_bytes) exceeds
+ * instead of a caller workspace; STREAM entries that split K keep their
+ * arrival counters and partials there and clear the counters with a small
+ * kernel on `stream` before the GEMM (two launches); PACKED entries need
+ * none and run as amd_strix_halo_kernels_launch_gemm.  The array is reserved
+ * on every device where the library's code object is loaded, whether or not
+ * this entry point is called.  The call allocates and frees nothing (its
+ * first call on a device looks the array's address up once).  Shapes whose
+ * workspace (amd_strix_halo_kernels_gemm_workspace_bytes) exceeds
  * SHK_NOALLOC_SCRATCH_BYTES are rejected with rc 1.  Every call on a device
- * shares that device's array: the conversion rewrites every byte the GEMM
- * reads, so no state carries over from an earlier call, but calls that
- * overlap in time on one device (different streams, or threads without
- * stream ordering) race on the array and give undefined results.  Same
- * arguments, validation and errors as amd_strix_halo_kernels_launch_gemm. */
+ * shares that device's array: the conversion (or the counter clear and the
+ * partial stores) rewrites every byte the GEMM reads before it reads it, so
+ * no state carries over from an earlier call, but calls that overlap in time
+ * on one device (different streams, or threads without stream ordering) race
+ * on the array and give undefined results.  Same arguments, validation and
+ * errors as amd_strix_halo_kernels_launch_gemm. */
 int amd_strix_halo_kernels_launch_gemm_noalloc(int kernel_index, int device_index, uintptr_t stream,
                                                const void* a, const void* b, const void* a_scale,
                                                const void* b_scale, void* out, int32_t m, int32_t n,

@@ -46,8 +46,8 @@ OPERANDS_PACKED = 0
 OPERANDS_FP6 = 1
 # STREAM entries (block_m 16, 32, 64; block_k 32; csrc/shk_skinny.h) read the
 # packed operands directly; per-channel calls split a tile's K over several
-# workgroups when given a workspace whose arrival counters start at zero
-# (every launch leaves them zero): sk_split_count / sk_workspace_bytes.
+# workgroups when given a zero-filled workspace (every launch leaves what it
+# used zero, counters and partials): sk_split_count / sk_workspace_bytes.
 OPERANDS_STREAM = 2
 FP6_MAX_K = 262144
 # Largest K of the fp6 entries (32-bit buffer offsets of a tile's panels);
@@ -169,7 +169,7 @@ MFMA32_SCALE_BYTES = 4 * 256
 # stages of 64 source bytes per row (shk_skinny.h).
 SK_NW = 4
 SK_BN = 64
-SK_TARGET_UNITS = 512
+SK_TARGET_UNITS = 256
 
 
 def _sk_geometry(r: int, swiglu: bool, subch: bool) -> tuple[int, int]:
@@ -213,7 +213,7 @@ def sk_workspace_bytes(desc: "KernelDesc", m: int, n: int, k: int) -> int:
         return 0
     tiles = (m // desc.block_m) * (n // desc.block_n)
     cf = 2 if desc.epilogue_kind == EPI_KIND_SWIGLU else 1
-    return ((tiles * 4 + 255) & ~255) + tiles * s * 4 * (desc.block_m // 16) * (desc.block_n // 64) * cf * 1024
+    return ((tiles * 4 + 255) & ~255) + tiles * s * (desc.block_n // 16) * (desc.block_m // 16) * cf * 1024
 
 
 def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subch=False, mk=64, group_m=8, pipe=0,

@@ -314,9 +314,10 @@ _SPLIT_WORKSPACES: dict[tuple[int, int], Any] = {}
 
 def _split_workspace(torch, device, stream_handle: int, stream, nbytes: int):
     """The workspace of the skinny (STREAM) launches on one stream of one
-    device: zero-filled when allocated, on that stream, and left with zero
-    counters by every launch, so launches in stream order share it.  It
-    grows (to a new zero-filled buffer) when a shape needs more."""
+    device: zero-filled when allocated, on that stream, and left zero by
+    every launch (counters and partials), so launches of any shape in stream
+    order share it.  It grows (to a new zero-filled buffer) when a shape
+    needs more."""
     key = (0 if device.index is None else int(device.index), stream_handle)
     with _SPLIT_LOCK:
         buf = _SPLIT_WORKSPACES.get(key)
@@ -335,7 +336,7 @@ def _gemm_call(torch, a, b, a_scale, b_scale, out, kernel, m, n, k, out_mode, li
     # fp6 entries convert both operands into a workspace first; it comes from
     # torch's caching allocator on the launch stream, so a later launch on
     # the same stream may reuse it.  Skinny entries that split K share one
-    # zero-filled workspace per stream (its counters must start at zero).
+    # zero-filled workspace per stream (it must be zero where a launch uses it).
     # (the table mirror's size, which gemm_workspace_bytes matches)
     desc = kt.TABLE[_table_index(kernel)]
     ws_bytes = desc.workspace_bytes(m, n, k)

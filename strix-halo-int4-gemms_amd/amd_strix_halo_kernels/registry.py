@@ -132,6 +132,11 @@ def _runs_k(kernel: KernelMetadata, k: int) -> bool:
 class KernelRegistry:
     def __init__(self, kernels: Iterable[KernelMetadata] = ()) -> None:
         self._kernels: dict[str, KernelMetadata] = {}
+        # Selections are memoized per request (mm() selects on every call, and
+        # a scan of the table costs hundreds of microseconds); the candidates
+        # are indexed by family.  register() clears both.
+        self._families: dict[tuple, list[KernelMetadata]] | None = None
+        self._selected: dict[tuple, KernelMetadata] = {}
         for kernel in kernels:
             self.register(kernel)
 
@@ -139,6 +144,19 @@ class KernelRegistry:
         if kernel.kernel_id in self._kernels:
             raise ValueError(f"duplicate kernel id: {kernel.kernel_id}")
         self._kernels[kernel.kernel_id] = kernel
+        self._families = None
+        self._selected = {}
+
+    def _family(self, dtype, scale, epilogue, layout, schedule) -> list[KernelMetadata]:
+        families = self._families
+        if families is None:
+            families = {}
+            for kern in self._kernels.values():
+                if kern.a_dtype is kern.b_dtype:
+                    key = (kern.a_dtype, kern.scale, kern.epilogue, kern.layout, kern.schedule)
+                    families.setdefault(key, []).append(kern)
+            self._families = families
+        return families.get((dtype, scale, epilogue, layout, schedule), [])
 
     def get(self, kernel_id: str) -> KernelMetadata:
         return self._kernels[kernel_id]
@@ -160,10 +178,14 @@ class KernelRegistry:
         schedule: KernelSchedule = KernelSchedule.STANDARD,
         require_compiled: bool = False,
     ) -> KernelMetadata:
+        request = (dtype, scale, epilogue, m, n, k, layout, split_k, schedule, require_compiled)
+        hit = self._selected.get(request)
+        if hit is not None:
+            return hit
         shape = LaunchShape(m, n, k)
         candidates = [
             kernel
-            for kernel in self._kernels.values()
+            for kernel in self._family(dtype, scale, epilogue, layout, schedule)
             if _matches(kernel, dtype, scale, epilogue, layout, schedule, split_k)
             and is_tile_multiple_shape(kernel, shape)
             and _runs_k(kernel, k)
@@ -175,7 +197,11 @@ class KernelRegistry:
                 f"no kernel for dtype={dtype.value}, scale={scale.label}, epilogue={epilogue.value}, "
                 f"layout={layout.value}, schedule={schedule.value}, shape=({m}, {n}, {k})"
             )
-        return max(candidates, key=_selection_key)
+        chosen = max(candidates, key=_selection_key)
+        if len(self._selected) >= 4096:  # bounded for callers that vary M call to call
+            self._selected = {}
+        self._selected[request] = chosen
+        return chosen
 
     def select_reference(
         self,
@@ -189,7 +215,7 @@ class KernelRegistry:
     ) -> KernelMetadata:
         candidates = [
             kernel
-            for kernel in self._kernels.values()
+            for kernel in self._family(dtype, scale, epilogue, layout, schedule)
             if _matches(kernel, dtype, scale, epilogue, layout, schedule, split_k)
         ]
         if not candidates:

@@ -45,6 +45,15 @@ hipError_t persistent_grid(const void* kernel, int block, unsigned tiles, unsign
   return hipSuccess;
 }
 
+// Clears n16 16-byte units at p: the arrival counters of a split skinny
+// launch on the no-allocation path, whose scratch the fp6 conversions of
+// other calls may have left dirty.  A kernel, not a memset, so that a graph
+// capture records an ordinary kernel node.
+__global__ __launch_bounds__(256) void clear_counters_kernel(int4* p, unsigned n16) {
+  const unsigned i = blockIdx.x * 256u + threadIdx.x;
+  if (i < n16) p[i] = make_int4(0, 0, 0, 0);
+}
+
 }  // namespace shk
 
 namespace {
@@ -524,16 +533,26 @@ int amd_strix_halo_kernels_launch_gemm_noalloc(int kernel_index, int device_inde
     return 1;
   DeviceGuard guard(device_index);
   if (guard.error() != hipSuccess) return fail_hip("hipSetDevice", guard.error());
-  if (c.e->d.operand_format == SHK_OPERANDS_FP6 ||
-      (c.e->d.operand_format == SHK_OPERANDS_STREAM && c.p.sk_splits > 1)) {
+  const bool split_stream = c.e->d.operand_format == SHK_OPERANDS_STREAM && c.p.sk_splits > 1;
+  if (c.e->d.operand_format == SHK_OPERANDS_FP6 || split_stream) {
     void* ptr = nullptr;
     if (scratch_address(device_index, &ptr)) return 1;
     c.p.work = static_cast<uint8_t*>(ptr);
   } else {
     c.p.work = nullptr;
   }
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (split_stream) {
+    // the partial slots are written before they are read; only the counters
+    // must start at zero (256-byte multiple, below the scratch size)
+    const unsigned n16 = (unsigned)(shk::sk_counter_bytes(c.e->d, m, n) / 16);
+    hipLaunchKernelGGL(shk::clear_counters_kernel, dim3((n16 + 255) / 256), dim3(256), 0, s,
+                       reinterpret_cast<int4*>(c.p.work), n16);
+    const hipError_t cerr = hipGetLastError();
+    if (cerr != hipSuccess) return fail_hip("kernel launch", cerr);
+  }
   const unsigned split = c.e->d.split_k > 1 ? (unsigned)c.e->d.split_k : 1u;
-  const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles, split), reinterpret_cast<hipStream_t>(stream));
+  const hipError_t err = c.e->dense(c.p, dim3((unsigned)c.tiles, split), s);
   if (err != hipSuccess) return fail_hip("kernel launch", err);
   return 0;
 }

@@ -31,8 +31,10 @@
 //    workgroup's reads use device-scope (sc1) accesses, which stay coherent
 //    across the XCDs' L2 caches without a cache writeback; each workgroup
 //    waits for its partial stores to complete before it counts itself.  The
-//    counters must be zero before a launch and every launch leaves them
-//    zero.
+//    workspace must be zero before the first launch, and every launch
+//    leaves all of it that it used zero (the last workgroup clears the
+//    tile's slots and counter), since the counters of one shape can lie
+//    where the partials of another were.
 //  * Subchannel scales: each group's partial must be scaled and folded into
 //    the fp32 total in group order, so the waves split the columns (WOUT =
 //    16) and every wave folds its groups in order, with the group scales
@@ -62,22 +64,25 @@
 
 namespace shk {
 
-constexpr int SK_NW = 4;        // waves per workgroup
-constexpr int SK_BN = 64;       // output columns per tile
+constexpr int SK_NW = 4;        // waves per workgroup of the subchannel and wide per-channel tiles
+constexpr int SK_BN = 64;       // output columns per K-split tile
 // An int4 wave accumulates 256 * sum(a*b) in int32: |256 * 64 * K| < 2^31
 // for K below 131072, i.e. at most 1023 stages of 128 K per wave and split.
 constexpr int SK_MAX_WAVE_STAGES_I4 = 1023;
 
-// Ring depth: the deepest of 4, 3, 2 stage slots whose rings (four waves)
-// fit in 78 KiB, so two workgroups share a CU where the tile allows.
+// Ring depth: the deepest of 4, 3, 2 stage slots whose rings fit the LDS
+// budget: 78 KiB for four waves (two workgroups share a CU where the tile
+// allows), 150 KiB for eight or more (one workgroup per CU).
 constexpr int sk_stage_bytes(int r, int wcols, bool subch) {
   return r * 64 + wcols * 64 + (subch ? (r / 16) * 256 + 256 : 0);
 }
-constexpr int sk_ring_depth(int stage) {
-  return SK_NW * 4 * stage <= 79872 ? 4 : (SK_NW * 3 * stage <= 79872 ? 3 : 2);
+constexpr int sk_ring_depth(int stage, int nw) {
+  const int budget = nw >= 8 ? 153600 : 79872;
+  return nw * 4 * stage <= budget ? 4 : (nw * 3 * stage <= budget ? 3 : 2);
 }
 
-template <int BITS_, int LAYOUT_, int R_, bool SWIGLU_, bool SUBCH_, int WOUT_ = SUBCH_ ? 16 : 0, int DEPTH_ = 0>
+template <int BITS_, int LAYOUT_, int R_, bool SWIGLU_, bool SUBCH_, int WOUT_ = SUBCH_ ? 16 : 0, int NW_ = SK_NW,
+          int BNK_ = SK_BN, int DEPTH_ = 0>
 struct SkCfg {
   static constexpr int BITS = BITS_;
   static constexpr int LAYOUT = LAYOUT_;
@@ -87,15 +92,16 @@ struct SkCfg {
   static constexpr int RT = R / 16;
   static constexpr bool SWIGLU = SWIGLU_;
   static constexpr bool SUBCH = SUBCH_;
-  static constexpr int NW = SK_NW;
+  static constexpr int NW = NW_;
   static constexpr int NT = 64 * NW;
   static constexpr int WOUT = WOUT_;                  // output columns per wave (0: waves split K)
   static constexpr bool KSPLIT = WOUT == 0;
-  static constexpr int BN = KSPLIT ? SK_BN : NW * WOUT;  // output columns of a tile
+  static constexpr int BN = KSPLIT ? BNK_ : NW * WOUT;  // output columns of a tile
   static constexpr int BNB = SWIGLU ? 2 * BN : BN;    // B columns of a tile ([up | gate] for SwiGLU)
   static constexpr int WCOLS = KSPLIT ? BNB : BNB / NW;  // B columns a wave loads and multiplies
   static constexpr int CT = WCOLS / 16;              // 16-column B tiles of a wave
   static constexpr int FT = KSPLIT ? 1 : WOUT / 16;   // 16-column output tiles a wave writes
+  static constexpr int NFIN = KSPLIT ? BN / 16 : NW;  // waves that write output (K-split: one tile each)
   static constexpr int CF = SWIGLU ? 2 : 1;          // up (and gate)
   static constexpr int FC = FT * CF;                 // int32 tiles a wave holds after the K sum
   static constexpr int KS = BITS == 4 ? 128 : 64;    // K per stage
@@ -108,7 +114,7 @@ struct SkCfg {
   static constexpr int A_DMA = A_BYTES / 1024;
   static constexpr int B_DMA = B_BYTES / 1024;
   static constexpr int DPS = A_DMA + B_DMA + (SUBCH ? RT + 1 : 0);  // DMA loads per stage
-  static constexpr int D = DEPTH_ > 0 ? DEPTH_ : sk_ring_depth(STAGE);
+  static constexpr int D = DEPTH_ > 0 ? DEPTH_ : sk_ring_depth(STAGE, NW);
   static constexpr int RING = NW * D * STAGE;
   static constexpr int RED = KSPLIT ? NW * CT * 1024 : 0;  // one row tile of the cross-wave sum
   static constexpr int LDS_BYTES = RING > RED ? RING : RED;
@@ -117,7 +123,8 @@ struct SkCfg {
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole DMA blocks per stage");
   static_assert((D - 1) * DPS < 64, "vmcnt range");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-  static_assert(!KSPLIT || CT == CF * NW, "each wave of a K-split tile finalizes one output column tile");
+  static_assert(!KSPLIT || NFIN <= NW, "a K-split tile has a wave for each output column tile");
+  static_assert(!KSPLIT || BN == 32 || BN == 64, "K-split tiles are 32 or 64 columns wide");
   static_assert(!SUBCH || WOUT == 16, "subchannel tiles give each wave 16 output columns");
   static_assert(KSPLIT || WOUT % 16 == 0, "whole 16-column tiles per wave");
 };
@@ -341,6 +348,31 @@ __device__ __forceinline__ void sk_wait(bool full) {
 // bit SC1 = 16 of the buffer intrinsics on gfx950).
 constexpr int SK_SC1 = 16;
 
+// The epilogue scales of a finalizer wave, loaded before its K loop so that
+// their latency passes under it: a_scale of its RT rows, b_scale of the
+// four columns n..n+3 of each output tile (up, and gate for SwiGLU).
+template <class C>
+struct SkScales {
+  float sa[C::RT];
+  float sbu[C::FT][4], sbg[C::FT][4];
+  __device__ __forceinline__ void load(const DenseArgs& p, int m0, int n0, int wave, int lane) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int rt = 0; rt < C::RT; ++rt) sa[rt] = load_bf16(p.a_scale + m0 + 16 * rt + (lane & 15));
+#pragma unroll
+    for (int f = 0; f < C::FT; ++f) {
+      const int n = n0 + (C::KSPLIT ? 16 * wave : C::WOUT * wave + 16 * f) + 4 * g;
+      sk_bf16x4(*reinterpret_cast<const uint2*>(p.b_scale + n), sbu[f]);
+      if constexpr (C::SWIGLU) {
+        sk_bf16x4(*reinterpret_cast<const uint2*>(p.b_scale + p.N + n), sbg[f]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sbg[f][q] = 0.0f;
+      }
+    }
+  }
+};
+
 template <class C>
 __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, int* last_flag, int lane, int wave,
                                            int tm, int tn, int split, int splits, int tile) {
@@ -359,9 +391,12 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
     for (int c = 0; c < C::CT; ++c) acc[rt][c] = v4i{0, 0, 0, 0};
 
   const int g = lane >> 4;
+  // the first stages' loads go out before anything else waits on memory
 #pragma unroll
   for (int i = 0; i < C::D - 1; ++i)
     if (i < mine) e.issue(lo + first + i * stride, i);
+  SkScales<C> scl;
+  if (p.out_mode != OUT_I32 && wave < C::NFIN) scl.load(p, e.m0, e.n0, wave, lane);
   for (int i = 0; i < mine; ++i) {
     const bool ahead = i + C::D - 1 < mine;
     if (ahead) {
@@ -391,8 +426,9 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
   wait_vmcnt<0>();
 
   // fin[rt][fc]: fc = f (up of output tile f) or FT + f (its gate).  K-split
-  // waves add their sums through LDS, one row tile at a time, and wave w
-  // keeps output tile w: B tiles w (up) and C::BN / 16 + w (gate).
+  // waves add their sums through LDS, one row tile at a time, and wave
+  // w < NFIN keeps output tile w: B tiles w (up) and C::BN / 16 + w (gate).
+  const bool finalizer = wave < C::NFIN;
   v4i fin[C::RT][C::FC];
   if constexpr (C::KSPLIT) {
 #pragma unroll
@@ -407,10 +443,12 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
       __syncthreads();
 #pragma unroll
       for (int cf = 0; cf < C::CF; ++cf) {
-        const int c = cf * C::NW + wave;
+        const int c = cf * C::NFIN + (finalizer ? wave : 0);
         v4i s = v4i{0, 0, 0, 0};
+        if (finalizer) {
 #pragma unroll
-        for (int w = 0; w < C::NW; ++w) s += sk_ld128(smem + 16 * ((w * C::CT + c) * 64 + lane));
+          for (int w = 0; w < C::NW; ++w) s += sk_ld128(smem + 16 * ((w * C::CT + c) * 64 + lane));
+        }
         fin[rt][cf] = s;
       }
     }
@@ -426,29 +464,31 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
 
   if (splits > 1) {
     // exact int32 partials: slot (tile, split) of the workspace after the
-    // counters; wave w's part is RT x FC tiles of 64 lanes x 16 bytes
+    // counters; finalizer wave w's part is RT x FC tiles of 64 lanes x 16 bytes
     int* counters = reinterpret_cast<int*>(p.work);
     const long counter_bytes = ((long)(p.M / C::R) * (p.N / C::BN) * 4 + 255) & ~255L;
     constexpr long WAVE_BYTES = (long)C::RT * C::FC * 1024;
-    constexpr long SLOT_BYTES = C::NW * WAVE_BYTES;
+    constexpr long SLOT_BYTES = C::NFIN * WAVE_BYTES;
     const uint8_t* parts = p.work + counter_bytes;
     const long ws_bytes = counter_bytes + ((long)(p.M / C::R) * (p.N / C::BN)) * splits * SLOT_BYTES;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(parts), 0, (int)(ws_bytes - counter_bytes), 0x00020000);
     const uint32_t mine_off = (uint32_t)(((long)tile * splits + split) * SLOT_BYTES + wave * WAVE_BYTES);
+    if (finalizer) {
 #pragma unroll
-    for (int rt = 0; rt < C::RT; ++rt)
+      for (int rt = 0; rt < C::RT; ++rt)
 #pragma unroll
-      for (int fc = 0; fc < C::FC; ++fc)
-        __builtin_amdgcn_raw_buffer_store_b128(fin[rt][fc], rs, mine_off + ((rt * C::FC + fc) * 64 + lane) * 16u, 0,
-                                               SK_SC1);
+        for (int fc = 0; fc < C::FC; ++fc)
+          __builtin_amdgcn_raw_buffer_store_b128(fin[rt][fc], rs, mine_off + ((rt * C::FC + fc) * 64 + lane) * 16u, 0,
+                                                 SK_SC1);
+    }
     wait_vmcnt<0>();  // the partial has reached the device-coherent level
     __syncthreads();
     if (threadIdx.x == 0)
       *last_flag = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                    splits - 1;
     __syncthreads();
-    if (!*last_flag) return;
+    if (!*last_flag || !finalizer) return;
     for (int s2 = 0; s2 < splits; ++s2) {
       if (s2 == split) continue;
       const uint32_t off = (uint32_t)(((long)tile * splits + s2) * SLOT_BYTES + wave * WAVE_BYTES);
@@ -459,24 +499,34 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
           fin[rt][fc] += __builtin_amdgcn_raw_buffer_load_b128(rs, off + ((rt * C::FC + fc) * 64 + lane) * 16u, 0,
                                                                SK_SC1);
     }
+    // Every slot of the tile goes back to zero, and so does its counter: a
+    // later launch of another shape may place its counters over this
+    // launch's partials, so a launch leaves all the workspace it used zero.
+    for (int s2 = 0; s2 < splits; ++s2) {
+      const uint32_t off = (uint32_t)(((long)tile * splits + s2) * SLOT_BYTES + wave * WAVE_BYTES);
+#pragma unroll
+      for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+        for (int fc = 0; fc < C::FC; ++fc)
+          __builtin_amdgcn_raw_buffer_store_b128(v4i{0, 0, 0, 0}, rs, off + ((rt * C::FC + fc) * 64 + lane) * 16u, 0,
+                                                 SK_SC1);
+    }
     if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  if (!finalizer) return;
   // Epilogue: (float(sum) * a_scale[m]) * b_scale[n], then ReLU2 / SwiGLU.
 #pragma unroll
   for (int f = 0; f < C::FT; ++f) {
     const int n = e.n0 + (C::KSPLIT ? 16 * wave : C::WOUT * wave + 16 * f) + 4 * g;
-    float sbu[4], sbg[4];
-    if (p.out_mode != OUT_I32) {
-      sk_bf16x4(*reinterpret_cast<const uint2*>(p.b_scale + n), sbu);
-      if constexpr (C::SWIGLU) sk_bf16x4(*reinterpret_cast<const uint2*>(p.b_scale + p.N + n), sbg);
-    }
+    const float(&sbu)[4] = scl.sbu[f];
+    const float(&sbg)[4] = scl.sbg[f];
 #pragma unroll
     for (int rt = 0; rt < C::RT; ++rt) {
       const int m = e.m0 + 16 * rt + (lane & 15);
       float up[4], gt[4];
       int iu[4], ig[4];
-      const float sa = p.out_mode != OUT_I32 ? load_bf16(p.a_scale + m) : 0.0f;
+      const float sa = scl.sa[rt];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         iu[q] = fin[rt][f][q];
@@ -635,7 +685,7 @@ __device__ __forceinline__ void sk_unit_sc(const DenseArgs& p, uint8_t* smem, in
 // tile, row tile) with the row tile fastest, so the workgroups reading the
 // same B columns run together on one XCD.
 template <class C>
-__global__ __launch_bounds__(256) void sk_gemm_kernel(const DenseArgs p) {
+__global__ __launch_bounds__(C::NT) void sk_gemm_kernel(const DenseArgs p) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS_BYTES];
   __shared__ int last_flag;
   const int lane = threadIdx.x & 63;

@@ -254,12 +254,14 @@ Entry bwd_entry(int layout) {
 }
 
 // Skinny entries (SHK_OPERANDS_STREAM, shk_skinny.h).  Workgroups that share
-// a per-channel tile's K: enough to give about kSkTargetUnits workgroups (two
-// per CU of an MI355X) while every wave keeps at least two stages, at most 16;
+// a per-channel tile's K: enough to give about kSkTargetUnits workgroups (one
+// per CU of an MI355X; at M = 16, N = K = 8192 two workgroups per tile run
+// 8.8 us against 9.9 us for four, each K split adding a tail of device-scope
+// round trips) while every wave keeps at least two stages, at most 16;
 // and for int4 at least as many as keep each wave's x256 int32 sum within
 // 1023 stages of 128 K (up to 64 at K = 2^24).  Without a workspace only
 // one, or 0 when K needs more.  Subchannel tiles always use one.
-constexpr int kSkTargetUnits = 512;
+constexpr int kSkTargetUnits = 256;
 inline int sk_split_count(const shk_kernel_desc& d, long m, long n, long k, bool with_workspace) {
   if (d.scale_mode == SHK_SCALE_SUBCHANNEL) return 1;
   const long ks = d.dtype_bits == 4 ? 128 : 64;
@@ -274,17 +276,18 @@ inline int sk_split_count(const shk_kernel_desc& d, long m, long n, long k, bool
   return (int)(s > need ? s : need);
 }
 // Workspace of a skinny launch with more than one split: the tiles' arrival
-// counters (zero before the first launch, left zero by every launch), padded
-// to 256 bytes, then an exact int32 partial of every (tile, split).
+// counters, padded to 256 bytes, then an exact int32 partial of every (tile,
+// split).  All of it is zero before the first launch and every launch leaves
+// what it used zero, whatever the shapes of the launches that share it.
 inline unsigned long long sk_workspace_bytes(const shk_kernel_desc& d, long m, long n, long k) {
   const int s = sk_split_count(d, m, n, k, true);
   if (s <= 1) return 0;
   const long tiles = (m / d.block_m) * (n / d.block_n);
   const long cf = d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2 : 1;
-  // per (tile, split): 4 waves x (block_m / 16) row tiles x (block_n / 64)
-  // output tiles per wave x (up, gate) x 1 KiB
+  // per (tile, split): (block_n / 16) output column tiles x (block_m / 16)
+  // row tiles x (up, gate) x 1 KiB
   return (unsigned long long)((tiles * 4 + 255) & ~255L) +
-         (unsigned long long)tiles * s * 4 * (d.block_m / 16) * (d.block_n / 64) * cf * 1024;
+         (unsigned long long)tiles * s * (d.block_n / 16) * (d.block_m / 16) * cf * 1024;
 }
 inline unsigned long long sk_counter_bytes(const shk_kernel_desc& d, long m, long n) {
   return (unsigned long long)((((m / d.block_m) * (n / d.block_n)) * 4 + 255) & ~255L);

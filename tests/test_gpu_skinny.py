@@ -121,9 +121,32 @@ def test_split_k_over_workgroups_is_exact(bits, layout, r, epilogue, device):
     _check(first, a_arg, b_arg, bits=bits, layout=layout, sa=sa, sb=sb, sub=None, epilogue=epilogue)
 
 
+def test_split_launches_of_different_shapes_share_the_workspace(device):
+    """Split launches of several shapes in a row on one stream share its
+    workspace.  The counters of a shape with more tiles lie where a shape
+    with fewer tiles kept its partials, so each launch must leave all of the
+    workspace it used zero: every output is exact and the workspace reads
+    all zero after every call."""
+    shapes = [(16, 128, 8192 + 32), (16, 8192, 8192), (32, 256, 4096), (16, 4096, 8192), (16, 128, 8192 + 32)]
+    key = (device.index or 0, torch.cuda.current_stream(device).cuda_stream)
+    for i, (m, n, k) in enumerate(shapes):
+        kernel = _stream_kernel(4, "nn", m)
+        assert kt.sk_split_count(kt.TABLE[kernel.table_index], m, n, k) > 1
+        a_q, b_q, a_arg, b_arg, sa, sb = dense_case(stable_seed("skinny-reuse", i), bits=4, layout="nn", m=m, n=n,
+                                                     k=k, subchannel=None, swiglu=False)
+        a, b = to_dev(torch, a_arg, device), to_dev(torch, b_arg, device)
+        ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
+        print(f"case {kernel.kernel_id} shape=({m},{n},{k}) splits="
+              f"{kt.sk_split_count(kt.TABLE[kernel.table_index], m, n, k)}", flush=True)
+        raw = native.launch_generated_kernel_i32(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw.cpu().numpy(), ref.int_matmul(a_q, b_q)), (m, n, k)
+        assert int(native._SPLIT_WORKSPACES[key].count_nonzero()) == 0, (m, n, k)
+
+
 def test_headline_skinny_shape_every_output(device):
     """M = 16, N = K = 8192 int4 per-channel (the skinny bench line): every
-    output bit-exact, on the split path (4 workgroups per tile)."""
+    output bit-exact, on the split path (2 workgroups per tile)."""
     m, n, k = 16, 8192, 8192
     seed = stable_seed("skinny-headline")
     a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout="nn", m=m, n=n, k=k, subchannel=None,
@@ -132,7 +155,7 @@ def test_headline_skinny_shape_every_output(device):
     ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
     kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=_spec(None), epilogue=shk.Epilogue.NONE,
                                          m=m, n=n, k=k)
-    assert kernel.tile.block_m == 16 and kt.sk_split_count(kt.TABLE[kernel.table_index], m, n, k) == 4
+    assert kernel.tile.block_m == 16 and kt.sk_split_count(kt.TABLE[kernel.table_index], m, n, k) == 2
     print(f"case {kernel.kernel_id} shape=({m},{n},{k})", flush=True)
     out = shk.mm(a, b, a_scale=ta, b_scale=tb)
     raw = native.launch_generated_kernel_i32(a, b, kernel=kernel, a_scale=ta, b_scale=tb)

@@ -140,12 +140,12 @@ def test_reference_small_m_selection_cases():
 
 
 def test_skinny_split_count_rule():
-    """About 512 workgroups, at least two stages per wave, at most 16 splits;
+    """About 256 workgroups (one per CU), at least two stages per wave, at most 16 splits;
     int4 waves stay within 1023 stages of 128 K; subchannel tiles never
     split; without a workspace only the unsplit launch (or none)."""
     d = next(x for x in kt.TABLE if x.is_stream and x.block_m == 16 and x.dtype_bits == 4 and x.scale_mode == 0
              and x.epilogue_kind == kt.EPI_KIND_PLAIN and x.split_k == 1 and x.schedule == 0)
-    assert kt.sk_split_count(d, 16, 8192, 8192) == 4  # 128 tiles, 64 stages
+    assert kt.sk_split_count(d, 16, 8192, 8192) == 2  # 128 tiles, 64 stages
     assert kt.sk_split_count(d, 16, 64, 8192) == 8  # 64 stages: 2 per wave
     assert kt.sk_split_count(d, 256, 8192, 8192) == 1  # 2048 tiles
     assert kt.sk_split_count(d, 16, 64, 32) == 1
@@ -155,7 +155,8 @@ def test_skinny_split_count_rule():
     assert kt.sk_split_count(d, 4096, 8192, 1 << 24) == 64
     sc = next(x for x in kt.TABLE if x.is_stream and x.scale_mode == kt.SCALE_SUBCHANNEL)
     assert kt.sk_split_count(sc, 16, 64, 1 << 20) == 1 and sc.workspace_bytes(16, 64, 1 << 20) == 0
-    assert d.workspace_bytes(16, 8192, 8192) == 512 + 128 * 4 * 4 * 1024
+    # counters of 128 tiles, then 128 tiles x 2 splits x 4 output tiles x 1 KiB
+    assert d.workspace_bytes(16, 8192, 8192) == 512 + 128 * 2 * 4 * 1024
 
 
 def test_workspace_bytes_match_the_library():
