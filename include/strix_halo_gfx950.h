@@ -329,7 +329,10 @@ int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_ind
  * No counterpart in the reference, whose forward takes the list from
  * calculate_group_info (ragged.py:201-323) as a separate step: the fp6
  * entries build it inside their conversion launch (up to 1024 groups), so
- * a call is two launches with no host work between them. */
+ * a call is two launches with no host work between them.  capacity must be
+ * at least amd_strix_halo_kernels_ragged_task_capacity(m, groups, block_m,
+ * align_tile) (rc 1 otherwise), the bound of any list those group sizes
+ * can make, since the sizes are read on the device. */
 int amd_strix_halo_kernels_launch_ragged_fwd_grouped(int kernel_index, int device_index, uintptr_t stream,
                                                      const void* lhs, const void* rhs, const void* a_scale,
                                                      const void* b_scale, const int32_t* group_sizes,

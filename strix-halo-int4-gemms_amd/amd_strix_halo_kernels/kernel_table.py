@@ -221,8 +221,10 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
     # pipe > 0: direct-to-LDS engine with a ring of `pipe` packed stages of 64
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
-    # fp6_sub: three stages of 128 + 128 rows x 128 K in fp6 (96 bytes) and a
-    # four-group scale ring of 768 bytes per group (shk_f6sub.h).
+    # fp6_sub: a 72 KiB ring of 128 + 128 rows in fp6 (96 bytes per 128 K) and
+    # a four-group scale ring of 768 bytes per group (shk_f6sub.h).  Groups of
+    # 256 run three 128-K stage slots (the entry's num_stages, 3); groups of
+    # 128 run six 64-K slots of the same ring, two per group.
     # fp6_small: three stages of 128 A rows + 128 B rows x 128 K in fp6 (96
     # bytes), then the B-scale slots (shk_f6small.h).
     brows = 2 * bn if swiglu else bn

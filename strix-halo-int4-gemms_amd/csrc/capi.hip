@@ -762,6 +762,14 @@ int amd_strix_halo_kernels_launch_ragged_fwd_grouped(int kernel_index, int devic
   if (e->d.operand_format == SHK_OPERANDS_FP6 && align_tile % 32 != 0)
     return fail("fp6 ragged entries need align_tile a multiple of 32 (tasks start on a 32-row panel)");
   if (capacity < 0) return fail("capacity must be non-negative");
+  // the device builds the list, so a list that could outgrow the buffer is
+  // refused here: the forward would otherwise skip every task and leave out
+  // unwritten
+  const int32_t need = amd_strix_halo_kernels_ragged_task_capacity(m, groups, tile, align_tile);
+  if (capacity < need)
+    return fail("capacity " + std::to_string(capacity) + " is below the " + std::to_string(need) +
+                " tasks the list may need for " + std::to_string(m) + " rows in " + std::to_string(groups) +
+                " groups (amd_strix_halo_kernels_ragged_task_capacity)");
   if (num_tasks_i32 == nullptr || tasks_i32 == nullptr) return fail("task list pointers must be non-null");
   if (groups > 0 && group_sizes == nullptr) return fail("group_sizes pointer must be non-null");
   const shk::TaskJob job{group_sizes, groups, tile, align_tile, capacity, tasks_i32, num_tasks_i32, nullptr};

@@ -22,26 +22,29 @@
 //  * the scales reach LDS by LDS-DMA in the same stream as the operands,
 //    so no load the compiler tracks sits in the K loop.
 //
-// Pipeline (that of shk_f6small.h): 128-K stages (two 32 x 64 fp6 blocks
-// per 32-row panel; 12 KiB of A and 12 KiB of B) in a ring of three slots.
-// Stage k: wait for this wave's DMA of stage k+1 and its LDS reads of stage
-// k (with every fragment register of that set as an operand), then the
+// Two engines fill the same 72 KiB ring and scale slots: groups of S = 256
+// run F6SubEngine below (three 128-K slots), groups of S = 128 run
+// F6SubEngine64 (six 64-K slots, two stages per group; described above it).
+// The table entry's num_stages (3) is that of the 128-K engine.
+//
+// Pipeline of F6SubEngine (that of shk_f6small.h): 128-K stages (two 32 x 64
+// fp6 blocks per 32-row panel; 12 KiB of A and 12 KiB of B) in a ring of three
+// slots. Stage k: wait for this wave's DMA of stage k+1 and its LDS reads of
+// stage k (with every fragment register of that set as an operand), then the
 // barrier; 8 MFMAs on the fragments of stage k (two 64-K steps of 2 x 2
 // blocks), each followed by two of the 16 LDS reads of stage k+1 into the
-// other register set, the first seven carrying the DMA loads of stage k+3
-// into slot k % 3 (six operand loads and one scale load per wave).  A group
-// is one (S = 128) or two (S = 256) stages; after its last stage the wave
-// waits for the reads of the next stage (naming their registers, so no
-// compiler copy of a fragment precedes its data) and folds.  128-K stages
-// halve the barriers and waits of 64-K ones, and give each stage's reads a
-// whole stage of MFMAs to land.
+// other register set, the first seven carrying the DMA loads of stage k+3 into
+// slot k % 3 (six operand loads and one scale load per wave).  A group is two
+// stages (S = 256); after its last stage the wave waits for the reads of the
+// next stage (naming their registers, so no compiler copy of a fragment
+// precedes its data) and folds.  128-K stages halve the barriers and waits of
+// 64-K ones, and give each stage's reads a whole stage of MFMAs to land.
 //
 // Scales of group g sit in slot g % 4 of a small ring: the a_scale dword
 // holding row r's scale (dword-aligned pair (e & ~1, e | 1) of e = row * G +
-// g) at 4 r, and the 128 b_scale values at 512.  With groups of 256 the
-// scales of a group load with its first stage, three stages before that
-// stage (by the previous group's second stage; those of groups 0 and 1 in
-// the prologue); with groups of 128 every stage loads its group's scales.
+// g) at 4 r, and the 128 b_scale values at 512.  With groups of 256 the scales
+// of a group load with its first stage, three stages before that stage (by the
+// previous group's second stage; those of groups 0 and 1 in the prologue).
 // The slot a load writes last held the scales of a group every wave has
 // folded before the stage's barrier.
 #pragma once

@@ -9,7 +9,11 @@ scans the device assembly for exactly that: an instruction that reads or
 writes a register of an asm ds_read still in flight, by the wave's
 lgkmcnt rules (an s_waitcnt lgkmcnt(N) retires all but the last N LDS and
 scalar-memory operations issued; a wave never has more than 15 outstanding,
-so the 16th issued retires the oldest).  Reads retire in issue order.
+so the 16th issued retires the oldest).  LDS operations retire in issue
+order, but scalar-memory (and flat) loads may return out of order: while one
+is pending, only lgkmcnt(0) proves that an older LDS read has landed, and the
+15-outstanding rule proves nothing.  An LDS instruction's own VGPR operands
+(address, write data, destination) are checked like any other's.
 
 The asm MFMAs are invisible to the compiler's hazard recognizer in the
 same way: their results arrive passes after the statement.  The scan also
@@ -59,9 +63,9 @@ def _dst(op: str, ops: list[str], line: str) -> set[int]:
 
 
 def _srcs(op: str, ops: list[str]) -> set[int]:
-    if op.startswith(("s_", "ds_")) or not ops:
+    if op.startswith("s_") or not ops:
         return set()
-    if op.startswith(("buffer_store", "global_store", "scratch_store")):
+    if op.startswith(("buffer_store", "global_store", "scratch_store", "ds_write", "ds_store")):
         cand = ops
     else:
         cand = ops[1:]
@@ -94,6 +98,8 @@ def _touched(op: str, ops: list[str], line: str) -> set[int]:
 _LABEL = re.compile(r"^(\.LBB\w+):")
 _BRANCH = re.compile(r"^s_(c?branch\w*)\s+(\.LBB\w+)")
 LGKM_MAX = 15  # outstanding LDS/SMEM operations a wave can have
+# lgkmcnt operations that may return out of order with LDS ones
+_SMEM = ("s_load", "s_buffer_load", "s_memtime", "s_memrealtime", "flat_")
 
 
 def _blocks(lines: list[tuple[int, str, bool]]):
@@ -125,7 +131,8 @@ def _blocks(lines: list[tuple[int, str, bool]]):
 
 def _step(state, no, s, in_asm, fn, found):
     """Advances (reads, mfmas) over one instruction, recording hazards in found (if not None)."""
-    reads, mfma = state  # reads: {line: (asm, regs, ops issued after)}; mfma: {line: (regs, wait states)}
+    # reads: {line: (asm ds_read, regs, ops issued after, out-of-order kind)}; mfma: {line: (regs, wait states)}
+    reads, mfma = state
     nop = _NOP.match(s)
     ws = int(nop.group(1)) + 1 if nop else 1
     op0, ops0 = _operands(s)
@@ -145,22 +152,28 @@ def _step(state, no, s, in_asm, fn, found):
     m = _LGKM.search(s)
     if s.startswith("s_waitcnt") and m:
         n = int(m.group(1))
+        if n == 0:
+            return {}, mfma
+        if any(x[3] for x in reads.values()):  # an out-of-order return may be what the count saw
+            return reads, mfma
         return {l: x for l, x in reads.items() if x[2] < n}, mfma
     op, ops = _operands(s)
     if found is not None:
         live = {}
-        for l, (is_asm, regs, _) in reads.items():
-            if is_asm:
+        for l, (is_asm, regs, _, _) in reads.items():
+            if is_asm and l != no:  # (a loop's earlier instance of this same read is not a conflict)
                 for r in regs:
                     live.setdefault(r, l)
-        if live and not op.startswith("ds_"):
+        if live:
             touched = (_srcs(op, ops) | _dst(op, ops, s)) & set(live)
             if touched:
                 found.append(f"{fn}: line {no} '{s}' touches v{sorted(touched)} of the asm ds_read at line "
                              f"{min(live[r] for r in touched)}")
-    if op.startswith(("ds_", "s_load", "s_buffer_load")):
-        reads = {l: (a, r, c + 1) for l, (a, r, c) in reads.items() if c + 1 < LGKM_MAX}
-        reads[no] = (in_asm and op.startswith("ds_read"), _dst(op, ops, s) if op.startswith("ds_read") else set(), 0)
+    if op.startswith(("ds_",) + _SMEM):
+        unordered = any(x[3] for x in reads.values())
+        reads = {l: (a, r, c + 1, u) for l, (a, r, c, u) in reads.items() if unordered or c + 1 < LGKM_MAX}
+        reads[no] = (in_asm and op.startswith("ds_read"), _dst(op, ops, s) if op.startswith("ds_read") else set(), 0,
+                     op.startswith(_SMEM))
     return reads, mfma
 
 
@@ -168,8 +181,8 @@ def _merge(a, b):
     if a is None:
         return b
     reads = dict(a[0])
-    for l, (x, r, c) in b[0].items():
-        reads[l] = (x, r, min(c, reads[l][2])) if l in reads else (x, r, c)
+    for l, (x, r, c, u) in b[0].items():
+        reads[l] = (x, r, min(c, reads[l][2]), u) if l in reads else (x, r, c, u)
     mfma = dict(a[1])
     for l, (r, w) in b[1].items():
         mfma[l] = (r, min(w, mfma[l][1])) if l in mfma else (r, w)

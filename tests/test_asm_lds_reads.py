@@ -118,3 +118,18 @@ def test_the_scan_finds_a_reuse_and_a_copy():
     asm6 = "\n".join(["_Zq:", ";;#ASMSTART", "ds_read_b32 v10, v1", ";;#ASMEND"] + ["ds_read_b32 v11, v1"] * 15 +
                       ["v_mov_b32_e32 v20, v10"])
     assert inflight_lds_hazards(asm6) == []
+    # ... but not while a scalar load (which may return out of order) is
+    # pending: then neither a counted wait nor 15 younger operations retire it
+    asm7 = "\n".join(["_Zs:", ";;#ASMSTART", "ds_read_b32 v10, v1", ";;#ASMEND", "s_load_dword s4, s[0:1], 0x0",
+                       "ds_read_b32 v11, v1", "s_waitcnt lgkmcnt(1)", "v_mov_b32_e32 v20, v10"])
+    found = inflight_lds_hazards(asm7)
+    assert len(found) == 1 and "v[10]" in found[0]
+    asm8 = "\n".join(["_Zt:", ";;#ASMSTART", "ds_read_b32 v10, v1", ";;#ASMEND", "s_load_dword s4, s[0:1], 0x0"] +
+                      ["ds_read_b32 v11, v1"] * 15 + ["v_mov_b32_e32 v20, v10"])
+    assert len(inflight_lds_hazards(asm8)) == 1
+    assert inflight_lds_hazards(asm7.replace("lgkmcnt(1)", "lgkmcnt(0)")) == []
+    # an in-flight fragment register used as an LDS address or as ds_write data
+    asm9 = "\n".join(["_Zd:", ";;#ASMSTART", "ds_read_b64 v[10:11], v1", ";;#ASMEND", "ds_read_b32 v12, v10",
+                       "ds_write_b32 v2, v11", "s_waitcnt lgkmcnt(0)", "ds_write_b32 v10, v11"])
+    found = inflight_lds_hazards(asm9)
+    assert len(found) == 2 and "v[10]" in found[0] and "v[11]" in found[1]

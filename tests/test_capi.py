@@ -167,6 +167,10 @@ def test_ragged_entry_points_validate_before_launch(lib):
     assert "task list pointers" in _err(lib)
     assert G(fp6.index, 0, 0, *args, 32, FAKE, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 16) == 1
     assert "workspace" in _err(lib)
+    # a task buffer below amd_strix_halo_kernels_ragged_task_capacity is refused
+    need = lib.amd_strix_halo_kernels_ragged_task_capacity(4096, 2, fp6.block_m, 32)
+    assert G(fp6.index, 0, 0, *args, 32, FAKE, FAKE, need - 1, FAKE, 4096, 16, 64, 2, 0, 0, FAKE, 1 << 30) == 1
+    assert f"below the {need} tasks" in _err(lib)
     assert G(bwd, 0, 0, *args, 32, FAKE, FAKE, 8, FAKE, 16, 16, 64, 2, 0, 0, FAKE, 1 << 20) == 1
 
 
