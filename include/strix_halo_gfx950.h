@@ -169,6 +169,23 @@ int amd_strix_halo_kernels_kernel_table_size(void);
 /* Copies entry `index` into *out.  Returns 0, or 1 for a bad index. */
 int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out);
 
+/* The dense entry the Python registry's select() picks (registry.py:254-352
+ * of the reference: same dtype, scale, epilogue, layout, schedule and
+ * split-K; the shape a tile multiple within the entry's K bound; the
+ * largest (measured throughput, block_m * block_n), the first on ties), for
+ * a caller that keeps the reference's own registry: the fields of its
+ * KernelMetadata, whose gfx1151 tiles have no entry here, and the call's
+ * logical shape map to a gfx950 table index.  dtype_bits 4 or 8; layout
+ * SHK_LAYOUT_*; subchannel 0 (per-channel) or 32..256; epilogue
+ * SHK_EPILOGUE_*; schedule SHK_SCHEDULE_*; split_k 0 for any, else the
+ * kernel's split.  Writes *kernel_index and returns 0, or returns 1 with
+ * last_error ("no kernel for ...") when no entry fits.  No counterpart in
+ * the reference, whose bridge (native.py:690-767) is handed a gfx1151
+ * table entry directly. */
+int amd_strix_halo_kernels_select_dense(int32_t dtype_bits, int32_t layout, int32_t subchannel, int32_t epilogue,
+                                        int32_t schedule, int32_t split_k, int32_t m, int32_t n, int32_t k,
+                                        int32_t* kernel_index);
+
 /* ---- dense GEMM -----------------------------------------------------------
  * Replaces amd_strix_halo_kernels_launch_hsaco (dispatch.cpp:224-283) as
  * called by native.launch_generated_kernel (native.py:690-767).

@@ -76,6 +76,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.amd_strix_halo_kernels_kernel_table_size.restype = I
     lib.amd_strix_halo_kernels_kernel_table_entry.argtypes = [I, ctypes.POINTER(_Desc)]
     lib.amd_strix_halo_kernels_kernel_table_entry.restype = I
+    lib.amd_strix_halo_kernels_select_dense.argtypes = [I32, I32, I32, I32, I32, I32, I32, I32, I32,
+                                                        ctypes.POINTER(I32)]
+    lib.amd_strix_halo_kernels_select_dense.restype = I
     lib.amd_strix_halo_kernels_launch_gemm.argtypes = [I, I, U, P, P, P, P, P, I32, I32, I32, I32, I32, I32]
     lib.amd_strix_halo_kernels_launch_gemm.restype = I
     lib.amd_strix_halo_kernels_gemm_workspace_bytes.argtypes = [I, I32, I32, I32, ctypes.POINTER(ctypes.c_uint64)]
@@ -531,6 +534,37 @@ def quantize_device(x: Any, *, mode: int, bits: int = 4, inv_scale: float = 1.0,
                                              int(out.shape[1]))
     _check(lib, rc)
     return out
+
+
+def select_dense_index(*, dtype_bits: int, layout: int, subchannel: int, epilogue: int, schedule: int,
+                       split_k: int, m: int, n: int, k: int, library_path=None) -> int:
+    """The table index amd_strix_halo_kernels_select_dense picks (the
+    registry's selection rule, evaluated by the library)."""
+    lib = _verified_library(library_path)
+    out = ctypes.c_int32(-1)
+    _check(lib, lib.amd_strix_halo_kernels_select_dense(dtype_bits, layout, subchannel, epilogue, schedule, split_k,
+                                                        m, n, k, ctypes.byref(out)))
+    return int(out.value)
+
+
+_LAYOUT_CODES = {"nn": kt.LAYOUT_NN, "nt": kt.LAYOUT_NT, "tn": kt.LAYOUT_TN, "tt": kt.LAYOUT_TT}
+_EPILOGUE_CODES = {"none": kt.EPILOGUE_NONE, "relu2": kt.EPILOGUE_RELU2, "swiglu": kt.EPILOGUE_SWIGLU}
+
+
+def index_for_foreign_kernel(kernel: Any, *, m: int, n: int, k: int, library_path=None) -> int:
+    """The gfx950 table index for a KernelMetadata of another registry (the
+    reference's gfx1151 tiles, registry.py:112-176, which have no entry
+    here), read by its public fields only (a_dtype, layout, scale,
+    epilogue, schedule, tile.split_k) and the call's logical shape: what a
+    bridge that keeps the reference's registry passes to
+    amd_strix_halo_kernels_select_dense."""
+    sub = kernel.scale.subchannel_size if kernel.scale.mode.value == "subchannel" else 0
+    return select_dense_index(dtype_bits=4 if kernel.a_dtype.value == "int4" else 8,
+                              layout=_LAYOUT_CODES[kernel.layout.value], subchannel=int(sub or 0),
+                              epilogue=_EPILOGUE_CODES[kernel.epilogue.value],
+                              schedule=kt.SCHEDULE_PERSISTENT if kernel.schedule.value == "persistent"
+                              else kt.SCHEDULE_STANDARD,
+                              split_k=int(kernel.tile.split_k), m=m, n=n, k=k, library_path=library_path)
 
 
 # ---------------------------------------------------------------------------

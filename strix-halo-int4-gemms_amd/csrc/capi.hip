@@ -486,6 +486,93 @@ int amd_strix_halo_kernels_kernel_table_entry(int index, shk_kernel_desc* out) {
   return 0;
 }
 
+namespace {
+
+// Throughput measured on MI355X for the entries the benchmark configurations
+// time (the Python registry's kernel_table.measured_tops): the first
+// ranking key of a selection, before the tile area.
+double measured_score(const shk_kernel_desc& d) {
+  if (d.schedule != SHK_SCHEDULE_STANDARD || d.split_k > 1) return 0.0;
+  if (d.operand_format == SHK_OPERANDS_FP6) {
+    if (d.scale_mode == SHK_SCALE_SUBCHANNEL) return 2001.0;
+    return d.epilogue_kind == SHK_EPI_KIND_PLAIN ? 3504.0 : 0.0;
+  }
+  if (d.dtype_bits == 8 && d.num_stages == 4 && d.block_m == 256)
+    return d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2014.0 : 2270.0;
+  return 0.0;
+}
+
+// Whether a dense entry serves the request's family: SwiGLU entries serve
+// SwiGLU, persistent and split-K entries the plain epilogue, the others
+// plain and ReLU2; subchannel entries a group size within their range.
+bool serves_family(const shk_kernel_desc& d, int bits, int layout, int subchannel, int epilogue, int schedule,
+                   int split_k) {
+  if (d.family != SHK_FAMILY_DENSE || d.dtype_bits != bits || d.layout != layout || d.schedule != schedule)
+    return false;
+  const int s = d.split_k > 1 ? d.split_k : 1;
+  if (split_k > 0 && s != split_k) return false;
+  if (subchannel == 0 ? d.scale_mode != SHK_SCALE_PER_CHANNEL
+                      : (d.scale_mode != SHK_SCALE_SUBCHANNEL || subchannel < d.min_subchannel ||
+                         subchannel > d.max_subchannel))
+    return false;
+  if (d.epilogue_kind == SHK_EPI_KIND_SWIGLU) return epilogue == SHK_EPILOGUE_SWIGLU;
+  if (d.schedule == SHK_SCHEDULE_PERSISTENT || s > 1) return epilogue == SHK_EPILOGUE_NONE;
+  return epilogue == SHK_EPILOGUE_NONE || epilogue == SHK_EPILOGUE_RELU2;
+}
+
+// The launch-shape rule of prepare_dense, without side effects.
+bool accepts_shape(const shk_kernel_desc& d, int m, int n, int k, int subchannel) {
+  const int s = d.split_k > 1 ? d.split_k : 1;
+  if (m % d.block_m || n % d.block_n || k % (d.block_k * s)) return false;
+  if (subchannel > 0 && k % subchannel) return false;
+  if (subchannel > 0 && s > 1 && d.operand_format != SHK_OPERANDS_STREAM && (k / s) % subchannel) return false;
+  return k <= dense_max_k(d);
+}
+
+}  // namespace
+
+int amd_strix_halo_kernels_select_dense(int32_t dtype_bits, int32_t layout, int32_t subchannel, int32_t epilogue,
+                                        int32_t schedule, int32_t split_k, int32_t m, int32_t n, int32_t k,
+                                        int32_t* kernel_index) {
+  g_last_error.clear();
+  if (kernel_index == nullptr) return fail("kernel_index must be non-null");
+  if (dtype_bits != 4 && dtype_bits != 8) return fail("dtype_bits must be 4 or 8");
+  if (layout < SHK_LAYOUT_NN || layout > SHK_LAYOUT_TT) return fail("layout must be 0 (NN), 1 (NT), 2 (TN) or 3 (TT)");
+  if (subchannel != 0 && subchannel != 32 && subchannel != 64 && subchannel != 128 && subchannel != 256)
+    return fail("subchannel must be 0 (per-channel) or one of 32, 64, 128, 256");
+  if (epilogue < SHK_EPILOGUE_NONE || epilogue > SHK_EPILOGUE_SWIGLU) return fail("epilogue must be 0, 1 or 2");
+  if (schedule != SHK_SCHEDULE_STANDARD && schedule != SHK_SCHEDULE_PERSISTENT)
+    return fail("schedule must be 0 (standard) or 1 (persistent)");
+  if (split_k < 0) return fail("split_k must be 0 (any) or positive");
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail("M, N, and K must be positive; got (" + std::to_string(m) + ", " + std::to_string(n) + ", " +
+                std::to_string(k) + ")");
+  const auto& t = table();
+  int best = -1;
+  double best_score = -1.0;
+  long best_area = -1;
+  for (int i = 0; i < (int)t.size(); ++i) {
+    const shk_kernel_desc& d = t[i].d;
+    if (!serves_family(d, dtype_bits, layout, subchannel, epilogue, schedule, split_k)) continue;
+    if (!accepts_shape(d, m, n, k, subchannel)) continue;
+    const double score = measured_score(d);
+    const long area = (long)d.block_m * d.block_n;
+    if (score > best_score || (score == best_score && area > best_area)) {
+      best = i;
+      best_score = score;
+      best_area = area;
+    }
+  }
+  if (best < 0)
+    return fail("no kernel for dtype_bits=" + std::to_string(dtype_bits) + ", subchannel=" +
+                std::to_string(subchannel) + ", epilogue=" + std::to_string(epilogue) + ", layout=" +
+                std::to_string(layout) + ", schedule=" + std::to_string(schedule) + ", split_k=" +
+                std::to_string(split_k) + ", shape=(" + std::to_string(m) + ", " + std::to_string(n) + ", " +
+                std::to_string(k) + ")");
+  *kernel_index = best;
+  return 0;
+}
+
 int amd_strix_halo_kernels_gemm_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k,
                                                 uint64_t* bytes) {
   g_last_error.clear();
