@@ -173,10 +173,16 @@ struct F6Engine {
   // 8 * bt (bt: B tile index).
   // kb0: first 64-K block of the K range this workgroup multiplies (a K
   // slice of a large-K launch; 0 otherwise).
+  // FRESH (a persistent kernel's tile loop): the thread index passes through
+  // an empty asm statement, so nothing derived from it is computed once
+  // before the loop and held, or spilled, across every tile's K loop.
+  template <bool FRESH = false>
   __device__ __forceinline__ void setup(uint8_t* smem, const uint8_t* a6, const uint8_t* b6, int m0, int bt, int kb,
                                         unsigned long long a_bytes, unsigned long long b_bytes, int kb0 = 0) {
-    lane = threadIdx.x & 63;
-    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int tid = (int)threadIdx.x;
+    if constexpr (FRESH) asm volatile("" : "+v"(tid));
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     wm = wave % 2;
     wn = wave / 2;
     lds0 = lds_address(smem);
@@ -193,12 +199,6 @@ struct F6Engine {
       const uint32_t o = 1024u * (DPW * wave + c) + 16u * lane - (is_a ? 0u : (uint32_t)OPB);
       voff[c] = (o / PANEL) * (uint32_t)panel_bytes + o % PANEL;
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
   }
 
   __device__ __forceinline__ Reads reads_of_slot(int slot) const {
@@ -240,10 +240,25 @@ struct F6Engine {
   // let the register allocator copy an accumulator or fragment between the
   // asm statements, and the copy would read a value the hardware has not
   // written yet (the compiler cannot see the MFMA or the load in the asm).
-  template <int S, int T>
+  // FIRST (the first stage of a tile): the MFMAs of its first 64-K step take
+  // 0 as the C operand and define the accumulators, so no VALU write ever
+  // precedes an MFMA's read of them (see run()).
+  template <int S, int T, bool FIRST>
   __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0) {
     constexpr int ST = T / 16, I = (T % 16) / 4, J = T % 4;
-    if constexpr (T % 2 == 1 && T < 2 * DPW) {
+    if constexpr (FIRST && T < 16 && T % 2 == 1 && T < 2 * DPW) {
+      constexpr int c = T / 2;
+      asm volatile(
+          "v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0 cbsz:2 blgp:2\n\t"
+          "buffer_load_dwordx4 %3, %4, %5 offen lds"
+          : "=a"(acc[I][J])
+          : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]), "v"(voff[c]), "s"(rs_st), "s"(so), "{m0}"(m0 + 1024u * c)
+          : "memory");
+    } else if constexpr (FIRST && T < 16) {
+      asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0 cbsz:2 blgp:2"
+                   : "=a"(acc[I][J])
+                   : "v"(fb[S][ST][J]), "v"(fa[S][ST][I]));
+    } else if constexpr (T % 2 == 1 && T < 2 * DPW) {
       constexpr int c = T / 2;
       // the compiler writes M0 before the statement; the MFMA is the wait
       // state the LDS-DMA load needs after that write
@@ -260,39 +275,21 @@ struct F6Engine {
     }
     read<1 - S, T>(r);
   }
-  template <int S, int... T>
+  template <int S, bool FIRST, int... T>
   __device__ __forceinline__ void ticks(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0,
                                         std::integer_sequence<int, T...>) {
-    (tick<S, T>(r, rs_st, so, m0), ...);
+    (tick<S, T, FIRST>(r, rs_st, so, m0), ...);
   }
   template <int S, int... Q>
   __device__ __forceinline__ void reads(const Reads& r, std::integer_sequence<int, Q...>) {
     (read<S, Q>(r), ...);
   }
 
-  // Clears the accumulators with MFMAs (A = B = 0, C = 0).  A persistent
-  // workgroup calls it before each tile: an asm MFMA whose C operand was
-  // last written by VALU code after an earlier MFMA of the same wave has
-  // read stale values, while an accumulator an MFMA wrote reads back right.
-  __device__ __forceinline__ void mfma_clear() {
-    v6i z;
-#pragma unroll
-    for (int w = 0; w < 6; ++w) z[w] = 0;
-    asm volatile("s_nop 4" : "+v"(z));  // VALU writes of z, then MFMAs read it: 2 wait states needed
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %1, 0 cbsz:2 blgp:2" : "+a"(acc[i][j]) : "v"(z));
-    // tied operands keep each accumulator in place; the fence lands the
-    // results before any other access
-    fence<7>();
-  }
-
   // fence<4> (s_nop 4: 5 wait states) stands between VALU writes of the
-  // accumulators (the prologue's clear) and the first asm MFMA that reads
-  // them as its C operand: a VALU write followed by an MFMA reading the
-  // register needs 2 wait states.  fence<7> (5 x s_nop 7: 40 wait states)
+  // accumulators and an asm MFMA that reads them as its C operand: a VALU
+  // write followed by an MFMA reading the register needs 2 wait states (the
+  // kernels here no longer make such writes: each tile's first MFMAs take 0
+  // as the C operand).  fence<7> (5 x s_nop 7: 40 wait states)
   // stands between the last asm MFMA and any other access to its result: an
   // XDL MFMA of up to 16 passes needs 18 wait states before a VALU, VMEM,
   // LDS or v_accvgpr_read instruction reads its destination or a VALU
@@ -330,7 +327,7 @@ struct F6Engine {
   // fetch a stale slot into the unused set and the DMA loads go through
   // `rs_end`, a resource of zero records: they return zeros without touching
   // memory, into a slot that holds no live data.
-  template <int S>
+  template <int S, bool FIRST = false>
   __device__ __forceinline__ void stage(const Reads& r, int k, int nst, int slot, const v4i& rs_end) {
     wait_vmcnt<DPW>();
     frag_fence<S, 0>();
@@ -339,8 +336,8 @@ struct F6Engine {
     const bool live = k + 3 < nst;
     const v4i rs_st = live ? rs : rs_end;
     const uint32_t so = live ? (uint32_t)(k + 3) * PANEL : 0u;
-    ticks<S>(r, rs_st, so, lds0 + (uint32_t)slot * STAGE + 1024u * DPW * wave,
-             std::make_integer_sequence<int, 32>{});
+    ticks<S, FIRST>(r, rs_st, so, lds0 + (uint32_t)slot * STAGE + 1024u * DPW * wave,
+                    std::make_integer_sequence<int, 32>{});
   }
   // Moves the read slot one ahead (wrapping after slot 2) and the stage slot.
   static __device__ __forceinline__ void advance(Reads& r, int& slot) {
@@ -349,8 +346,20 @@ struct F6Engine {
   }
 
   // nst: 128-K stages (at least one; none leaves the sums at zero).
+  // The first stage runs on its own with FIRST MFMAs, which define the
+  // accumulators: a persistent workgroup's accumulators were last written by
+  // the previous tile's MFMAs, and an asm MFMA whose C operand a VALU write
+  // (a clear) had overwritten after an earlier MFMA of the wave was seen to
+  // read stale values.  The remaining stages alternate register sets from
+  // set 1.
   __device__ __forceinline__ void run(int nst) {
     if (nst <= 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;  // no MFMA reads them
       wait_vmcnt<0>();  // loads issued before the call (the B scales)
       return;
     }
@@ -365,30 +374,31 @@ struct F6Engine {
     wait_vmcnt<2 * DPW>();
     asm volatile("s_barrier" ::: "memory");
     reads<0>(reads_of_slot(0), std::make_integer_sequence<int, 32>{});
-    fence<4>();
     // r: read slot of stage k+1; slot: slot of stage k
     Reads r = reads_of_slot(1);
     int slot = 0;
-    int k = 0;
+    stage<0, true>(r, 0, nst, slot, rs_end);
+    advance(r, slot);
+    int k = 1;
     for (; k + 2 <= nst; k += 2) {
-      stage<0>(r, k, nst, slot, rs_end);
+      stage<1>(r, k, nst, slot, rs_end);
       advance(r, slot);
-      stage<1>(r, k + 1, nst, slot, rs_end);
+      stage<0>(r, k + 1, nst, slot, rs_end);
       advance(r, slot);
     }
     // The last stage's reads fetch a stale slot into the set that no MFMA
     // uses.  They land before the paths merge and before the set's
     // registers could be reused: the fences name every register of the set
-    // (set 0 after the pairs, set 1 after an odd last stage).  Wait states
-    // after the last MFMA likewise, so that a copy the register allocator
-    // places on a merge reads finished accumulators.
-    frag_fence<0, 0>();
-    frag_fence<0, 1>();
+    // (set 1 after the first stage and after the pairs, set 0 after an even
+    // last stage).  Wait states after the last MFMA likewise, so that a copy
+    // the register allocator places on a merge reads finished accumulators.
+    frag_fence<1, 0>();
+    frag_fence<1, 1>();
     fence<7>();
     if (k < nst) {
-      stage<0>(r, k, nst, slot, rs_end);
-      frag_fence<1, 0>();
-      frag_fence<1, 1>();
+      stage<1>(r, k, nst, slot, rs_end);
+      frag_fence<0, 0>();
+      frag_fence<0, 1>();
       fence<7>();
     }
     fence<7>();
@@ -750,8 +760,8 @@ __device__ __forceinline__ void f6_gemm_tile(const DenseArgs& p, uint8_t* smem, 
     klen = min(F6_MAX_K, p.K - k0);
   }
   E e;
-  e.setup(smem, p.a, p.b, m0, tn, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.b_cols, p.K), k0 / 64);
-  if constexpr (PERSIST) e.mfma_clear();
+  e.template setup<PERSIST>(smem, p.a, p.b, m0, tn, p.K / 64, f6_operand_bytes(p.M, p.K),
+                            f6_operand_bytes(p.b_cols, p.K), k0 / 64);
   float sa[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sa[i] = RAW ? 0.0f : load_bf16(p.a_scale + m0 + e.out_row(i));
