@@ -69,6 +69,40 @@ def test_asm_loads_wait_for_valu_written_sgprs(assembly, unit):
     assert not found, "\n".join(found[:10])
 
 
+def _functions(asm: str):
+    import re
+
+    for m in re.finditer(r"^(_Z\S+):", asm, re.M):
+        end = asm.find(".Lfunc_end", m.end())
+        yield m.group(1), asm[m.end():end].splitlines()
+
+
+def test_fp6_gemm_accumulators_are_written_only_by_mfmas(assembly):
+    """In every fp6 GEMM kernel, nothing but MFMAs writes the accumulators
+    between the first MFMA and the last: no VALU write or register copy of
+    an AGPR (a VALU-written C operand after an earlier MFMA of the wave was
+    read stale) and no scratch access (a spilled accumulator).  The
+    persistent kernels, which run the K loop once per tile, keep their
+    scratch under 64 bytes per lane."""
+    import re
+
+    checked = 0
+    for name, lines in _functions(assembly["dense_f6"]):
+        if "f6_gemm_kernel" not in name and "f6_gemm_persistent" not in name:
+            continue
+        mf = [i for i, line in enumerate(lines) if "v_mfma" in line]
+        assert mf, name
+        bad = [lines[i].strip() for i in range(mf[0], mf[-1])
+               if re.search(r"v_accvgpr_(write|mov)|scratch_|^\s*v_\w+(_e\d+)?\s+a\[?\d", lines[i])
+               and "v_mfma" not in lines[i]]
+        assert not bad, (name, bad[:4])
+        if "f6_gemm_persistent" in name:
+            size = re.search(re.escape(name) + r"\.private_seg_size, (\d+)", assembly["dense_f6"])
+            assert size and int(size.group(1)) < 64, (name, size and size.group(1))
+        checked += 1
+    assert checked >= 10
+
+
 def test_the_sgpr_scan_finds_a_reload_before_an_asm_load():
     asm = "\n".join([
         "_Zk:", "v_readlane_b32 s8, v112, 14", ";;#ASMSTART", "s_nop 0",
