@@ -112,6 +112,9 @@ class KernelDesc:
         """Bytes of the workspace for shape (m, n, k): fp6 operands (FP6;
         per-channel calls with K > FP6_MAX_K add [m, b_cols] int32 sums), the
         split-K counters and partials (STREAM), 0 for PACKED."""
+        return _workspace_bytes(self, m, n, k)
+
+    def _workspace_bytes(self, m: int, n: int, k: int) -> int:
         if self.is_stream:
             return sk_workspace_bytes(self, m, n, k)
         if not self.needs_workspace:
@@ -355,6 +358,12 @@ def _build() -> tuple[KernelDesc, ...]:
 
 
 TABLE: tuple[KernelDesc, ...] = _build()
+
+
+@functools.lru_cache(maxsize=4096)
+def _workspace_bytes(desc: KernelDesc, m: int, n: int, k: int) -> int:
+    # memoized: mm() sizes the workspace on every call
+    return desc._workspace_bytes(m, n, k)
 
 
 def measured_tops(desc: KernelDesc) -> float | None:

@@ -199,8 +199,12 @@ def _torch() -> Any:
 
 
 def _stream_handle(torch: Any, tensor: Any, stream: Any | None) -> int:
-    selected = stream if stream is not None else torch.cuda.current_stream(tensor.device)
-    return int(selected.cuda_stream)
+    if stream is not None:
+        return int(stream.cuda_stream)
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:  # the handle alone, without building a Stream object per call
+        return int(raw(_device_index(tensor)))
+    return int(torch.cuda.current_stream(tensor.device).cuda_stream)
 
 
 def _device_index(tensor: Any) -> int:
@@ -221,13 +225,13 @@ def _require_bfloat16_scale(torch: Any, name: str, tensor: Any) -> Any:
 
 
 def _require_device(torch: Any, tensors: dict[str, Any]) -> None:
-    if not torch.cuda.is_available():
-        raise RuntimeError("native generated kernels require a CUDA/HIP torch device")
     first = None
     for name, t in tensors.items():
         if t is None:
             continue
         if not getattr(t, "is_cuda", False):
+            if not torch.cuda.is_available():
+                raise RuntimeError("native generated kernels require a CUDA/HIP torch device")
             raise RuntimeError(f"native generated kernels require CUDA/HIP tensors; {name} is on {t.device}")
         if first is None:
             first = t.device
