@@ -1,41 +1,43 @@
-// 128 x 128 per-channel tile on the fp6 MFMA, two workgroups per CU.
+// 128 x 128 per-channel tile on the fp6 MFMA, two or three workgroups per CU.
 //
 // The small-grid counterpart of F6Engine (shk_f6.h) for the ragged calls,
 // whose grids hold few 256 x 256 tiles (the C5 forward: ~220 tiles for 256
 // CUs, each only 16 K stages deep): a workgroup of 4 waves owns 128 rows x
-// 128 columns (64 x 64 per wave, 2 x 2 accumulators of 32 x 32), uses 73 KiB
-// of LDS and at most 256 registers a lane, so two workgroups share a CU and
-// one's prologue, epilogue and barriers overlap the other's MFMAs.
+// 128 columns (64 x 64 per wave, 2 x 2 accumulators of 32 x 32) and uses at
+// most 168 registers a lane.  With a ring of P = 3 slots (73 KiB of LDS) two
+// workgroups share a CU, with P = 2 (49 KiB) three; one workgroup's
+// prologue, epilogue and barriers overlap the others' MFMAs.
 //
 // Operands are the fp6 blocks of shk_f6.h.  The MFMA is the scaled form
 // (v_mfma_scale_f32_32x32x64_f8f6f4) with E8M0 2^3 on both v/8 operands,
 // so the accumulators hold the exact integer sums (|sum| <= 64 * K <= 2^24
 // for K <= 262144).  The pipeline is F6Engine's at a quarter of the tile:
 // 128-K stages (two 32 x 64 blocks per 32-row panel, 12 KiB of A and 12 KiB
-// of B) in a ring of three slots.  Stage k: wait for this wave's DMA of
-// stage k+1 and its LDS reads of stage k (with every fragment register of
-// that set as an operand, so no compiler copy of a fragment precedes its
-// data), then the barrier; 8 MFMAs on the fragments of stage k (two K steps
-// of 2 x 2 blocks), each followed by two of the 16 LDS reads of stage k+1
-// into the other register set, the first six carrying one DMA load each of
-// stage k+3 into slot k % 3.  A stage therefore has 8 MFMAs to hide its
-// reads' latency, where 64-K stages of 4 MFMAs waited on them.  The
-// accumulators are cleared by VALU writes before the first MFMA of the
-// (one) tile of the workgroup.
+// of B) in a ring of P slots.  Stage k: wait for this wave's DMA of stage
+// k+1 and its LDS reads of stage k (with every fragment register of that
+// set as an operand, so no compiler copy of a fragment precedes its data),
+// then the barrier; 8 MFMAs on the fragments of stage k (two K steps of
+// 2 x 2 blocks), each followed by two of the 16 LDS reads of stage k+1 into
+// the other register set, the first six carrying one DMA load each of stage
+// k+P into slot k % P (free: its fragments were read during stage k-1).  A
+// stage therefore has 8 MFMAs to hide its reads' latency, where 64-K stages
+// of 4 MFMAs waited on them.  The accumulators are cleared by VALU writes
+// before the first MFMA of the (one) tile of the workgroup.
 #pragma once
 
 #include "shk_f6.h"
 
 namespace shk {
 
-template <class C>
+template <class C, int PS = 3>
 struct F6SmallEngine {
-  static constexpr int P = 3;                       // ring slots
+  static constexpr int P = PS;                      // ring slots
+  static_assert(P == 2 || P == 3, "two or three ring slots");
   static constexpr int NW = 4;
   static constexpr int PANEL = 2 * F6_BLOCK;        // 32 rows x 128 K: 3 KiB
   static constexpr int OPB = 4 * PANEL;             // one operand's stage: 12 KiB
   static constexpr int STAGE = 2 * OPB;             // 24 KiB
-  static constexpr int RING = P * STAGE;            // 72 KiB
+  static constexpr int RING = P * STAGE;            // 72 or 48 KiB
   static constexpr int LDS_BYTES = RING;            // B scales follow (MFMA32_SCALE_BYTES)
   static constexpr int DPW = STAGE / 1024 / NW;     // 6 DMA loads per wave per stage
   static constexpr int TN = 64;                     // output columns per wave
@@ -198,15 +200,16 @@ struct F6SmallEngine {
   }
 
   // Stage k (128 K) on set S.  Top: this wave's DMA of stage k+1 has landed
-  // (that of k+2 may be outstanding) and its LDS reads of stage k are done,
-  // then the barrier: stage k+1 is complete in LDS and no wave still reads
-  // slot k % 3.  Then the 8 MFMAs of stage k, the reads of stage k+1 and the
-  // DMA of stage k+3 into slot k % 3.  Past the last stage the DMA loads go
-  // through a resource of zero records into a slot that holds no live data,
-  // and the reads fetch a stale slot into the set no MFMA uses.
+  // (with three slots that of k+2 may be outstanding) and its LDS reads of
+  // stage k are done, then the barrier: stage k+1 is complete in LDS and no
+  // wave still reads slot k % P.  Then the 8 MFMAs of stage k, the reads of
+  // stage k+1 and the DMA of stage k+P into slot k % P.  Past the last stage
+  // the DMA loads go through a resource of zero records into a slot that
+  // holds no live data, and the reads fetch a stale slot into the set no
+  // MFMA uses.
   template <int S>
   __device__ __forceinline__ void stage(const Reads& r, int k, int nst, int slot, const v4i& rs_end, int s8) {
-    wait_vmcnt<DPW>();
+    wait_vmcnt<(P - 2) * DPW>();
     frag_fence<S>();
     asm volatile("s_barrier" ::: "memory");
     const bool live = k + P < nst;
@@ -215,10 +218,11 @@ struct F6SmallEngine {
     ticks<S>(r, rs_st, so, lds0 + (uint32_t)slot * STAGE + 1024u * DPW * wave, s8,
              std::make_integer_sequence<int, 8>{});
   }
-  // Moves the read slot one ahead (wrapping after slot 2) and the stage slot.
+  // Moves the read slot (that of stage k+1, one past `slot`) one ahead,
+  // wrapping after slot P-1, and the stage slot.
   static __device__ __forceinline__ void advance(Reads& r, int& slot) {
-    r.add(slot == 1 ? (uint32_t)(-2 * STAGE) : (uint32_t)STAGE);
-    slot = slot == 2 ? 0 : slot + 1;
+    r.add(slot == P - 2 ? (uint32_t)(-(P - 1) * STAGE) : (uint32_t)STAGE);
+    slot = slot == P - 1 ? 0 : slot + 1;
   }
 
   // nst: 128-K stages (0 leaves the sums at zero).
@@ -229,7 +233,7 @@ struct F6SmallEngine {
     }
     const v4i rs_end = v4i{rs.x, rs.y, 0, rs.w};
     const int s8 = 130;  // E8M0 2^3: both operands hold v/8
-    // stages 0..2 (zeros past the last stage), then stage 0 into set 0
+    // stages 0..P-1 (zeros past the last stage), then stage 0 into set 0
 #pragma unroll
     for (int st = 0; st < P; ++st)
 #pragma unroll
@@ -290,12 +294,19 @@ __device__ __forceinline__ void f6s_read_b_scales(const E& e, const uint8_t* slo
 // With MASK only rows [row_lo, row_hi) and columns below col_hi are written
 // (col_hi a multiple of 8, so a 16-byte unit is in or out whole).
 // NO_NAN (bf16): no value is NaN, so the hardware conversion is exact.
+// The stores write through the L2 (cache policy SC1, bit 16 of the buffer
+// intrinsics on gfx950): a tile's output then leaves no dirty lines for the
+// write-back at the end of the kernel, which the last workgroups' outputs
+// otherwise wait for (the C5 forward, one box, A/B of four builds: 1.1 us
+// faster per call with a three-slot ring, 1.2 us with a two-slot one).
 template <int MODE, bool NO_NAN, bool MASK, class E>
 __device__ __forceinline__ void f6s_store(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                           const float (&sa)[2], const uint2 (&sb)[2][4]) {
   constexpr int ESZ = MODE == OUT_BF16 ? 2 : 4;
   constexpr int PITCH = 64 * ESZ;  // bytes of a staged row
   constexpr int UNITS = PITCH / 16;
+  constexpr int WRITE_THROUGH = 16;
+  static_assert(E::NW * 64 * PITCH <= E::RING, "the staged results fit the ring");
   auto swz = [](int r) { return UNITS == 16 ? (r & 15) : ((r >> 1) & 7); };
   // every wave has finished reading the ring
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -358,7 +369,7 @@ __device__ __forceinline__ void f6s_store(const E& e, const OutView& o, uint8_t*
     const int row = m0 + e.wm * 64 + r;
     if (!MASK || (col_in && row >= o.row_lo && row < o.row_hi))
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rsc, voff,
-                                             (uint32_t)(ROWS * t) * ldo * ESZ, 0);
+                                             (uint32_t)(ROWS * t) * ldo * ESZ, WRITE_THROUGH);
   }
 }
 
