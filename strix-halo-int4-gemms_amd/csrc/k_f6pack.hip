@@ -28,7 +28,16 @@ __device__ __forceinline__ v6i f6_convert(const uint4& x) {
   return __builtin_bit_cast(v6i, __builtin_amdgcn_cvt_scalef32_pk32_fp6_f16(h, 1.0f));
 }
 
-__device__ __forceinline__ void f6_store_lane(uint8_t* block, int lane, const v6i& y) {
+// write_through (uniform): the stores carry SC1, so the block's lines go to
+// memory as they are written instead of at the end of the kernel.
+__device__ __forceinline__ void f6_store_lane(uint8_t* block, int lane, const v6i& y, bool write_through) {
+  if (write_through) {
+    const v4i lo = v4i{y[0], y[1], y[2], y[3]};
+    const v2i hi = v2i{y[4], y[5]};
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(block + 16 * lane), "v"(lo) : "memory");
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(block + 1024 + 8 * lane), "v"(hi) : "memory");
+    return;
+  }
   *reinterpret_cast<uint4*>(block + 16 * lane) = make_uint4(y[0], y[1], y[2], y[3]);
   *reinterpret_cast<uint2*>(block + 1024 + 8 * lane) = make_uint2(y[4], y[5]);
 }
@@ -126,7 +135,7 @@ __device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
   uint8_t* dst = p.dst + g * p.dst_group + first * F6_BLOCK;
 #pragma unroll
   for (int b = 0; b < kNB; ++b)
-    if (live[b]) f6_store_lane(dst + b * F6_BLOCK, lane, f6_convert(x[b]));
+    if (live[b]) f6_store_lane(dst + b * F6_BLOCK, lane, f6_convert(x[b]), p.write_through);
 }
 
 // MN-major source (K row kp holds two K values of every packed row, one per
@@ -201,7 +210,7 @@ __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_
       const v2i hi = ds_read_tr8(q + 2048);
       const uint4 y = make_uint4(lo.x, lo.y, hi.x, hi.y);
       const long blk = (long)(8 * t + b) * p.kb + kb;
-      f6_store_lane(dst + blk * F6_BLOCK, lane, f6_convert(y));
+      f6_store_lane(dst + blk * F6_BLOCK, lane, f6_convert(y), p.write_through);
     }
   }
 }

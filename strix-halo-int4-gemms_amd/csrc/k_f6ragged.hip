@@ -172,7 +172,7 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
   const unsigned long long a_group = f6_operand_bytes(round32(a.M), kw);
   const long kp = a.k_cap / 2;
   const F6PackArgs pa{a.lhs,     a.work,  a.lda,         a.M,    kw / 64, 0, a.groups, kp * a.M, a_group,
-                      a.group_sizes, a.k_cap, piece_bytes(a.lhs, a.lda)};
+                      a.group_sizes, a.k_cap, piece_bytes(a.lhs, a.lda), true};
   const F6PackArgs pb{a.rhs,
                       a.work + (unsigned long long)a.groups * a_group,
                       a.ldb,
@@ -184,7 +184,8 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
                       f6_operand_bytes(round32(a.N), kw),
                       a.group_sizes,
                       a.k_cap,
-                      piece_bytes(a.rhs, a.ldb)};
+                      piece_bytes(a.rhs, a.ldb),
+                      true};
   hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
   if (err != hipSuccess) return err;
   if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);

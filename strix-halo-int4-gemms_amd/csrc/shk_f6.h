@@ -89,6 +89,7 @@ struct F6PackArgs {
   const int32_t* k_len;         // per-operand logical K length, or null
   int k_cap;                    // K length without k_len; the upper clamp of k_len
   int vec;                      // source alignment: 16, 8 or 1
+  bool write_through = false;   // the block stores write through the L2 (cache policy SC1)
 };
 
 // 32-row panels of an operand with `rows` rows.
