@@ -228,12 +228,12 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
     # a four-group scale ring of 768 bytes per group (shk_f6sub.h).  Groups of
     # 256 run three 128-K stage slots (the entry's num_stages, 3); groups of
     # 128 run six 64-K slots of the same ring, two per group.
-    # fp6_small: three stages of 128 A rows + 128 B rows x 128 K in fp6 (96
-    # bytes), then the B-scale slots (shk_f6small.h).
+    # fp6_small: two stages of 128 A rows + 128 B rows x 128 K in fp6 (96
+    # bytes), then the B-scale slots (shk_f6small.h; k_f6ragged.hip).
     brows = 2 * bn if swiglu else bn
     if fp6_small:
         fp6 = True
-        pipe = 3
+        pipe = 2
         lds = pipe * (bm + bn) * 96 + MFMA32_SCALE_BYTES
     elif fp6_sub:
         fp6 = True

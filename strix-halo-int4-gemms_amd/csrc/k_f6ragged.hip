@@ -5,13 +5,11 @@
 // fp6 tile of shk_f6small.h over the converted blocks: the ragged grids are
 // small (the MoE forward of G=8, M=8192, N=1408 makes ~750 of these tiles
 // against ~220 of 256 x 256), so the finer tile fills the CUs and lets one
-// workgroup's prologue and epilogue overlap another's MFMAs.  The bf16
-// forward runs a two-slot ring, three workgroups per CU, so that the 748
-// tiles of that call start in one round (768 slots) instead of 1.46 rounds
-// of 512; its fp32 and int32 forms, whose epilogue stages 64 KiB of
-// results, and the backward (fp32) keep three slots at two per CU.  The
-// conversion absorbs the operand layouts, so one GEMM kernel per output
-// mode serves every layout.
+// workgroup's prologue and epilogue overlap another's MFMAs.  Both run the
+// engine's two-slot ring, three workgroups per CU, so that the 748 tiles of
+// that forward start in one round (768 slots) instead of 1.46 rounds of
+// 512.  The conversion absorbs the operand layouts, so one GEMM kernel per
+// output mode serves every layout.
 //
 // Forward (ragged.py:1008-1229 semantics): out[rows of group g] =
 // lhs[rows] @ rhs[g].  Workgroup (task, tn) takes the task's 128 rows from
@@ -34,10 +32,9 @@ namespace {
 
 // 128 A rows x 128 B rows, 2 x 2 waves, plain epilogue.
 using F6R = Cfg<4, true, true, 128, 128, 128, 2, 2, false, false, 64, false, 0>;
-using F6RE = F6SmallEngine<F6R>;
-// ring slots of the forward by output mode (see above)
-template <int MODE>
-constexpr int kFwdSlots = MODE == OUT_BF16 ? 2 : 3;
+// ring slots of both kernels (see above)
+constexpr int kSlots = 2;
+using F6RE = F6SmallEngine<F6R, kSlots>;
 constexpr int kTile = 128;
 
 __host__ __device__ inline int round32(int x) { return (x + 31) & ~31; }
@@ -53,8 +50,8 @@ __device__ __forceinline__ int xcd_contiguous(int w, int total) {
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256, 5 - kFwdSlots<MODE>) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
-  using E = F6SmallEngine<F6R, kFwdSlots<MODE>>;
+__global__ __launch_bounds__(256, 3) void f6_ragged_fwd_kernel(const RaggedFwdArgs p) {
+  using E = F6RE;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_n = (p.N + kTile - 1) / kTile;
   const int ntasks = *p.num_tasks;
@@ -87,7 +84,7 @@ __global__ __launch_bounds__(256, 5 - kFwdSlots<MODE>) void f6_ragged_fwd_kernel
 }
 
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
+__global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
   using E = F6RE;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = (p.M + kTile - 1) / kTile;

@@ -1,4 +1,5 @@
 // 128 x 128 per-channel tile on the fp6 MFMA, two or three workgroups per CU.
+// The ragged kernels (k_f6ragged.hip) run it with two ring slots.
 //
 // The small-grid counterpart of F6Engine (shk_f6.h) for the ragged calls,
 // whose grids hold few 256 x 256 tiles (the C5 forward: ~220 tiles for 256
@@ -299,6 +300,8 @@ __device__ __forceinline__ void f6s_read_b_scales(const E& e, const uint8_t* slo
 // write-back at the end of the kernel, which the last workgroups' outputs
 // otherwise wait for (the C5 forward, one box, A/B of four builds: 1.1 us
 // faster per call with a three-slot ring, 1.2 us with a two-slot one).
+// With two slots the 4-byte outputs (64 KiB for the four waves) stage in
+// two passes.
 template <int MODE, bool NO_NAN, bool MASK, class E>
 __device__ __forceinline__ void f6s_store(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                           const float (&sa)[2], const uint2 (&sb)[2][4]) {
@@ -306,52 +309,18 @@ __device__ __forceinline__ void f6s_store(const E& e, const OutView& o, uint8_t*
   constexpr int PITCH = 64 * ESZ;  // bytes of a staged row
   constexpr int UNITS = PITCH / 16;
   constexpr int WRITE_THROUGH = 16;
-  static_assert(E::NW * 64 * PITCH <= E::RING, "the staged results fit the ring");
+  // All 64 rows of a wave at once when the four waves' rows fit the ring,
+  // else (4-byte values in a two-slot ring) one 32-row half i per pass
+  // through the same region: a wave's LDS accesses run in order, so a pass's
+  // writes follow the previous pass's reads.
+  constexpr int PASSES = E::NW * 64 * PITCH <= E::RING ? 1 : 2;
+  constexpr int SROWS = 64 / PASSES;
+  static_assert(E::NW * SROWS * PITCH <= E::RING, "the staged results fit the ring");
   auto swz = [](int r) { return UNITS == 16 ? (r & 15) : ((r >> 1) & 7); };
   // every wave has finished reading the ring
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  uint8_t* region = smem + (size_t)e.wave * 64 * PITCH;
+  uint8_t* region = smem + (size_t)e.wave * SROWS * PITCH;
   const int lane = e.lane;
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float s4[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) s4[t] = f6_bf16_at(sb[j][q], t);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r = 32 * i + (lane & 31);
-        const int c = 32 * j + 8 * q + 4 * (lane >> 5);  // first of the lane's 4 columns in the wave's 64
-        uint32_t w[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if constexpr (MODE == OUT_I32) {
-            w[t] = (uint32_t)e.acc_int(i, j, 4 * q + t);
-          } else {
-            float x = e.acc_value(i, j, 4 * q + t) * sa[i];
-            x = x * s4[t];
-            w[t] = __float_as_uint(x);
-          }
-        }
-        if constexpr (MODE == OUT_BF16) {
-          uint32_t lo, hi;
-          if constexpr (NO_NAN) {
-            lo = pack_bf16x2_nonan(__uint_as_float(w[0]), __uint_as_float(w[1]));
-            hi = pack_bf16x2_nonan(__uint_as_float(w[2]), __uint_as_float(w[3]));
-          } else {
-            lo = f32_to_bf16_rne(__uint_as_float(w[0])) | (f32_to_bf16_rne(__uint_as_float(w[1])) << 16);
-            hi = f32_to_bf16_rne(__uint_as_float(w[2])) | (f32_to_bf16_rne(__uint_as_float(w[3])) << 16);
-          }
-          // unit c / 8, half (c / 4) % 2
-          *reinterpret_cast<uint2*>(region + r * PITCH + 16 * ((c >> 3) ^ swz(r)) + 8 * ((c >> 2) & 1)) =
-              make_uint2(lo, hi);
-        } else {
-          *reinterpret_cast<uint4*>(region + r * PITCH + 16 * ((c >> 2) ^ swz(r))) = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
   // read back 64 / UNITS rows per instruction and store whole row segments
   const uint32_t ldo = (uint32_t)o.ld;
   const unsigned long long first = (unsigned long long)m0 * ldo + n0;
@@ -363,13 +332,58 @@ __device__ __forceinline__ void f6s_store(const E& e, const OutView& o, uint8_t*
   const uint32_t voff = ((uint32_t)(e.wm * 64 + rr) * ldo + (uint32_t)col) * ESZ;
   const bool col_in = !MASK || n0 + col < o.col_hi;
 #pragma unroll
-  for (int t = 0; t < 64 / ROWS; ++t) {
-    const int r = ROWS * t + rr;
-    const uint4 x = *reinterpret_cast<const uint4*>(region + r * PITCH + 16 * (u ^ swz(r)));
-    const int row = m0 + e.wm * 64 + r;
-    if (!MASK || (col_in && row >= o.row_lo && row < o.row_hi))
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rsc, voff,
-                                             (uint32_t)(ROWS * t) * ldo * ESZ, WRITE_THROUGH);
+  for (int h = 0; h < PASSES; ++h) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float s4[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s4[t] = f6_bf16_at(sb[j][q], t);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          if (PASSES == 2 && i != h) continue;
+          const int r = (PASSES == 1 ? 32 * i : 0) + (lane & 31);  // staged row
+          const int c = 32 * j + 8 * q + 4 * (lane >> 5);  // first of the lane's 4 columns in the wave's 64
+          uint32_t w[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            if constexpr (MODE == OUT_I32) {
+              w[t] = (uint32_t)e.acc_int(i, j, 4 * q + t);
+            } else {
+              float x = e.acc_value(i, j, 4 * q + t) * sa[i];
+              x = x * s4[t];
+              w[t] = __float_as_uint(x);
+            }
+          }
+          if constexpr (MODE == OUT_BF16) {
+            uint32_t lo, hi;
+            if constexpr (NO_NAN) {
+              lo = pack_bf16x2_nonan(__uint_as_float(w[0]), __uint_as_float(w[1]));
+              hi = pack_bf16x2_nonan(__uint_as_float(w[2]), __uint_as_float(w[3]));
+            } else {
+              lo = f32_to_bf16_rne(__uint_as_float(w[0])) | (f32_to_bf16_rne(__uint_as_float(w[1])) << 16);
+              hi = f32_to_bf16_rne(__uint_as_float(w[2])) | (f32_to_bf16_rne(__uint_as_float(w[3])) << 16);
+            }
+            // unit c / 8, half (c / 4) % 2
+            *reinterpret_cast<uint2*>(region + r * PITCH + 16 * ((c >> 3) ^ swz(r)) + 8 * ((c >> 2) & 1)) =
+                make_uint2(lo, hi);
+          } else {
+            *reinterpret_cast<uint4*>(region + r * PITCH + 16 * ((c >> 2) ^ swz(r))) =
+                make_uint4(w[0], w[1], w[2], w[3]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+    for (int t = 0; t < SROWS / ROWS; ++t) {
+      const int r = ROWS * t + rr;
+      const uint4 x = *reinterpret_cast<const uint4*>(region + r * PITCH + 16 * (u ^ swz(r)));
+      const int row = m0 + e.wm * 64 + h * SROWS + r;
+      if (!MASK || (col_in && row >= o.row_lo && row < o.row_hi))
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rsc, voff,
+                                               (uint32_t)(h * SROWS + ROWS * t) * ldo * ESZ, WRITE_THROUGH);
+    }
   }
 }
 

@@ -320,9 +320,9 @@ def test_fp6_ragged_entries_report_their_workspace(lib):
         fp6 = [d for d in kt.entries(family) if d.operand_format == kt.OPERANDS_FP6]
         assert sorted(d.layout for d in fp6) == [kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN, kt.LAYOUT_TT]
         for d in fp6:
-            # 128 x 128 tiles, three 24 KiB stages of 128 K and the B-scale slots: two per CU
-            assert d.scale_mode == kt.SCALE_PER_CHANNEL and (d.block_m, d.block_k, d.num_stages) == (128, 128, 3)
-            assert d.lds_bytes == 74752
+            # 128 x 128 tiles, two 24 KiB stages of 128 K and the B-scale slots: three per CU
+            assert d.scale_mode == kt.SCALE_PER_CHANNEL and (d.block_m, d.block_k, d.num_stages) == (128, 128, 2)
+            assert d.lds_bytes == 50176
             for m, n, kp, g in ((8192, 1408, 1024, 8), (17, 24, 32, 3), (2048, 1408, 1001, 8), (1, 8, 1, 1)):
                 kw = -(-2 * kp // 128) * 128
                 m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
