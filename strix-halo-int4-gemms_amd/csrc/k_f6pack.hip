@@ -80,22 +80,26 @@ __device__ __forceinline__ int f6_blocks_read(int len) { return 2 * ((len + 127)
 // bytes of one MN-major source tile in LDS: 32 K rows x 256 packed rows
 constexpr int F6_KTILE = 32 * 256;
 
-// Blocks per wave (K-major) and 64-K blocks per workgroup (MN-major), with
-// every load of a wave issued before its first conversion.  Measured on
-// the C2 operands (8192 x 8192): one block per K-major wave runs at the
-// speed of a device copy of the same bytes (more per wave is 4-6% slower),
-// while two 64-K blocks per MN-major workgroup are 19% faster than one when
-// the source is cache-resident and equal from HBM.
-constexpr int kNB = 1;
+// Blocks per wave (K-major: F6PackArgs::kmajor_blocks, 1 or 2) and 64-K
+// blocks per workgroup (MN-major), with every load of a wave issued before
+// its first conversion.  Measured on the C2 operands (8192 x 8192): one
+// block per K-major wave runs at the speed of a device copy of the same
+// bytes (two per wave: the C2 call 0.6% slower, four: 3%), while two 64-K
+// blocks per MN-major workgroup are 19% faster than one when the source is
+// cache-resident and equal from HBM.  The ragged calls' conversions take two
+// blocks per K-major wave: the C5 forward call 34.3 -> 33.1 us (A/B, one
+// box), with a third fewer workgroups to dispatch.
 constexpr int kKW = 2;
 
 // K-major source (row r holds its K values contiguously, two per byte): a
-// wave converts kNB consecutive blocks (panel-major order, so mostly the
+// wave converts NB consecutive blocks (panel-major order, so mostly the
 // same panel's next 64-K blocks); a lane loads its 16 source bytes of each
 // directly.  Nibble j of a little-endian source word is K value 8w + j of
 // its 32, so K values at or past the operand's length are cleared word by
 // word.
-__device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
+template <int NB>
+__device__ __forceinline__ void pack_kmajor_nb(const F6PackArgs& p, int wg) {
+  constexpr int kNB = NB;
   const int lane = threadIdx.x & 63;
   const long blocks = (long)f6_panels(p.rows) * p.kb;
   const long per_group = (blocks + 4 * kNB - 1) / (4 * kNB);
@@ -136,6 +140,11 @@ __device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
 #pragma unroll
   for (int b = 0; b < kNB; ++b)
     if (live[b]) f6_store_lane(dst + b * F6_BLOCK, lane, f6_convert(x[b]), p.write_through);
+}
+
+__device__ __forceinline__ void pack_kmajor(const F6PackArgs& p, int wg) {
+  if (p.kmajor_blocks == 2) pack_kmajor_nb<2>(p, wg);
+  else pack_kmajor_nb<1>(p, wg);
 }
 
 // MN-major source (K row kp holds two K values of every packed row, one per
@@ -216,10 +225,11 @@ __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_
 }
 
 // Workgroups of one operand batch: per operand, one per 256-row tile and kKW
-// 64-K blocks (MN-major) or per 4 * kNB blocks (K-major: kNB per wave).
+// 64-K blocks (MN-major) or per 4 * NB blocks (K-major: NB per wave).
 long pack_groups(const F6PackArgs& a, bool mn_major) {
+  const int nb = a.kmajor_blocks == 2 ? 2 : 1;
   const long per = mn_major ? (long)((a.rows + F6_TILE - 1) / F6_TILE) * ((a.kb + kKW - 1) / kKW)
-                            : ((long)f6_panels(a.rows) * a.kb + 4 * kNB - 1) / (4 * kNB);
+                            : ((long)f6_panels(a.rows) * a.kb + 4 * nb - 1) / (4 * nb);
   return per * a.groups;
 }
 

@@ -152,9 +152,10 @@ int piece_bytes(const uint8_t* src, long ld) {
 hipError_t launch_f6_ragged_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
   const int kw = round128(a.K);
   const unsigned long long a_bytes = f6_operand_bytes(round32(a.M), kw);
-  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda)};
+  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda),
+                      false, 2};
   const F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
-                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb)};
+                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb), false, 2};
   hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s,
                                    a.job.sizes != nullptr ? &a.job : nullptr);
   if (err != hipSuccess) return err;
@@ -169,7 +170,7 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
   const unsigned long long a_group = f6_operand_bytes(round32(a.M), kw);
   const long kp = a.k_cap / 2;
   const F6PackArgs pa{a.lhs,     a.work,  a.lda,         a.M,    kw / 64, 0, a.groups, kp * a.M, a_group,
-                      a.group_sizes, a.k_cap, piece_bytes(a.lhs, a.lda), true};
+                      a.group_sizes, a.k_cap, piece_bytes(a.lhs, a.lda), true, 2};
   const F6PackArgs pb{a.rhs,
                       a.work + (unsigned long long)a.groups * a_group,
                       a.ldb,
@@ -182,7 +183,8 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
                       a.group_sizes,
                       a.k_cap,
                       piece_bytes(a.rhs, a.ldb),
-                      true};
+                      true,
+                      2};
   hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
   if (err != hipSuccess) return err;
   if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);

@@ -90,6 +90,7 @@ struct F6PackArgs {
   int k_cap;                    // K length without k_len; the upper clamp of k_len
   int vec;                      // source alignment: 16, 8 or 1
   bool write_through = false;   // the block stores write through the L2 (cache policy SC1)
+  int kmajor_blocks = 1;        // K-major: 64-K blocks per wave (1 or 2)
 };
 
 // 32-row panels of an operand with `rows` rows.
