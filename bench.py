@@ -71,21 +71,33 @@ def _log(msg: str) -> None:
 
 def _time_steps(torch, fn, steps: int, warmup: int):
     """Runs fn warmup + steps times; returns (wall ms/step, mean and median
-    device ms per call).
+    device ms per call) (see _time_steps_device)."""
+    wall_ms, _, mean, median = _time_steps_device(torch, fn, steps, warmup)
+    return wall_ms, mean, median
+
+
+def _time_steps_device(torch, fn, steps: int, warmup: int):
+    """Runs fn warmup + steps times; returns (wall ms/step, device ms/step,
+    mean and median device ms per call).
 
     The timed loop issues the K calls back to back, as a caller's loop does,
     bracketed by synchronize: an event recorded between two calls adds a gap
     of ~11 us on the GPU (kernel trace of C2: 0 us from one call's last
     kernel to the next call's first without events, 11.5 us with a pair), so
-    the per-call events run in a second pass of the same K calls."""
+    the device time per step comes from one event pair around the whole
+    loop, and the per-call events run in a second pass of the same K calls."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    first, last = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    first.record()
     for _ in range(steps):
         fn()
+    last.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    device_ms = first.elapsed_time(last) / steps
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     for i in range(steps):
@@ -95,7 +107,7 @@ def _time_steps(torch, fn, steps: int, warmup: int):
     torch.cuda.synchronize()
     kern = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     kern.sort()
-    return wall_ms, sum(kern) / len(kern), kern[len(kern) // 2]
+    return wall_ms, device_ms, sum(kern) / len(kern), kern[len(kern) // 2]
 
 
 IDLE_WARMUP, IDLE_CALLS = 5, 20
@@ -244,7 +256,7 @@ def bench_c3(torch, shk, steps, warmup):
     def step():
         return shk.mm(a, b, a_scale=sa, b_scale=sb, scale=spec, epilogue=shk.Epilogue.RELU2)
 
-    wall, kern, _ = _time_steps(torch, step, steps, warmup)
+    wall, dev, kern, _ = _time_steps_device(torch, step, steps, warmup)
     ops = 2 * m * n * k
 
     def cpu():
@@ -253,8 +265,8 @@ def bench_c3(torch, shk, steps, warmup):
                                                         epilogue=shk.Epilogue.RELU2, use_reference=True),
             a, b, sa, sb, m=m, ops_per_row=2 * n * k, what="C3 int4 sc256 ReLU2")
 
-    return {"tops": ops / (kern * 1e-3) / 1e12, "kernel_ms": kern, "wall_ms": wall,
-            "frac_int8_peak": ops / (kern * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS, "_cpu": cpu}
+    return {"tops": ops / (dev * 1e-3) / 1e12, "device_ms": dev, "wall_ms": wall, "event_ms_per_call": kern,
+            "frac_int8_peak": ops / (dev * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS, "_cpu": cpu}
 
 
 def bench_c4(torch, shk, steps, warmup):
@@ -268,7 +280,7 @@ def bench_c4(torch, shk, steps, warmup):
     def step():
         return shk.fused_swiglu_up_gate(a, b, a_scale=sa, b_scale=sb, dtype=shk.OperandDType.INT8)
 
-    wall, kern, _ = _time_steps(torch, step, steps, warmup)
+    wall, dev, kern, _ = _time_steps_device(torch, step, steps, warmup)
     ops = 2 * m * (2 * d) * k
 
     def cpu():
@@ -278,8 +290,8 @@ def bench_c4(torch, shk, steps, warmup):
                                                                           use_reference=True),
             a, b, sa, sb, m=m, ops_per_row=2 * (2 * d) * k, what="C4 int8 fused SwiGLU")
 
-    return {"tops": ops / (kern * 1e-3) / 1e12, "kernel_ms": kern, "wall_ms": wall,
-            "frac_int8_peak": ops / (kern * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS, "_cpu": cpu}
+    return {"tops": ops / (dev * 1e-3) / 1e12, "device_ms": dev, "wall_ms": wall, "event_ms_per_call": kern,
+            "frac_int8_peak": ops / (dev * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS, "_cpu": cpu}
 
 
 def bench_c2_persistent(torch, shk, steps, warmup):
@@ -459,7 +471,7 @@ def bench_c5(torch, shk, steps, warmup):
     if not torch.equal(ref_out, out_f):
         raise RuntimeError("ragged forward: direct launch differs from the API call")
 
-    wall_f, kern_f, _ = _time_steps(torch, fwd, steps, warmup)
+    wall_f, dev_f, kern_f, _ = _time_steps_device(torch, fwd, steps, warmup)
     ops = 2 * rows * n * k
     bytes_f = rows * k // 2 + groups * k * n // 2 + 2 * rows + 2 * groups * n + 2 * rows * n
 
@@ -480,7 +492,7 @@ def bench_c5(torch, shk, steps, warmup):
     if not torch.equal(api_b, out_b):
         raise RuntimeError("ragged backward: direct launch differs from the API call")
 
-    wall_b, kern_b, _ = _time_steps(torch, bwd, steps, warmup)
+    wall_b, dev_b, kern_b, _ = _time_steps_device(torch, bwd, steps, warmup)
 
     # The public calls, as the reference's ragged benchmark times them
     # (autotune.py:746-777): host validation of group_sizes (one device-to-host
@@ -502,15 +514,17 @@ def bench_c5(torch, shk, steps, warmup):
     return {
         "_cpu": cpu,
         "group_sizes": sizes.tolist(),
-        "fwd": {"kernel_ms": kern_f, "wall_ms": wall_f, "tops": ops / (kern_f * 1e-3) / 1e12,
+        "fwd": {"device_ms": dev_f, "wall_ms": wall_f, "event_ms_per_call": kern_f,
+                "tops": ops / (dev_f * 1e-3) / 1e12,
                 "api_wall_ms": api_wall_f, "api_event_ms": api_kern_f,
-                "gbs": bytes_f / (kern_f * 1e-3) / 1e9,
-                "frac_hbm": bytes_f / (kern_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                "frac_int8_peak": ops / (kern_f * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS},
-        "bwd": {"kernel_ms": kern_b, "wall_ms": wall_b, "tops": ops_b / (kern_b * 1e-3) / 1e12,
+                "gbs": bytes_f / (dev_f * 1e-3) / 1e9,
+                "frac_hbm": bytes_f / (dev_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "frac_int8_peak": ops / (dev_f * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS},
+        "bwd": {"device_ms": dev_b, "wall_ms": wall_b, "event_ms_per_call": kern_b,
+                "tops": ops_b / (dev_b * 1e-3) / 1e12,
                 "api_wall_ms": api_wall_b, "api_event_ms": api_kern_b,
-                "gbs": bytes_b / (kern_b * 1e-3) / 1e9,
-                "frac_hbm": bytes_b / (kern_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                "gbs": bytes_b / (dev_b * 1e-3) / 1e9,
+                "frac_hbm": bytes_b / (dev_b * 1e-3) / 1e9 / HBM_PEAK_GBS},
     }
 
 
