@@ -83,30 +83,45 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_fwd_kernel(const RaggedFwdAr
   f6s_finish<MODE, true>(e, o, smem, m0, tn * kTile, sa);
 }
 
+// Regions of the backward's per-group tile grid: sm x sn = 8, one per XCD;
+// 0 x 0 where none fits.  Rows split evenly; columns may split unevenly.
+__host__ __device__ inline void bwd_regions(int tiles_m, int tiles_n, int& sm, int& sn) {
+  sm = sn = 0;
+  if (tiles_m % 4 == 0 && tiles_n >= 2) sm = 4, sn = 2;
+  else if (tiles_m % 2 == 0 && tiles_n % 4 == 0) sm = 2, sn = 4;
+  else if (tiles_m % 8 == 0) sm = 8, sn = 1;
+  else if (tiles_n % 8 == 0) sm = 1, sn = 8;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
   using E = F6RE;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
   const int tiles_m = (p.M + kTile - 1) / kTile;
   const int tiles_n = (p.N + kTile - 1) / kTile;
-  // Each group's tiles_m x tiles_n grid splits into 8 regions of sm x sn
-  // tile rows and columns, one per XCD, so an XCD reads its A tiles for sn
-  // and its B tiles for sm column / row neighbours from its own L2 and holds
-  // tiles of every group, whatever their lengths.  Grids that split no such
-  // way run in order.
+  // Each group's tiles_m x tiles_n grid splits into 8 regions, sm along M
+  // and sn along N, one per XCD, so an XCD reads each of its A tiles for the
+  // column tiles of its region and each B tile for its row tiles from its
+  // own L2, and holds tiles of every group, whatever their lengths.  Rows
+  // split evenly, columns into floor or ceil(tiles_n / sn) (C5's 11 column
+  // tiles: 5 and 6, so a B tile is read by 4 XCDs instead of all 8 with
+  // 8 x 1 regions: the C5 backward 42.4 -> 41.8 us per call, A/B on one
+  // box).  Grids that split no such way run in order.
   int sm = 0, sn = 0;  // region counts along M and N (sm * sn = 8)
-  if (tiles_m % 4 == 0 && tiles_n % 2 == 0) sm = 4, sn = 2;
-  else if (tiles_m % 2 == 0 && tiles_n % 4 == 0) sm = 2, sn = 4;
-  else if (tiles_m % 8 == 0) sm = 8, sn = 1;
-  else if (tiles_n % 8 == 0) sm = 1, sn = 8;
+  bwd_regions(tiles_m, tiles_n, sm, sn);
   int g, tm, tn;
   if (sm) {
     const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
-    const int bm = tiles_m / sm, bn = tiles_n / sn;  // tiles of a region
+    // rows: bm per region; columns: regions of floor or ceil(tiles_n / sn),
+    // each XCD's workgroups laid out for the widest (the rest return)
+    const int bm = tiles_m / sm, bn = (tiles_n + sn - 1) / sn;
     g = i / (bm * bn);
     const int local = i - g * (bm * bn);
+    const int xn = x % sn;
+    const int c0 = tiles_n * xn / sn, width = tiles_n * (xn + 1) / sn - c0;
+    if (local % bn >= width) return;
     tm = (x / sn) * bm + local / bn;
-    tn = (x % sn) * bn + local % bn;
+    tn = c0 + local % bn;
   } else {
     g = blockIdx.x / (tiles_m * tiles_n);
     const int t = blockIdx.x - g * (tiles_m * tiles_n);
@@ -166,6 +181,17 @@ hipError_t launch_f6_ragged_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s
 }
 
 hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
+  {
+    // with XCD regions, every XCD's workgroups cover its widest region
+    const int tiles_m = (a.M + kTile - 1) / kTile, tiles_n = (a.N + kTile - 1) / kTile;
+    int sm, sn;
+    bwd_regions(tiles_m, tiles_n, sm, sn);
+    if (sm) {
+      const long long n = 8LL * a.groups * (tiles_m / sm) * ((tiles_n + sn - 1) / sn);
+      if (n > 0x7FFFFFFFLL) return hipErrorInvalidValue;
+      grid.x = (unsigned)n;
+    }
+  }
   const int kw = round128(a.k_cap);
   const unsigned long long a_group = f6_operand_bytes(round32(a.M), kw);
   const long kp = a.k_cap / 2;
