@@ -358,8 +358,12 @@ def test_ragged_bwd_multi_stage(scale, split_k, device):
 # fp6 backward: every layout, odd and tile-crossing K capacities with
 # random values past each group's length, empty and one-row groups, M and N
 # not multiples of 32
+# (groups, M, K capacity, N, group sizes).  The last four split each group's
+# tile grid into XCD regions: 4 x 2 with 1 and 3 column tiles (regions of 0
+# and 1, 1 and 2 columns), 4 x 2 with 2, and 2 x 4 with 4.
 FP6_BWD_SHAPES = [(3, 48, 39, 24, [5, 0, 37]), (5, 200, 1024, 136, [700, 0, 1, 1023, 512]),
-                  (2, 264, 300, 40, [300, 129])]
+                  (2, 264, 300, 40, [300, 129]), (3, 512, 72, 96, [40, 0, 72]), (2, 512, 136, 296, [136, 77]),
+                  (2, 1024, 64, 256, [64, 1]), (4, 256, 40, 512, [0, 40, 13, 2])]
 
 
 @pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
