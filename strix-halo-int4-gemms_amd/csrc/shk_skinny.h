@@ -347,6 +347,8 @@ __device__ __forceinline__ void sk_wait(bool full) {
 // Device-scope (sc1) 16-byte accesses of the split partials (cache policy
 // bit SC1 = 16 of the buffer intrinsics on gfx950).
 constexpr int SK_SC1 = 16;
+// Partial slots the last workgroup of a split tile loads at once.
+constexpr int SK_BATCH = 4;
 
 // The epilogue scales of a finalizer wave, loaded before its K loop so that
 // their latency passes under it: a_scale of its RT rows, b_scale of the
@@ -489,15 +491,32 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
                    splits - 1;
     __syncthreads();
     if (!*last_flag || !finalizer) return;
-    for (int s2 = 0; s2 < splits; ++s2) {
-      if (s2 == split) continue;
-      const uint32_t off = (uint32_t)(((long)tile * splits + s2) * SLOT_BYTES + wave * WAVE_BYTES);
+    // The other splits' partials, SK_BATCH slots at a time: every load of a
+    // batch is issued before the first add, so their round trips overlap
+    // (M = 16, N = K = 8192 on 4 splits: 15.4 -> 14.9 us per launch from
+    // HBM).  This split's own slot and the slots past the last read through
+    // an offset beyond the resource, which returns zeros.
+    for (int s0 = 0; s0 < splits; s0 += SK_BATCH) {
+      v4i part[SK_BATCH][C::RT][C::FC];
 #pragma unroll
-      for (int rt = 0; rt < C::RT; ++rt)
+      for (int j = 0; j < SK_BATCH; ++j) {
+        const int s2 = s0 + j;
+        const uint32_t off = (s2 < splits && s2 != split)
+                                 ? (uint32_t)(((long)tile * splits + s2) * SLOT_BYTES + wave * WAVE_BYTES)
+                                 : 0x80000000u;
 #pragma unroll
-        for (int fc = 0; fc < C::FC; ++fc)
-          fin[rt][fc] += __builtin_amdgcn_raw_buffer_load_b128(rs, off + ((rt * C::FC + fc) * 64 + lane) * 16u, 0,
-                                                               SK_SC1);
+        for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+          for (int fc = 0; fc < C::FC; ++fc)
+            part[j][rt][fc] = __builtin_amdgcn_raw_buffer_load_b128(
+                rs, off + ((rt * C::FC + fc) * 64 + lane) * 16u, 0, SK_SC1);
+      }
+#pragma unroll
+      for (int j = 0; j < SK_BATCH; ++j)
+#pragma unroll
+        for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+          for (int fc = 0; fc < C::FC; ++fc) fin[rt][fc] += part[j][rt][fc];
     }
     // Every slot of the tile goes back to zero, and so does its counter: a
     // later launch of another shape may place its counters over this
