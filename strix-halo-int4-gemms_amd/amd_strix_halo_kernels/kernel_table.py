@@ -367,22 +367,34 @@ def _workspace_bytes(desc: KernelDesc, m: int, n: int, k: int) -> int:
 
 
 def measured_tops(desc: KernelDesc) -> float | None:
-    """Throughput measured on MI355X for the entries the BASELINE configs
-    time (bench.py, one GPU; the whole call including operand conversion),
-    used by the registry's selection like the reference's benchmark TOPS
-    (registry.py:254-352): fp6 int4 per-channel 256x256 (C2, 8192^3), fp6
-    int4 subchannel 128x128 (C3), int8 32x32 SwiGLU 256x128 (C4, 4096 x
-    2*11008 x 4096) and int8 plain 256x256 (8192^3).  Other entries have no
-    measurement and rank by tile area."""
+    """Throughput measured on MI355X (bench.py and sweeps on one GPU; the
+    whole call including operand conversion), used by the registry's
+    selection like the reference's benchmark TOPS (registry.py:254-352):
+    fp6 int4 per-channel 256x256 (C2, 8192^3), fp6 int4 SwiGLU 256x128
+    (4096 x 2*11008 x 4096), fp6 int4 subchannel 128x128 (C3), int8 32x32
+    SwiGLU 256x128 (C4) and int8 plain 256x256 (8192^3), and the skinny
+    per-channel tiles (SKINNY_TOPS).  Other entries have no measurement and
+    rank by tile area."""
     if desc.family != FAMILY_DENSE or desc.schedule != SCHEDULE_STANDARD or desc.split_k > 1:
         return None
     if desc.operand_format == OPERANDS_FP6:
         if desc.scale_mode == SCALE_SUBCHANNEL:
             return 2001.0
-        return 3504.0 if desc.epilogue_kind == EPI_KIND_PLAIN else None
+        return 3504.0 if desc.epilogue_kind == EPI_KIND_PLAIN else 3161.0
+    if desc.operand_format == OPERANDS_STREAM:
+        return SKINNY_TOPS if desc.scale_mode == SCALE_PER_CHANNEL else None
     if desc.dtype_bits == 8 and desc.num_stages == 4 and desc.block_m == 256:
         return 2014.0 if desc.epilogue_kind == EPI_KIND_SWIGLU else 2270.0
     return None
+
+
+# The skinny per-channel tiles' figure: the bench's skinny line (int4, M = 16,
+# N = K = 8192, 8.9 us per launch: 241 TOPS).  int8 and SwiGLU skinny tiles
+# carry it too: at N = K = 4096 and M = 64 to 4160 every skinny per-channel
+# tile (int4 and int8, plain and SwiGLU) ran 1.2-3x faster than the
+# register-staged 64x64 and 128x128 tiles, which outranked it by area.  The
+# larger measured tiles keep their higher figures where they fit.
+SKINNY_TOPS = 241.0
 
 
 def entries(family: int) -> tuple[KernelDesc, ...]:

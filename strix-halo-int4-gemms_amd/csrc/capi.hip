@@ -495,8 +495,10 @@ double measured_score(const shk_kernel_desc& d) {
   if (d.schedule != SHK_SCHEDULE_STANDARD || d.split_k > 1) return 0.0;
   if (d.operand_format == SHK_OPERANDS_FP6) {
     if (d.scale_mode == SHK_SCALE_SUBCHANNEL) return 2001.0;
-    return d.epilogue_kind == SHK_EPI_KIND_PLAIN ? 3504.0 : 0.0;
+    return d.epilogue_kind == SHK_EPI_KIND_PLAIN ? 3504.0 : 3161.0;
   }
+  if (d.operand_format == SHK_OPERANDS_STREAM)  // the skinny per-channel tiles
+    return d.scale_mode == SHK_SCALE_PER_CHANNEL ? 241.0 : 0.0;
   if (d.dtype_bits == 8 && d.num_stages == 4 && d.block_m == 256)
     return d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2014.0 : 2270.0;
   return 0.0;

@@ -60,7 +60,7 @@ def test_registry_is_built_from_the_table():
 @pytest.mark.parametrize(
     "dtype,scale,epilogue,shape,tile",
     [
-        (shk.OperandDType.INT4, PC, shk.Epilogue.NONE, (128, 1024, 64), (128, 128)),           # C1
+        (shk.OperandDType.INT4, PC, shk.Epilogue.NONE, (128, 1024, 64), (64, 64)),             # C1 (skinny)
         (shk.OperandDType.INT4, PC, shk.Epilogue.NONE, (8192, 8192, 8192), (256, 256)),        # C2
         (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 256), shk.Epilogue.RELU2,
          (4096, 16384, 4096), (128, 128)),                                                     # C3
@@ -71,7 +71,8 @@ def test_registry_is_built_from_the_table():
 )
 def test_select_picks_the_fastest_then_the_largest_fitting_tile(dtype, scale, epilogue, shape, tile):
     """Measured MI355X throughput ranks first (C2-C4 pick the measured fp6
-    and int8 32x32 entries), tile area next (C1, subchannel 64)."""
+    and int8 32x32 entries, C1 the measured skinny tiles, the tallest of
+    them), tile area next (subchannel 64)."""
     m, n, k = shape
     kernel = shk.default_registry.select(dtype=dtype, scale=scale, epilogue=epilogue, m=m, n=n, k=k)
     assert (kernel.tile.block_m, kernel.tile.block_n) == tile
@@ -97,7 +98,8 @@ def test_select_raises_for_shapes_no_kernel_accepts():
 def test_select_knows_each_entry_k_bound():
     """K past an entry's gfx950 bound is never selected: int4 per-channel K
     of 131072 and above skips the int8 engines' unsplit tiles (x16-widened int32
-    accumulators) for a split-K or fp6 entry, K above 262144 runs on the fp6
+    accumulators) for a split-K, skinny (K split over workgroups) or fp6
+    entry, K above 262144 runs on the fp6
     tile in K slices, and past 2^24 no kernel fits (LookupError, the
     registry's contract for an unserved shape)."""
     pc = shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL)
@@ -107,7 +109,7 @@ def test_select_knows_each_entry_k_bound():
         assert kt.TABLE[kern.table_index].supports_k(k), kern.kernel_id
     kern = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=128,
                                        n=128, k=196608)
-    assert kern.tile.split_k > 1
+    assert kern.tile.split_k > 1 or kt.TABLE[kern.table_index].is_stream
     kern = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=pc, epilogue=shk.Epilogue.NONE, m=256,
                                        n=256, k=524288)
     assert kt.TABLE[kern.table_index].operand_format == kt.OPERANDS_FP6
