@@ -73,7 +73,7 @@ void append_all(std::vector<Entry>& t) {
 
 #if !SHK_DENSE_DMA
 // Persistent schedule: the 64 x 64 subchannel tiles for groups of 64 and up
-// and of 32 (int4; the fp6 tiles serve per-channel and groups of 128, 256).
+// and of 32 (int4; the fp6 tiles serve per-channel and groups of 64 to 256).
 void append_persistent(std::vector<Entry>& t) {
   if constexpr (kBits == 4) {
     t.push_back(dense_persistent_entry<C<64, 64, 64, 2, 2, false, true, 64>>(kLayout, 8));

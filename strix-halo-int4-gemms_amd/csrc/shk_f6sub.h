@@ -1,8 +1,8 @@
 // int4 x int4 subchannel GEMM on the fp6 MFMA.
 //
 // out = epilogue(sum over K groups g of (float(A_g @ B_g) * a_scale[m, g]) *
-// b_scale[g, n]), groups of S = 128 or 256 K values, summed in fp32 in group
-// order (api.py:299-325).  The operands are the fp6 blocks of shk_f6.h.
+// b_scale[g, n]), groups of S = 64, 128 or 256 K values, summed in fp32 in
+// group order (api.py:299-325).  The operands are the fp6 blocks of shk_f6.h.
 //
 // Each group's partial products must be scaled on their own, so every S K
 // values the accumulators are folded into fp32 totals with VALU work; that
@@ -22,10 +22,11 @@
 //  * the scales reach LDS by LDS-DMA in the same stream as the operands,
 //    so no load the compiler tracks sits in the K loop.
 //
-// Two engines fill the same 72 KiB ring and scale slots: groups of S = 256
-// run F6SubEngine below (three 128-K slots), groups of S = 128 run
-// F6SubEngine64 (six 64-K slots, two stages per group; described above it).
-// The table entry's num_stages (3) is that of the 128-K engine.
+// Two engines fill the same 72 KiB ring: groups of S = 256 run F6SubEngine
+// below (three 128-K slots, four scale slots), groups of S = 64 and 128 run
+// F6SubEngine64 (six 64-K slots, one or two stages per group, eight scale
+// slots; described above it).  The table entry's num_stages (3) is that of
+// the 128-K engine; its LDS the larger layout, the 64-K engine's.
 //
 // Pipeline of F6SubEngine (that of shk_f6small.h): 128-K stages (two 32 x 64
 // fp6 blocks per 32-row panel; 12 KiB of A and 12 KiB of B) in a ring of three
@@ -478,16 +479,18 @@ struct F6SubEngine {
   }
 };
 
-// The 64-K-stage engine, for groups of 128: one 32 x 64 fp6 block per
-// 32-row panel per stage (6 KiB of A and 6 KiB of B) in a ring of six
-// slots, SPG = 2 stages per group.  Stage k: wait for this wave's DMA of
-// stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
+// The 64-K-stage engine, for groups of 64 and 128: one 32 x 64 fp6 block
+// per 32-row panel per stage (6 KiB of A and 6 KiB of B) in a ring of six
+// slots, SPG = 1 or 2 stages per group.  Stage k: wait for this wave's DMA
+// of stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
 // carrying (the first two) the 8 LDS reads of stage k+1's fragments and the
 // 4 DMA loads of stage k+6 into slot k % 6 (3 operand loads and one scale
 // load per wave); then a fence that waits for this stage's LDS reads with
-// every fragment register of the other set as an operand.  Scales of group
-// g load 5 stages before its first stage, into slot g % 4 of the scale ring
-// (laid out as for the 128-K engine).  (The 128-K engine does not fit 256
+// every fragment register of the other set as an operand.  Stage k loads
+// the scales of stage k+6's group into slot (group % 8) of the scale ring
+// (laid out as for the 128-K engine): with one stage per group, groups k ..
+// k+6 are live at stage k (group k folds after it), and every earlier group
+// folded before stage k's barrier.  (The 128-K engine does not fit 256
 // registers with a fold after every stage.)
 template <class C, int SPG>
 struct F6SubEngine64 {
@@ -497,14 +500,15 @@ struct F6SubEngine64 {
   static constexpr int STAGE = 2 * OPB;             // 12 KiB
   static constexpr int RING = P * STAGE;            // 72 KiB
   static constexpr int SCALE_SLOT = 768;            // 128 a dwords + 128 b halves
-  static constexpr int LDS_BYTES = RING + 4 * SCALE_SLOT;
+  static constexpr int SCALE_SLOTS = 8;
+  static constexpr int LDS_BYTES = RING + SCALE_SLOTS * SCALE_SLOT;
   static constexpr int OPW = STAGE / 1024 / NW;     // 3 operand loads per wave per stage
   static constexpr int DPW = OPW + 1;               // and one scale load
   static constexpr int TN = 64;                     // output columns per wave
   static constexpr int FN = 2;
   static_assert(C::BM == 128 && C::BROWS == 128 && C::WM == 2 && C::WN == 2 && C::SUBCH && !C::SWIGLU,
                 "128 x 128 tiles of 2 x 2 waves, subchannel, plain epilogue");
-  static_assert(SPG == 2 || SPG == 4, "groups of 128 or 256 K");
+  static_assert(SPG == 1 || SPG == 2 || SPG == 4, "groups of 64, 128 or 256 K");
 
   v16f acc[2][2];
   float tot[2][2][16];
@@ -574,7 +578,7 @@ struct F6SubEngine64 {
   }
   // LDS destination of this wave's scale load for group g
   __device__ __forceinline__ uint32_t scale_m0(int g) const {
-    return lds0 + (uint32_t)RING + (uint32_t)(g & 3) * SCALE_SLOT + (wave < 2 ? 256u * wave : 512u);
+    return lds0 + (uint32_t)RING + (uint32_t)(g & (SCALE_SLOTS - 1)) * SCALE_SLOT + (wave < 2 ? 256u * wave : 512u);
   }
 
   struct Reads {
@@ -733,8 +737,13 @@ struct F6SubEngine64 {
   // once.  (A zero product's sign may differ, which changes no sum: the
   // totals start at +0, and x + -0 = x + +0 for every x.)  A wave whose
   // scales fall outside that range folds in the reference's order.
+  // FAST false (one stage per group): every wave folds in the reference's
+  // order, three VALU operations per value and no rank-1 products, whose
+  // two 32-register results do not fit beside the registers of two stages
+  // per loop trip; all_fast still records whether the scales were in range.
+  template <bool FAST>
   __device__ __forceinline__ void fold(const uint8_t* smem, int g) {
-    const uint8_t* sl = smem + RING + (g & 3) * SCALE_SLOT;
+    const uint8_t* sl = smem + RING + (g & (SCALE_SLOTS - 1)) * SCALE_SLOT;
     uint32_t sa_bits[2], sb_bits[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -749,12 +758,16 @@ struct F6SubEngine64 {
     auto in_range = [](uint32_t b) {
       return (b & 0x7FFFu) == 0u || (((b >> 7) & 0xFFu) - (127u - 60u)) < 108u;
     };
-    const bool ok = in_range(sa_bits[0]) && in_range(sa_bits[1]) && in_range(sb_bits[0]) && in_range(sb_bits[1]);
-    if (__all(ok)) {
-      f6sub_fold_fast(acc, tot, lane, sa_bits, sb_bits);
-      return;
+    const bool ok = in_range(sa_bits[0]) & in_range(sa_bits[1]) & in_range(sb_bits[0]) & in_range(sb_bits[1]);
+    if constexpr (FAST) {
+      if (__all(ok)) {
+        f6sub_fold_fast(acc, tot, lane, sa_bits, sb_bits);
+        return;
+      }
+      all_fast = false;
+    } else {
+      if (!__all(ok)) all_fast = false;
     }
-    all_fast = false;
     float sa[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) sa[i] = __uint_as_float(sa_bits[i] << 16);
@@ -826,21 +839,38 @@ struct F6SubEngine64 {
     fence<4>();
     r = reads_of_slot(1);
     int slot = 0;
-    for (int k = 0; k < nst; k += SPG) {
-      // one group: SPG stages, alternating register sets (SPG is even)
-      stage<0, true>(r, k, nst, slot, rs_end, rss_end, s8);
-      advance(r, slot);
-      stage<1, false>(r, k + 1, nst, slot, rs_end, rss_end, s8);
-      advance(r, slot);
-      if constexpr (SPG == 4) {
-        stage<0, false>(r, k + 2, nst, slot, rs_end, rss_end, s8);
+    if constexpr (SPG == 1) {
+      // one group per stage: two stages (one per register set) per trip,
+      // each followed by its fold (nst is even: K is a multiple of 128)
+      for (int k = 0; k < nst; k += 2) {
+        stage<0, true>(r, k, nst, slot, rs_end, rss_end, s8);
         advance(r, slot);
-        stage<1, false>(r, k + 3, nst, slot, rs_end, rss_end, s8);
+        fence<7>();
+        if constexpr (RAW) fold_raw();
+        else fold<false>(smem, k);
+        stage<1, true>(r, k + 1, nst, slot, rs_end, rss_end, s8);
         advance(r, slot);
+        fence<7>();
+        if constexpr (RAW) fold_raw();
+        else fold<false>(smem, k + 1);
       }
-      fence<7>();
-      if constexpr (RAW) fold_raw();
-      else fold(smem, k / SPG);
+    } else {
+      for (int k = 0; k < nst; k += SPG) {
+        // one group: SPG stages, alternating register sets (SPG is even)
+        stage<0, true>(r, k, nst, slot, rs_end, rss_end, s8);
+        advance(r, slot);
+        stage<1, false>(r, k + 1, nst, slot, rs_end, rss_end, s8);
+        advance(r, slot);
+        if constexpr (SPG == 4) {
+          stage<0, false>(r, k + 2, nst, slot, rs_end, rss_end, s8);
+          advance(r, slot);
+          stage<1, false>(r, k + 3, nst, slot, rs_end, rss_end, s8);
+          advance(r, slot);
+        }
+        fence<7>();
+        if constexpr (RAW) fold_raw();
+        else fold<true>(smem, k / SPG);
+      }
     }
     // the loads past the last stage land before the workgroup's LDS is freed
     wait_vmcnt<0>();
@@ -915,13 +945,24 @@ __device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, 
       }
 }
 
+// The engine for groups of S = 64 * G64: the 128-K-stage engine for 256,
+// the 64-K-stage one (G64 stages per group) for 64 and 128.
+template <class C, int G64>
+using F6SubEngineFor = std::conditional_t<G64 == 4, F6SubEngine<C>, F6SubEngine64<C, G64>>;
+// LDS of every subchannel kernel: the larger of the two engines' layouts.
+template <class C>
+constexpr int f6_sub_lds_bytes() {
+  return F6SubEngine<C>::LDS_BYTES > F6SubEngine64<C, 1>::LDS_BYTES ? F6SubEngine<C>::LDS_BYTES
+                                                                       : F6SubEngine64<C, 1>::LDS_BYTES;
+}
+
 // One 128 x 128 output tile of the subchannel GEMM over fp6 blocks (p.a /
-// p.b point at the converted A and B); SPG = S / 128 (2: the 128-K-stage
-// engine, 1: the 64-K-stage one).
-template <class C, int MODE, int EPI, int SPG>
+// p.b point at the converted A and B); G64 = S / 64.
+template <class C, int MODE, int EPI, int G64>
 __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, int tile) {
-  using E = std::conditional_t<SPG == 2, F6SubEngine<C>, F6SubEngine64<C, 2>>;
-  static_assert(F6SubEngine<C>::LDS_BYTES == F6SubEngine64<C, 2>::LDS_BYTES, "both engines fill the same LDS");
+  static_assert(G64 == 1 || G64 == 2 || G64 == 4, "groups of 64, 128 or 256");
+  using E = F6SubEngineFor<C, G64>;
+  static_assert(E::LDS_BYTES <= f6_sub_lds_bytes<C>(), "the engine fits the kernel's LDS");
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
@@ -931,7 +972,7 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
   E e;
   e.setup(smem, p.a, p.b, m0, n0, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.N, p.K), p.a_scale,
           p.b_scale, p.M, p.N, p.K / p.subchannel);
-  e.template run<MODE == OUT_I32>(smem, p.K / (SPG == 2 ? 128 : 64));
+  e.template run<MODE == OUT_I32>(smem, p.K / (G64 == 4 ? 128 : 64));
   const OutView o{p.out, p.b_scale, p.N, p.M, p.N, 0, p.M, p.N};
   if constexpr (MODE == OUT_I32) {
     f6sub_store_words(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
@@ -947,20 +988,20 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
 
 // One kernel per output mode, epilogue and group size; one workgroup per
 // tile, two workgroups per CU.
-template <class C, int MODE, int EPI, int SPG>
+template <class C, int MODE, int EPI, int G64>
 __global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C>::LDS_BYTES];
-  f6_sub_tile<C, MODE, EPI, SPG>(p, smem, blockIdx.x);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[f6_sub_lds_bytes<C>()];
+  f6_sub_tile<C, MODE, EPI, G64>(p, smem, blockIdx.x);
 }
 
 // Persistent schedule (as f6_gemm_persistent): gridDim.x workgroups stride
 // over the tiles, with every LDS read done before the next tile's prologue.
-template <class C, int MODE, int EPI, int SPG>
+template <class C, int MODE, int EPI, int G64>
 __global__ __launch_bounds__(256, 2) void f6_sub_persistent(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngine<C>::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[f6_sub_lds_bytes<C>()];
   const int tiles = (p.M / C::BM) * (p.N / C::BN);
   for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
-    f6_sub_tile<C, MODE, EPI, SPG>(p, smem, t);
+    f6_sub_tile<C, MODE, EPI, G64>(p, smem, t);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }

@@ -372,12 +372,13 @@ def test_fp6_kernels_every_stage_count(kernel, k, device):
 @pytest.mark.parametrize("kernel", _FP6_SUB, ids=lambda k: k.kernel_id)
 @pytest.mark.parametrize("groups", [1, 2, 3, 5])
 def test_fp6_subchannel_every_group_count(kernel, groups, device):
-    """One to five scale groups: each is folded into the fp32 totals in group
-    order, as the oracle sums them, so the results are bit-identical; the
-    int32 output is the whole exact sum.  Scales spread over two decades so
-    that a fold in the wrong order or with the wrong group's scales shows."""
+    """One to five scale groups (groups of 64 in pairs: K is a multiple of the
+    tile's 128): each is folded into the fp32 totals in group order, as the
+    oracle sums them, so the results are bit-identical; the int32 output is
+    the whole exact sum.  Scales spread over two decades so that a fold in the
+    wrong order or with the wrong group's scales shows."""
     _, layout, sub, epi = _kernel_params(kernel)
-    m, n, k = 256, 384, groups * sub
+    m, n, k = 256, 384, groups * max(sub, kernel.tile.block_k)
     seed = stable_seed(f"{kernel.kernel_id}/{groups}")
     a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=sub,
                                                  swiglu=False, scale_lo=0.001, scale_hi=0.1)
@@ -398,7 +399,7 @@ def test_fp6_subchannel_special_scales(kernel, device):
     and zeros put waves on both paths in every group; every output is
     bit-identical to the oracle (NaN as the canonical 0x7FC0)."""
     _, layout, sub, epi = _kernel_params(kernel)
-    m, n, k = 256, 256, 3 * sub
+    m, n, k = 256, 256, 3 * max(sub, kernel.tile.block_k)
     seed = stable_seed("sub-special", kernel.kernel_id)
     a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=4, layout=layout, m=m, n=n, k=k, subchannel=sub,
                                                  swiglu=False, scale_lo=0.001, scale_hi=0.1)
