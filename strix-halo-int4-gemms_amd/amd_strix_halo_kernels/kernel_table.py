@@ -225,10 +225,11 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
     # source bytes per tile row; 0: register-staged engine, two widened stages.
     # fp6: three stages of 256 A rows + 256 B rows x 128 K in fp6 (96 bytes).
     # fp6_sub: a 72 KiB ring of 128 + 128 rows in fp6 (96 bytes per 128 K) and
-    # an eight-group scale ring of 768 bytes per group (shk_f6sub.h).  Groups
-    # of 256 run three 128-K stage slots (the entry's num_stages, 3) and four
-    # of the scale slots; groups of 64 and 128 run six 64-K slots of the same
-    # ring, one or two per group.
+    # an eight-slot scale ring (shk_f6sub.h).  Groups of 256 run three 128-K
+    # stage slots (the entry's num_stages, 3) and four 768-byte scale slots;
+    # groups of 64 and 128 run six 64-K slots of the same ring, one or two per
+    # group, and eight 768-byte scale slots; groups of 32 two per 64-K slot and
+    # eight 1024-byte scale slots (two b_scale rows each), the entry's LDS.
     # fp6_small: two stages of 128 A rows + 128 B rows x 128 K in fp6 (96
     # bytes), then the B-scale slots (shk_f6small.h; k_f6ragged.hip).
     brows = 2 * bn if swiglu else bn
@@ -239,7 +240,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
     elif fp6_sub:
         fp6 = True
         pipe = 3
-        lds = pipe * (bm + bn) * 96 + 8 * 768
+        lds = pipe * (bm + bn) * 96 + 8 * 1024
     elif fp6:
         pipe = 3
         lds = pipe * (bm + 256) * 96 + MFMA32_SCALE_BYTES
@@ -253,7 +254,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         dtype_bits=bits,
         layout=layout,
         scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
-        min_subchannel=(32 if mk == 32 else 64) if subch else 0,
+        min_subchannel=(32 if mk == 32 or fp6_sub else 64) if subch else 0,
         max_subchannel=(32 if mk == 32 else 256) if subch else 0,
         epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
         block_m=bm,

@@ -16,13 +16,14 @@ using C = Cfg<4, true, true, 256, BN, 128, 2, 2, SWIGLU, false, 64, false, 0>;
 using CSub = Cfg<4, true, true, 128, 128, 128, 2, 2, false, true, 64, false, 0>;
 
 // Subchannel GEMM on converted operands: one kernel per output mode,
-// epilogue and group size (S = 64, 128 or 256: S / 64 is the template's last
-// argument).
+// epilogue and group size (S = 32, 64, 128 or 256: S / 32 is the template's
+// last argument).
 template <int MODE, int EPI>
 void launch_sub(const DenseArgs& g, dim3 grid, hipStream_t s) {
-  if (g.subchannel == 64) hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 1>), grid, dim3(256), 0, s, g);
-  else if (g.subchannel == 128) hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 2>), grid, dim3(256), 0, s, g);
-  else hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 4>), grid, dim3(256), 0, s, g);
+  if (g.subchannel == 32) hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 1>), grid, dim3(256), 0, s, g);
+  else if (g.subchannel == 64) hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 2>), grid, dim3(256), 0, s, g);
+  else if (g.subchannel == 128) hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 4>), grid, dim3(256), 0, s, g);
+  else hipLaunchKernelGGL((f6_sub_kernel<CSub, MODE, EPI, 8>), grid, dim3(256), 0, s, g);
 }
 hipError_t launch_f6sub_gemm(const DenseArgs& a, dim3 grid, hipStream_t s) {
   DenseArgs g = a;
@@ -42,9 +43,10 @@ hipError_t launch_f6sub(const DenseArgs& a, dim3 grid, hipStream_t s) {
 }
 template <int MODE, int EPI>
 hipError_t launch_sub_persistent(const DenseArgs& g, unsigned tiles, hipStream_t s) {
-  if (g.subchannel == 64) return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 1>>(g, tiles, 256, s);
-  if (g.subchannel == 128) return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 2>>(g, tiles, 256, s);
-  return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 4>>(g, tiles, 256, s);
+  if (g.subchannel == 32) return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 1>>(g, tiles, 256, s);
+  if (g.subchannel == 64) return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 2>>(g, tiles, 256, s);
+  if (g.subchannel == 128) return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 4>>(g, tiles, 256, s);
+  return launch_persistent<&f6_sub_persistent<CSub, MODE, EPI, 8>>(g, tiles, 256, s);
 }
 hipError_t launch_f6sub_gemm_persistent(const DenseArgs& a, dim3 grid, hipStream_t s) {
   DenseArgs g = a;
@@ -66,7 +68,7 @@ hipError_t launch_f6sub_persistent(const DenseArgs& a, dim3 grid, hipStream_t s)
 }
 Entry f6sub_entry(int layout) {
   shk_kernel_desc d = desc_of<CSub>(SHK_FAMILY_DENSE, layout, 8);
-  d.min_subchannel = 64;
+  d.min_subchannel = 32;
   d.max_subchannel = 256;
   d.num_stages = F6SubEngine<CSub>::P;
   d.lds_bytes = f6_sub_lds_bytes<CSub>();

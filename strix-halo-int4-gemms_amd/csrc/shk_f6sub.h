@@ -1,8 +1,9 @@
 // int4 x int4 subchannel GEMM on the fp6 MFMA.
 //
 // out = epilogue(sum over K groups g of (float(A_g @ B_g) * a_scale[m, g]) *
-// b_scale[g, n]), groups of S = 64, 128 or 256 K values, summed in fp32 in
-// group order (api.py:299-325).  The operands are the fp6 blocks of shk_f6.h.
+// b_scale[g, n]), groups of S = 32, 64, 128 or 256 K values, summed in fp32
+// in group order (api.py:299-325).  The operands are the fp6 blocks of
+// shk_f6.h.
 //
 // Each group's partial products must be scaled on their own, so every S K
 // values the accumulators are folded into fp32 totals with VALU work; that
@@ -23,10 +24,11 @@
 //    so no load the compiler tracks sits in the K loop.
 //
 // Two engines fill the same 72 KiB ring: groups of S = 256 run F6SubEngine
-// below (three 128-K slots, four scale slots), groups of S = 64 and 128 run
-// F6SubEngine64 (six 64-K slots, one or two stages per group, eight scale
-// slots; described above it).  The table entry's num_stages (3) is that of
-// the 128-K engine; its LDS the larger layout, the 64-K engine's.
+// below (three 128-K slots, four scale slots), groups of S = 32, 64 and 128
+// run F6SubEngine64 (six 64-K slots, two groups per stage or one or two
+// stages per group, eight scale slots; described above it).  The table
+// entry's num_stages (3) is that of the 128-K engine; its LDS the largest
+// layout, the 64-K engine's for groups of 32.
 //
 // Pipeline of F6SubEngine (that of shk_f6small.h): 128-K stages (two 32 x 64
 // fp6 blocks per 32-row panel; 12 KiB of A and 12 KiB of B) in a ring of three
@@ -479,9 +481,10 @@ struct F6SubEngine {
   }
 };
 
-// The 64-K-stage engine, for groups of 64 and 128: one 32 x 64 fp6 block
-// per 32-row panel per stage (6 KiB of A and 6 KiB of B) in a ring of six
-// slots, SPG = 1 or 2 stages per group.  Stage k: wait for this wave's DMA
+// The 64-K-stage engine, for groups of 32, 64 and 128: one 32 x 64 fp6
+// block per 32-row panel per stage (6 KiB of A and 6 KiB of B) in a ring of
+// six slots, SPG = 1 or 2 stages per group (SPG = 0: two groups of 32 per
+// stage, see half_stage).  Stage k: wait for this wave's DMA
 // of stage k+1, then the barrier; 4 MFMAs on the fragments of stage k,
 // carrying (the first two) the 8 LDS reads of stage k+1's fragments and the
 // 4 DMA loads of stage k+6 into slot k % 6 (3 operand loads and one scale
@@ -490,8 +493,9 @@ struct F6SubEngine {
 // the scales of stage k+6's group into slot (group % 8) of the scale ring
 // (laid out as for the 128-K engine): with one stage per group, groups k ..
 // k+6 are live at stage k (group k folds after it), and every earlier group
-// folded before stage k's barrier.  (The 128-K engine does not fit 256
-// registers with a fold after every stage.)
+// folded before stage k's barrier; with two groups per stage, a slot holds
+// both groups' a_scale dwords and b_scale rows.  (The 128-K engine does not
+// fit 256 registers with a fold after every stage.)
 template <class C, int SPG>
 struct F6SubEngine64 {
   static constexpr int P = 6;                       // ring slots
@@ -499,7 +503,8 @@ struct F6SubEngine64 {
   static constexpr int OPB = 4 * F6_BLOCK;          // 128 rows x 64 K: 6 KiB
   static constexpr int STAGE = 2 * OPB;             // 12 KiB
   static constexpr int RING = P * STAGE;            // 72 KiB
-  static constexpr int SCALE_SLOT = 768;            // 128 a dwords + 128 b halves
+  static constexpr bool HALF = SPG == 0;            // groups of 32: two per stage
+  static constexpr int SCALE_SLOT = HALF ? 1024 : 768;  // 128 a dwords + 128 b halves (HALF: two b rows)
   static constexpr int SCALE_SLOTS = 8;
   static constexpr int LDS_BYTES = RING + SCALE_SLOTS * SCALE_SLOT;
   static constexpr int OPW = STAGE / 1024 / NW;     // 3 operand loads per wave per stage
@@ -508,7 +513,7 @@ struct F6SubEngine64 {
   static constexpr int FN = 2;
   static_assert(C::BM == 128 && C::BROWS == 128 && C::WM == 2 && C::WN == 2 && C::SUBCH && !C::SWIGLU,
                 "128 x 128 tiles of 2 x 2 waves, subchannel, plain epilogue");
-  static_assert(SPG == 1 || SPG == 2 || SPG == 4, "groups of 64, 128 or 256 K");
+  static_assert(SPG == 0 || SPG == 1 || SPG == 2 || SPG == 4, "groups of 32, 64, 128 or 256 K");
 
   v16f acc[2][2];
   float tot[2][2][16];
@@ -518,6 +523,7 @@ struct F6SubEngine64 {
   v4i rs;        // operand DMA resource (waves 0-1: A, 2-3: B)
   v4i rss;       // scale DMA resource (waves 0-1: a_scale, 2-3: b_scale)
   int sbase;     // waves 0-1: element index row * G of the lane's row; 2-3: byte of its b_scale pair
+                 // (HALF: the byte offset of the lane's scale dword of group 0; wave 3: of group 1)
   int groups;    // G = K / S
   int sb_row;    // bytes of one b_scale row (N * 2)
   uint32_t lds0;
@@ -560,6 +566,8 @@ struct F6SubEngine64 {
       rss = buffer_words(b_scale, 2ull * (unsigned long long)g * n_cols);
       sbase = 2 * (n0 + 2 * lane);
     }
+    // (G is a multiple of 4 with groups of 32, so row * G is even)
+    if constexpr (HALF) sbase = is_a ? 2 * sbase : sbase + (wave == 3 ? sb_row : 0);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -572,13 +580,20 @@ struct F6SubEngine64 {
     all_fast = true;
   }
 
-  // byte offset of this lane's scale dword for group g
-  __device__ __forceinline__ uint32_t scale_voff(int g) const {
+  // byte offset of this lane's scale dword for stage st: waves 0-1 the
+  // a_scale dword of the stage's group (HALF: the dword holding both of its
+  // groups, the first one even), waves 2-3 two b_scale columns of it (HALF:
+  // wave 3 those of the second group)
+  __device__ __forceinline__ uint32_t scale_voff(int st) const {
+    if constexpr (HALF) return (uint32_t)(sbase + (wave < 2 ? 4 * st : 2 * st * sb_row));
+    const int g = st / (HALF ? 1 : SPG);
     return wave < 2 ? (uint32_t)(2 * (sbase + g)) & ~3u : (uint32_t)(g * sb_row + sbase);
   }
-  // LDS destination of this wave's scale load for group g
-  __device__ __forceinline__ uint32_t scale_m0(int g) const {
-    return lds0 + (uint32_t)RING + (uint32_t)(g & (SCALE_SLOTS - 1)) * SCALE_SLOT + (wave < 2 ? 256u * wave : 512u);
+  // LDS destination of this wave's scale load for stage st
+  __device__ __forceinline__ uint32_t scale_m0(int st) const {
+    const int slot = (HALF ? st : st / (HALF ? 1 : SPG)) & (SCALE_SLOTS - 1);
+    return lds0 + (uint32_t)RING + (uint32_t)slot * SCALE_SLOT +
+           (wave < 2 ? 256u * wave : (HALF && wave == 3 ? 768u : 512u));
   }
 
   struct Reads {
@@ -625,11 +640,24 @@ struct F6SubEngine64 {
   // the scale dword), followed by LDS reads 4T .. 4T+3 of the next stage
   // for T < 2: all reads go out early, so they have landed when the stage's
   // closing fence waits for them.
-  template <int S, int T, bool ZERO>
+  // PART 1: the DMA load only, PART 2: the LDS reads only (the two halves
+  // of a HALF stage).
+  template <int S, int T, bool ZERO, int PART = 0>
   __device__ __forceinline__ void tick(const Reads& r, const v4i& rs_st, uint32_t so, uint32_t m0_st,
                                        const v4i& rss_st, uint32_t svo, uint32_t sm0, int s8) {
     constexpr int I = T / 2, J = T % 2;
-    if constexpr (T < OPW) {
+    if constexpr (PART == 2) {
+      if constexpr (ZERO)
+        asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, 0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2"
+                     : "+v"(acc[I][J])
+                     : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8)
+                     : "memory");
+      else
+        asm volatile("v_mfma_scale_f32_32x32x64_f8f6f4 %0, %1, %2, %0, %3, %3 op_sel_hi:[0,0,0] cbsz:2 blgp:2"
+                     : "+v"(acc[I][J])
+                     : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8)
+                     : "memory");
+    } else if constexpr (T < OPW) {
       // the compiler writes M0 before the statement; the MFMA is the wait
       // state the LDS-DMA load needs after that write
       if constexpr (ZERO)
@@ -662,7 +690,7 @@ struct F6SubEngine64 {
             : "v"(fb[S][J]), "v"(fa[S][I]), "v"(s8), "v"(svo), "s"(rss_st), "{m0}"(sm0)
             : "memory");
     }
-    if constexpr (T < 2) {
+    if constexpr (T < 2 && PART != 1) {
       read<1 - S, 4 * T>(r);
       read<1 - S, 4 * T + 1>(r);
       read<1 - S, 4 * T + 2>(r);
@@ -690,6 +718,21 @@ struct F6SubEngine64 {
       asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
                    : "+v"(acc[0][0]), "+v"(acc[0][1]), "+v"(acc[1][0]), "+v"(acc[1][1]));
   }
+  // Every total is an operand: a fold's adds are all done here, so none is
+  // moved below the next MFMAs, which write the accumulators it reads (the
+  // compiler would give those MFMAs a second accumulator set).
+  __device__ __forceinline__ void tot_fence() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float* t = tot[i][j];
+        asm volatile(""
+                     : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]), "+v"(t[6]),
+                       "+v"(t[7]), "+v"(t[8]), "+v"(t[9]), "+v"(t[10]), "+v"(t[11]), "+v"(t[12]), "+v"(t[13]),
+                       "+v"(t[14]), "+v"(t[15]));
+      }
+  }
   // This wave's LDS reads into set S have landed; every register of the set
   // is an operand, so no copy of it is placed before this point.
   template <int S>
@@ -708,16 +751,56 @@ struct F6SubEngine64 {
     const bool live = kl < nst;
     const v4i rs_st = live ? rs : rs_end;
     const v4i rss_st = live ? rss : rss_end;
-    const int gl = kl / SPG;
     const uint32_t so = live ? (uint32_t)kl * F6_BLOCK : 0u;
-    const uint32_t svo = live ? scale_voff(gl) : 0u;
+    const uint32_t svo = live ? scale_voff(kl) : 0u;
     const uint32_t m0_st = lds0 + (uint32_t)slot * STAGE + 1024u * OPW * wave;
-    const uint32_t sm0 = scale_m0(gl);
+    const uint32_t sm0 = scale_m0(kl);
     tick<S, 0, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
     tick<S, 1, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
     tick<S, 2, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
     tick<S, 3, ZERO>(r, rs_st, so, m0_st, rss_st, svo, sm0, s8);
     frag_fence<1 - S>();
+  }
+
+  // HALF: stage k holds groups 2k (K 0..31 of every block) and 2k+1 (K
+  // 32..63); lanes 0-31 of each fragment hold K 0..31 of their row or column
+  // and lanes 32-63 K 32..63, and each lane's E8M0 scale applies to its own
+  // 32 values.  The four MFMAs of group 2k take scale 2^3 on lanes 0-31 and
+  // 2^-127 on lanes 32-63 (s_lo), whose products (at most 2^-249 in
+  // magnitude) round away in the fp32 result; they carry the stage's DMA
+  // loads.  Then group 2k's fold; the same four MFMAs with the scales swapped
+  // (s_hi) take group 2k+1 and carry the reads of stage k+1's fragments; the
+  // wait for those reads; group 2k+1's fold.
+  template <int S, bool RAW>
+  __device__ __forceinline__ void half_stage(const uint8_t* smem, const Reads& r, int k, int nst, int slot,
+                                             const v4i& rs_end, const v4i& rss_end, int s_lo, int s_hi) {
+    wait_vmcnt<(P - 2) * DPW>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int kl = k + P;  // the stage loaded now
+    const bool live = kl < nst;
+    const v4i rs_st = live ? rs : rs_end;
+    const v4i rss_st = live ? rss : rss_end;
+    const uint32_t so = live ? (uint32_t)kl * F6_BLOCK : 0u;
+    const uint32_t svo = live ? scale_voff(kl) : 0u;
+    const uint32_t m0_st = lds0 + (uint32_t)slot * STAGE + 1024u * OPW * wave;
+    const uint32_t sm0 = scale_m0(kl);
+    tick<S, 0, true, 1>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_lo);
+    tick<S, 1, true, 1>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_lo);
+    tick<S, 2, true, 1>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_lo);
+    tick<S, 3, true, 1>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_lo);
+    fence<7>();
+    if constexpr (RAW) fold_raw();
+    else fold<false>(smem, 2 * k);
+    tot_fence();
+    tick<S, 0, true, 2>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_hi);
+    tick<S, 1, true, 2>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_hi);
+    tick<S, 2, true, 2>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_hi);
+    tick<S, 3, true, 2>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_hi);
+    frag_fence<1 - S>();
+    fence<7>();
+    if constexpr (RAW) fold_raw();
+    else fold<false>(smem, 2 * k + 1);
+    tot_fence();
   }
   static __device__ __forceinline__ void advance(Reads& r, int& slot) {
     r.add(slot == P - 2 ? (uint32_t)(-(P - 1) * STAGE) : (uint32_t)STAGE);
@@ -743,7 +826,8 @@ struct F6SubEngine64 {
   // per loop trip; all_fast still records whether the scales were in range.
   template <bool FAST>
   __device__ __forceinline__ void fold(const uint8_t* smem, int g) {
-    const uint8_t* sl = smem + RING + (g & (SCALE_SLOTS - 1)) * SCALE_SLOT;
+    const uint8_t* sl = smem + RING + ((HALF ? g >> 1 : g) & (SCALE_SLOTS - 1)) * SCALE_SLOT;
+    const uint8_t* sbl = sl + 512 + (HALF ? 256 * (g & 1) : 0);  // the group's b_scale row
     uint32_t sa_bits[2], sb_bits[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -754,7 +838,7 @@ struct F6SubEngine64 {
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      sb_bits[j] = *reinterpret_cast<const uint16_t*>(sl + 512 + 2 * (wn * TN + 32 * j + (lane & 31)));
+      sb_bits[j] = *reinterpret_cast<const uint16_t*>(sbl + 2 * (wn * TN + 32 * j + (lane & 31)));
     auto in_range = [](uint32_t b) {
       return (b & 0x7FFFu) == 0u || (((b >> 7) & 0xFFu) - (127u - 60u)) < 108u;
     };
@@ -775,7 +859,7 @@ struct F6SubEngine64 {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint2 w = *reinterpret_cast<const uint2*>(sl + 512 + 2 * out_col(j, q));
+        const uint2 w = *reinterpret_cast<const uint2*>(sbl + 2 * out_col(j, q));
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -821,7 +905,7 @@ struct F6SubEngine64 {
       // of the resource's SGPRs, as in lds_dma16)
       asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds"
                    :
-                   : "v"(live ? scale_voff(st / SPG) : 0u), "s"(live ? rss : rss_end), "{m0}"(scale_m0(st / SPG))
+                   : "v"(live ? scale_voff(st) : 0u), "s"(live ? rss : rss_end), "{m0}"(scale_m0(st))
                    : "memory");
     }
     wait_vmcnt<(P - 1) * DPW>();
@@ -839,7 +923,15 @@ struct F6SubEngine64 {
     fence<4>();
     r = reads_of_slot(1);
     int slot = 0;
-    if constexpr (SPG == 1) {
+    if constexpr (HALF) {
+      const int s_lo = lane < 32 ? s8 : 0, s_hi = lane < 32 ? 0 : s8;
+      for (int k = 0; k < nst; k += 2) {
+        half_stage<0, RAW>(smem, r, k, nst, slot, rs_end, rss_end, s_lo, s_hi);
+        advance(r, slot);
+        half_stage<1, RAW>(smem, r, k + 1, nst, slot, rs_end, rss_end, s_lo, s_hi);
+        advance(r, slot);
+      }
+    } else if constexpr (SPG == 1) {
       // one group per stage: two stages (one per register set) per trip,
       // each followed by its fold (nst is even: K is a multiple of 128)
       for (int k = 0; k < nst; k += 2) {
@@ -945,24 +1037,24 @@ __device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, 
       }
 }
 
-// The engine for groups of S = 64 * G64: the 128-K-stage engine for 256,
-// the 64-K-stage one (G64 stages per group) for 64 and 128.
-template <class C, int G64>
-using F6SubEngineFor = std::conditional_t<G64 == 4, F6SubEngine<C>, F6SubEngine64<C, G64>>;
-// LDS of every subchannel kernel: the larger of the two engines' layouts.
+// The engine for groups of S = 32 * G32: the 128-K-stage engine for 256,
+// the 64-K-stage one for 32, 64 and 128 (G32 / 2 stages per group; 0: two
+// groups per stage).
+template <class C, int G32>
+using F6SubEngineFor = std::conditional_t<G32 == 8, F6SubEngine<C>, F6SubEngine64<C, G32 / 2>>;
+// The largest LDS layout of the subchannel kernels (the table entry's).
 template <class C>
 constexpr int f6_sub_lds_bytes() {
-  return F6SubEngine<C>::LDS_BYTES > F6SubEngine64<C, 1>::LDS_BYTES ? F6SubEngine<C>::LDS_BYTES
-                                                                       : F6SubEngine64<C, 1>::LDS_BYTES;
+  return F6SubEngine<C>::LDS_BYTES > F6SubEngine64<C, 0>::LDS_BYTES ? F6SubEngine<C>::LDS_BYTES
+                                                                       : F6SubEngine64<C, 0>::LDS_BYTES;
 }
 
 // One 128 x 128 output tile of the subchannel GEMM over fp6 blocks (p.a /
-// p.b point at the converted A and B); G64 = S / 64.
-template <class C, int MODE, int EPI, int G64>
+// p.b point at the converted A and B); G32 = S / 32.
+template <class C, int MODE, int EPI, int G32>
 __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, int tile) {
-  static_assert(G64 == 1 || G64 == 2 || G64 == 4, "groups of 64, 128 or 256");
-  using E = F6SubEngineFor<C, G64>;
-  static_assert(E::LDS_BYTES <= f6_sub_lds_bytes<C>(), "the engine fits the kernel's LDS");
+  static_assert(G32 == 1 || G32 == 2 || G32 == 4 || G32 == 8, "groups of 32, 64, 128 or 256");
+  using E = F6SubEngineFor<C, G32>;
   const int tiles_m = p.M / C::BM;
   const int tiles_n = p.N / C::BN;
   int tm, tn;
@@ -972,7 +1064,7 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
   E e;
   e.setup(smem, p.a, p.b, m0, n0, p.K / 64, f6_operand_bytes(p.M, p.K), f6_operand_bytes(p.N, p.K), p.a_scale,
           p.b_scale, p.M, p.N, p.K / p.subchannel);
-  e.template run<MODE == OUT_I32>(smem, p.K / (G64 == 4 ? 128 : 64));
+  e.template run<MODE == OUT_I32>(smem, p.K / (G32 == 8 ? 128 : 64));
   const OutView o{p.out, p.b_scale, p.N, p.M, p.N, 0, p.M, p.N};
   if constexpr (MODE == OUT_I32) {
     f6sub_store_words(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
@@ -988,20 +1080,20 @@ __device__ __forceinline__ void f6_sub_tile(const DenseArgs& p, uint8_t* smem, i
 
 // One kernel per output mode, epilogue and group size; one workgroup per
 // tile, two workgroups per CU.
-template <class C, int MODE, int EPI, int G64>
+template <class C, int MODE, int EPI, int G32>
 __global__ __launch_bounds__(256, 2) void f6_sub_kernel(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[f6_sub_lds_bytes<C>()];
-  f6_sub_tile<C, MODE, EPI, G64>(p, smem, blockIdx.x);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngineFor<C, G32>::LDS_BYTES];
+  f6_sub_tile<C, MODE, EPI, G32>(p, smem, blockIdx.x);
 }
 
 // Persistent schedule (as f6_gemm_persistent): gridDim.x workgroups stride
 // over the tiles, with every LDS read done before the next tile's prologue.
-template <class C, int MODE, int EPI, int G64>
+template <class C, int MODE, int EPI, int G32>
 __global__ __launch_bounds__(256, 2) void f6_sub_persistent(const DenseArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[f6_sub_lds_bytes<C>()];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F6SubEngineFor<C, G32>::LDS_BYTES];
   const int tiles = (p.M / C::BM) * (p.N / C::BN);
   for (int t = blockIdx.x; t < tiles; t += gridDim.x) {
-    f6_sub_tile<C, MODE, EPI, G64>(p, smem, t);
+    f6_sub_tile<C, MODE, EPI, G32>(p, smem, t);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
 }

@@ -223,9 +223,9 @@ def test_fp6_entries_report_their_workspace(lib):
     } | {(layout, kt.EPI_KIND_PLAIN, kt.SCALE_SUBCHANNEL) for layout in layouts}
     for d in fp6:
         if d.scale_mode == kt.SCALE_SUBCHANNEL:
-            # 128 x 128 tiles, three 24 KiB stages and the 6 KiB scale ring; groups of 64, 128 or 256
-            assert (d.block_m, d.block_n, d.num_stages, d.lds_bytes) == (128, 128, 3, 79872)
-            assert (d.min_subchannel, d.max_subchannel) == (64, 256)
+            # 128 x 128 tiles, three 24 KiB stages and the 8 KiB scale ring; groups of 32 to 256
+            assert (d.block_m, d.block_n, d.num_stages, d.lds_bytes) == (128, 128, 3, 81920)
+            assert (d.min_subchannel, d.max_subchannel) == (32, 256)
         else:
             assert d.block_m == 256 and d.num_stages == 3 and d.lds_bytes == 148480
         assert d.dtype_bits == 4

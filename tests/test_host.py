@@ -69,13 +69,15 @@ def test_registry_is_built_from_the_table():
          (4096, 4096, 4096), (128, 128)),
         (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 64), shk.Epilogue.NONE,
          (4096, 4096, 4160), (64, 64)),
+        (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 32), shk.Epilogue.RELU2,
+         (4096, 16384, 4096), (128, 128)),
     ],
 )
 def test_select_picks_the_fastest_then_the_largest_fitting_tile(dtype, scale, epilogue, shape, tile):
     """Measured MI355X throughput ranks first (C2-C4 pick the measured fp6
     and int8 32x32 entries, C1 the measured skinny tiles, the tallest of
-    them, subchannel 64 the fp6 subchannel entry), tile area next (subchannel
-    64 with K not a multiple of the 128-K tiles)."""
+    them, subchannel 32 and 64 the fp6 subchannel entry), tile area next
+    (subchannel 64 with K not a multiple of the 128-K tiles)."""
     m, n, k = shape
     kernel = shk.default_registry.select(dtype=dtype, scale=scale, epilogue=epilogue, m=m, n=n, k=k)
     assert (kernel.tile.block_m, kernel.tile.block_n) == tile
