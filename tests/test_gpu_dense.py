@@ -202,8 +202,13 @@ def test_config_c2_8192_cubed(device):
     assert np.array_equal(got, want)
 
 
-def test_config_c3_subchannel_relu2(device):
-    got, want, _ = _big_dense(device, bits=4, m=4096, n=16384, k=4096, sub=256, epilogue="relu2", seed=3)
+@pytest.mark.parametrize("sub", [256, 128, 64, 32])
+def test_config_c3_subchannel_relu2(sub, device):
+    """C3 at full size, every output checked, for every group size the fp6
+    subchannel tile serves (256 is the BASELINE config): 16 to 128 groups
+    folded in order, groups of 32 two to a 64-K stage."""
+    print(f"case C3 shape subchannel {sub}", flush=True)
+    got, want, _ = _big_dense(device, bits=4, m=4096, n=16384, k=4096, sub=sub, epilogue="relu2", seed=3)
     assert got.shape == (4096, 16384)
     assert np.array_equal(got, want)
 
