@@ -168,22 +168,28 @@ class KernelDesc:
 # 256 bytes of B scales in LDS past the stage ring (shk_f6.h).
 MFMA32_SCALE_BYTES = 4 * 256
 
-# Skinny (STREAM) tiles: 4 waves, 64 output columns, wave-private rings of
-# stages of 64 source bytes per row (shk_skinny.h).
+# Skinny (STREAM) tiles: 4 waves, wave-private rings of stages of 64 source
+# bytes per row (shk_skinny.h); 64 output columns per-channel, 16 subchannel
+# (the waves share the columns and take the scale groups in turn).
 SK_NW = 4
 SK_BN = 64
+SK_BN_SUBCH = 16
 SK_TARGET_UNITS = 256
 
 
 def _sk_geometry(r: int, swiglu: bool, subch: bool) -> tuple[int, int]:
     """(ring depth, LDS bytes) of a skinny tile of r rows (SkCfg)."""
-    bnb = 2 * SK_BN if swiglu else SK_BN
-    wcols = bnb // SK_NW if subch else bnb
+    bn = SK_BN_SUBCH if subch else SK_BN
+    wcols = 2 * bn if swiglu else bn
     stage = r * 64 + wcols * 64 + ((r // 16) * 256 + 256 if subch else 0)
-    depth = 4 if SK_NW * 4 * stage <= 79872 else (3 if SK_NW * 3 * stage <= 79872 else 2)
+    tiles = (r // 16) * (wcols // 16)
+    ch = (4 if tiles == 1 else 2 if tiles == 2 else 1) if subch else 0  # groups per wave and round
+    chain = 2 * SK_NW * ch * tiles * 1024  # two rounds of scaled partials
+    budget = 79872 - chain
+    depth = 4 if SK_NW * 4 * stage <= budget else (3 if SK_NW * 3 * stage <= budget else 2)
     ring = SK_NW * depth * stage
     red = 0 if subch else SK_NW * (wcols // 16) * 1024
-    return depth, max(ring, red)
+    return depth, max(ring, red) + chain
 
 
 def sk_split_count(desc: "KernelDesc", m: int, n: int, k: int, with_workspace: bool = True) -> int:
@@ -277,7 +283,8 @@ def _sk_desc(index, bits, layout, r, *, swiglu=False, subch=False, schedule=SCHE
         scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
         min_subchannel=32 if subch else 0, max_subchannel=256 if subch else 0,
         epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
-        block_m=r, block_n=SK_BN, block_k=32, num_waves=SK_NW, num_stages=depth, lds_bytes=lds,
+        block_m=r, block_n=SK_BN_SUBCH if subch else SK_BN, block_k=32, num_waves=SK_NW, num_stages=depth,
+        lds_bytes=lds,
         group_size_m=1, operand_format=OPERANDS_STREAM, schedule=schedule, split_k=split_k)
 
 
@@ -375,8 +382,8 @@ def measured_tops(desc: KernelDesc) -> float | None:
     fp6 int4 per-channel 256x256 (C2, 8192^3), fp6 int4 SwiGLU 256x128
     (4096 x 2*11008 x 4096), fp6 int4 subchannel 128x128 (C3), int8 32x32
     SwiGLU 256x128 (C4) and int8 plain 256x256 (8192^3), and the skinny
-    per-channel tiles (SKINNY_TOPS).  Other entries have no measurement and
-    rank by tile area."""
+    tiles (SKINNY_TOPS, SKINNY_SUB_TOPS).  Other entries have no measurement
+    and rank by tile area."""
     if desc.family != FAMILY_DENSE or desc.schedule != SCHEDULE_STANDARD or desc.split_k > 1:
         return None
     if desc.operand_format == OPERANDS_FP6:
@@ -384,7 +391,7 @@ def measured_tops(desc: KernelDesc) -> float | None:
             return 2001.0
         return 3504.0 if desc.epilogue_kind == EPI_KIND_PLAIN else 3161.0
     if desc.operand_format == OPERANDS_STREAM:
-        return SKINNY_TOPS if desc.scale_mode == SCALE_PER_CHANNEL else None
+        return SKINNY_TOPS if desc.scale_mode == SCALE_PER_CHANNEL else SKINNY_SUB_TOPS[desc.block_m]
     if desc.dtype_bits == 8 and desc.num_stages == 4 and desc.block_m == 256:
         return 2014.0 if desc.epilogue_kind == EPI_KIND_SWIGLU else 2270.0
     return None
@@ -397,6 +404,27 @@ def measured_tops(desc: KernelDesc) -> float | None:
 # register-staged 64x64 and 128x128 tiles, which outranked it by area.  The
 # larger measured tiles keep their higher figures where they fit.
 SKINNY_TOPS = 241.0
+
+# The skinny subchannel tiles' figures by tile height: int4, N = K = 8192,
+# groups of 128; 16 rows at M = 16 (22.3 us, 96 TOPS), 32 and 64 rows at
+# M = 64 (46.6 and 56.6 us: 184 and 152 TOPS), so the 32-row tile, the
+# fastest of them at M = 64 and 192, ranks first where it fits.  They rank
+# above the register-staged subchannel tiles up to M = SKINNY_SUB_MAX_M rows:
+# at N = K = 4096 they ran 3x faster at M = 64 and 1.0-1.4x at M = 192, and
+# from M = 576 up to 1.8x slower (groups of 32 from M = 320).
+SKINNY_SUB_TOPS = {16: 96.0, 32: 184.0, 64: 152.0}
+SKINNY_SUB_MAX_M = 256
+
+
+def selection_tops(desc: KernelDesc, m: int) -> float | None:
+    """measured_tops as select ranks an entry for M rows (capi.hip
+    measured_score): the skinny subchannel tiles' figure holds up to
+    SKINNY_SUB_MAX_M rows."""
+    tops = measured_tops(desc)
+    if (tops is not None and desc.operand_format == OPERANDS_STREAM and desc.scale_mode == SCALE_SUBCHANNEL
+            and m > SKINNY_SUB_MAX_M):
+        return None
+    return tops
 
 
 def entries(family: int) -> tuple[KernelDesc, ...]:

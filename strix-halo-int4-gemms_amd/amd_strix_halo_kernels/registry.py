@@ -4,7 +4,8 @@ Same selection contract as the reference's KernelRegistry (registry.py:254-352):
 candidates must match dtype, scale spec, epilogue, layout and schedule, be
 even-K, obey the split rule, and (for ``select``) accept the shape as a tile
 multiple; among them the one with the largest (measured_tops or 0,
-BLOCK_M * BLOCK_N) wins, the first on ties.  The entries come from the gfx950
+BLOCK_M * BLOCK_N) wins, the first on ties (the skinny subchannel tiles'
+figure counts up to kernel_table.SKINNY_SUB_MAX_M rows).  The entries come from the gfx950
 kernel table (``kernel_table.TABLE``) instead of gfx1151 tile seeds: every
 dense table entry is registered once per epilogue and subchannel size it
 serves.
@@ -103,8 +104,13 @@ def iter_supported_kernel_metadata() -> Iterable[KernelMetadata]:
                 )
 
 
-def _selection_key(kernel: KernelMetadata) -> tuple[float, int]:
-    return (kernel.measured_tops or 0.0, kernel.tile.block_m * kernel.tile.block_n)
+def _selection_key(kernel: KernelMetadata, m: int) -> tuple[float, int]:
+    tops = kernel.measured_tops
+    if tops is not None and kernel.table_index is not None and m > kt.SKINNY_SUB_MAX_M:
+        desc = kt.TABLE[kernel.table_index]
+        if desc.operand_format == kt.OPERANDS_STREAM and desc.scale_mode == kt.SCALE_SUBCHANNEL:
+            tops = None  # the skinny subchannel figure holds for few rows only (kernel_table.selection_tops)
+    return (tops or 0.0, kernel.tile.block_m * kernel.tile.block_n)
 
 
 def _matches(kernel: KernelMetadata, dtype, scale, epilogue, layout, schedule, split_k) -> bool:
@@ -197,7 +203,7 @@ class KernelRegistry:
                 f"no kernel for dtype={dtype.value}, scale={scale.label}, epilogue={epilogue.value}, "
                 f"layout={layout.value}, schedule={schedule.value}, shape=({m}, {n}, {k})"
             )
-        chosen = max(candidates, key=_selection_key)
+        chosen = max(candidates, key=lambda kern: _selection_key(kern, m))
         if len(self._selected) >= 4096:  # bounded for callers that vary M call to call
             self._selected = {}
         self._selected[request] = chosen
@@ -223,7 +229,8 @@ class KernelRegistry:
                 f"no reference kernel metadata for dtype={dtype.value}, scale={scale.label}, "
                 f"epilogue={epilogue.value}, layout={layout.value}, schedule={schedule.value}"
             )
-        return max(candidates, key=_selection_key)
+        # no shape: rank as for a large M (the skinny subchannel figure applies to few rows only)
+        return max(candidates, key=lambda kern: _selection_key(kern, 1 << 30))
 
     def with_status(self, kernel_id: str, status: KernelStatus, **updates: object) -> "KernelRegistry":
         copied = KernelRegistry(self._kernels.values())

@@ -491,14 +491,17 @@ namespace {
 // Throughput measured on MI355X for the entries the benchmark configurations
 // time (the Python registry's kernel_table.measured_tops): the first
 // ranking key of a selection, before the tile area.
-double measured_score(const shk_kernel_desc& d) {
+double measured_score(const shk_kernel_desc& d, int m) {
   if (d.schedule != SHK_SCHEDULE_STANDARD || d.split_k > 1) return 0.0;
   if (d.operand_format == SHK_OPERANDS_FP6) {
     if (d.scale_mode == SHK_SCALE_SUBCHANNEL) return 2001.0;
     return d.epilogue_kind == SHK_EPI_KIND_PLAIN ? 3504.0 : 3161.0;
   }
-  if (d.operand_format == SHK_OPERANDS_STREAM)  // the skinny per-channel tiles
-    return d.scale_mode == SHK_SCALE_PER_CHANNEL ? 241.0 : 0.0;
+  if (d.operand_format == SHK_OPERANDS_STREAM) {  // the skinny tiles (subchannel: by tile height, up to 256 rows)
+    if (d.scale_mode == SHK_SCALE_PER_CHANNEL) return 241.0;
+    if (m > 256) return 0.0;
+    return d.block_m == 16 ? 96.0 : (d.block_m == 32 ? 184.0 : 152.0);
+  }
   if (d.dtype_bits == 8 && d.num_stages == 4 && d.block_m == 256)
     return d.epilogue_kind == SHK_EPI_KIND_SWIGLU ? 2014.0 : 2270.0;
   return 0.0;
@@ -557,7 +560,7 @@ int amd_strix_halo_kernels_select_dense(int32_t dtype_bits, int32_t layout, int3
     const shk_kernel_desc& d = t[i].d;
     if (!serves_family(d, dtype_bits, layout, subchannel, epilogue, schedule, split_k)) continue;
     if (!accepts_shape(d, m, n, k, subchannel)) continue;
-    const double score = measured_score(d);
+    const double score = measured_score(d, m);
     const long area = (long)d.block_m * d.block_n;
     if (score > best_score || (score == best_score && area > best_area)) {
       best = i;

@@ -36,9 +36,12 @@
 //    tile's slots and counter), since the counters of one shape can lie
 //    where the partials of another were.
 //  * Subchannel scales: each group's partial must be scaled and folded into
-//    the fp32 total in group order, so the waves split the columns (WOUT =
-//    16) and every wave folds its groups in order, with the group scales
-//    brought into the stage slots by LDS-DMA.
+//    the fp32 total in group order.  The four waves share the tile's 16
+//    output columns (GSPLIT) and take the groups in turn: in round r wave w
+//    multiplies group 4r + w and scales its integer partial; the four scaled
+//    partials meet in LDS, and after the round's barrier wave 0 adds them
+//    into the totals in group order (sk_unit_sc).  The group scales come
+//    into the stage slots by LDS-DMA.
 //
 // Fragment layout.  v_mfma_i32_16x16x64_i8 takes B as its first operand
 // (D rows = output columns) and A as its second (D columns = output rows);
@@ -76,8 +79,8 @@ constexpr int SK_MAX_WAVE_STAGES_I4 = 1023;
 constexpr int sk_stage_bytes(int r, int wcols, bool subch) {
   return r * 64 + wcols * 64 + (subch ? (r / 16) * 256 + 256 : 0);
 }
-constexpr int sk_ring_depth(int stage, int nw) {
-  const int budget = nw >= 8 ? 153600 : 79872;
+constexpr int sk_ring_depth(int stage, int nw, int reserved = 0) {
+  const int budget = (nw >= 8 ? 153600 : 79872) - reserved;  // reserved: LDS the tile uses beside the rings
   return nw * 4 * stage <= budget ? 4 : (nw * 3 * stage <= budget ? 3 : 2);
 }
 
@@ -96,9 +99,10 @@ struct SkCfg {
   static constexpr int NT = 64 * NW;
   static constexpr int WOUT = WOUT_;                  // output columns per wave (0: waves split K)
   static constexpr bool KSPLIT = WOUT == 0;
-  static constexpr int BN = KSPLIT ? BNK_ : NW * WOUT;  // output columns of a tile
+  static constexpr bool GSPLIT = SUBCH;              // the waves share WOUT columns and split the groups
+  static constexpr int BN = KSPLIT ? BNK_ : (GSPLIT ? WOUT : NW * WOUT);  // output columns of a tile
   static constexpr int BNB = SWIGLU ? 2 * BN : BN;    // B columns of a tile ([up | gate] for SwiGLU)
-  static constexpr int WCOLS = KSPLIT ? BNB : BNB / NW;  // B columns a wave loads and multiplies
+  static constexpr int WCOLS = KSPLIT || GSPLIT ? BNB : BNB / NW;  // B columns a wave loads and multiplies
   static constexpr int CT = WCOLS / 16;              // 16-column B tiles of a wave
   static constexpr int FT = KSPLIT ? 1 : WOUT / 16;   // 16-column output tiles a wave writes
   static constexpr int NFIN = KSPLIT ? BN / 16 : NW;  // waves that write output (K-split: one tile each)
@@ -114,10 +118,15 @@ struct SkCfg {
   static constexpr int A_DMA = A_BYTES / 1024;
   static constexpr int B_DMA = B_BYTES / 1024;
   static constexpr int DPS = A_DMA + B_DMA + (SUBCH ? RT + 1 : 0);  // DMA loads per stage
-  static constexpr int D = DEPTH_ > 0 ? DEPTH_ : sk_ring_depth(STAGE, NW);
+  // GSPLIT: each wave takes CH consecutive groups per round; two rounds'
+  // scaled partials, one 16 x 16 tile (1 KiB) per wave, group, row tile and
+  // B column tile, follow the rings
+  static constexpr int CH = !GSPLIT ? 0 : (RT * CT == 1 ? 4 : (RT * CT == 2 ? 2 : 1));
+  static constexpr int CHAIN = GSPLIT ? 2 * NW * CH * RT * CT * 1024 : 0;
+  static constexpr int D = DEPTH_ > 0 ? DEPTH_ : sk_ring_depth(STAGE, NW, CHAIN);
   static constexpr int RING = NW * D * STAGE;
   static constexpr int RED = KSPLIT ? NW * CT * 1024 : 0;  // one row tile of the cross-wave sum
-  static constexpr int LDS_BYTES = RING > RED ? RING : RED;
+  static constexpr int LDS_BYTES = (RING > RED ? RING : RED) + CHAIN;
   static constexpr int SHIFT = BITS == 4 ? 8 : 0;  // int4 accumulators hold 256 * sum
   static_assert(STAGE == A_BYTES + B_BYTES + SA_BYTES + SB_BYTES, "stage layout");
   static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole DMA blocks per stage");
@@ -125,7 +134,8 @@ struct SkCfg {
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
   static_assert(!KSPLIT || NFIN <= NW, "a K-split tile has a wave for each output column tile");
   static_assert(!KSPLIT || BN == 32 || BN == 64, "K-split tiles are 32 or 64 columns wide");
-  static_assert(!SUBCH || WOUT == 16, "subchannel tiles give each wave 16 output columns");
+  static_assert(!SUBCH || WOUT == 16 || (WOUT == 32 && !SWIGLU),
+                "subchannel tiles: 16 output columns, or 32 without SwiGLU (one 256-byte b_scale load per stage)");
   static_assert(KSPLIT || WOUT % 16 == 0, "whole 16-column tiles per wave");
 };
 
@@ -268,6 +278,8 @@ struct SkEngine {
   // rounded down to 4 bytes (sa_mis = 0 or 2 bytes past it)
   v4i rss_a, rss_b;
   uint32_t sb_voff, sa_mis;
+  int sh;                  // log2 of the group size (a power of two, 32 .. 256)
+  uint32_t sa_row[C::RT];  // element index m * G + lane / 16 of the lane's a_scale load, per row tile
 
   __device__ __forceinline__ SkEngine(const DenseArgs& args, uint8_t* smem, int lane_, int wave_, int m0_, int n0_)
       : p(args), lane(lane_), wave(wave_), m0(m0_), n0(n0_) {
@@ -289,8 +301,9 @@ struct SkEngine {
         return (uint32_t)(nn0 + t);
       } else {
         constexpr int WO = C::WOUT;
-        if constexpr (C::SWIGLU) return (uint32_t)(t < WO ? nn0 + WO * w + t : N + nn0 + WO * w + t - WO);
-        return (uint32_t)(nn0 + WO * w + t);
+        const int wo = C::GSPLIT ? 0 : WO * w;  // GSPLIT: every wave takes the tile's columns
+        if constexpr (C::SWIGLU) return (uint32_t)(t < WO ? nn0 + wo + t : N + nn0 + wo + t - WO);
+        return (uint32_t)(nn0 + wo + t);
       }
     };
     pb.init(lane, ldb, [=](uint32_t r) { return bcol((int)r) * ldb; }, [=](uint32_t u) { return bcol(16 * (int)u); });
@@ -304,9 +317,13 @@ struct SkEngine {
       rss_b = buffer_words(p.b_scale, 2ull * (unsigned long long)p.scale_cols * p.b_cols);
       // lane = 16 j + e: group slot j, dword e % 8 of piece e / 8 (up, gate)
       const int j = lane >> 4, e = lane & 15;
-      const int piece = C::SWIGLU ? (e >> 3) : 0;
+      const int piece = C::CT == 2 ? (e >> 3) : 0;  // 16-column piece (SwiGLU: up, gate)
       const int col = (int)bcol(16 * piece) + 2 * (e & 7);
       sb_voff = 2u * (uint32_t)(j * p.b_cols + col);
+      sh = __builtin_ctz((unsigned)p.subchannel);
+#pragma unroll
+      for (int rt = 0; rt < C::RT; ++rt)
+        sa_row[rt] = (uint32_t)((m0 + 16 * rt + (lane & 15)) * p.scale_cols + (lane >> 4));
     }
   }
 
@@ -316,13 +333,11 @@ struct SkEngine {
     pa.issue(rsa, PA::soff(st, (uint32_t)p.lda), base);
     pb.issue(rsb, PB::soff(st, (uint32_t)p.ldb), base + C::A_BYTES);
     if constexpr (C::SUBCH) {
-      const int g0 = st * C::KS / p.subchannel;
+      const int g0 = (st * C::KS) >> sh;  // the first group of the stage
       // a-scale dword holding element (m, g0 + j) of row m = m0 + 16 rt + lane % 16
 #pragma unroll
-      for (int rt = 0; rt < C::RT; ++rt) {
-        const long e = (long)(m0 + 16 * rt + (lane & 15)) * p.scale_cols + g0 + (lane >> 4);
-        lds_dma4(rss_a, (sa_mis + 2u * (uint32_t)e) & ~3u, 0u, base + SA_OFF + 256u * rt);
-      }
+      for (int rt = 0; rt < C::RT; ++rt)
+        lds_dma4(rss_a, (sa_mis + 2u * (sa_row[rt] + (uint32_t)g0)) & ~3u, 0u, base + SA_OFF + 256u * rt);
       lds_dma4(rss_b, sb_voff, 2u * (uint32_t)g0 * (uint32_t)p.b_cols, base + SB_OFF);
     }
   }
@@ -567,21 +582,32 @@ __device__ __forceinline__ void sk_unit_pc(const DenseArgs& p, uint8_t* smem, in
 }
 
 // ---------------------------------------------------------------------------
-// Subchannel tile: each wave multiplies 16 output columns over all of K and
-// folds every group in order: tot += (float(sum_g) * a_scale[m, g]) *
-// b_scale[g, n] (api.py:311-325), or, in the raw mode, adds sum_g.
+// Subchannel tile (GSPLIT): the four waves share the tile's 16 output
+// columns (and the gate's 16 for SwiGLU) and take its groups in chunks of
+// CH consecutive groups: in round r, wave w multiplies chunk 4r + w (its
+// stages, or for chunks shorter than a stage its groups' steps of one
+// stage, the A fragments of the other lanes zeroed for groups of 32) and
+// scales each group's integer partial,
+// x = (float(sum_g) * a_scale[m, g]) * b_scale[g, n] (api.py:311-325).  The
+// round's 4 CH values of x go through LDS; after the round's barrier wave 0
+// adds them into the totals in group order, which is the reference's order
+// of the sums (the raw mode adds the integer partials).  Wave 0 stores the
+// tile.
 
+// x of one group from its integer partials and the scales in the stage slot
+// (j: the group's slot among the stage's scales; odd_a[rt]: whether the
+// lane's a_scale element of group 0 is the high half of its dword).
 template <class C>
-__device__ __forceinline__ void sk_fold(const DenseArgs& p, const uint8_t* slot, int j, int gidx, int lane, int m0,
-                                        uint32_t sa_mis, v4i (&acc)[C::RT][C::CT], float (&tot)[C::RT][C::CT][4]) {
+__device__ __forceinline__ void sk_scale_group(const DenseArgs& p, const uint8_t* slot, int j, int g, int lane,
+                                               const int (&odd_a)[C::RT], const v4i (&acc)[C::RT][C::CT],
+                                               v4i (&x)[C::RT][C::CT]) {
   if (p.out_mode == OUT_I32) {
 #pragma unroll
     for (int rt = 0; rt < C::RT; ++rt)
 #pragma unroll
       for (int c = 0; c < C::CT; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          tot[rt][c][q] = __int_as_float(__float_as_int(tot[rt][c][q]) + (acc[rt][c][q] >> C::SHIFT));
+        for (int q = 0; q < 4; ++q) x[rt][c][q] = acc[rt][c][q] >> C::SHIFT;
     return;
   }
   float sb[C::CT][4];
@@ -590,10 +616,8 @@ __device__ __forceinline__ void sk_fold(const DenseArgs& p, const uint8_t* slot,
     sk_bf16x4(sk_ld64(slot + SkEngine<C>::SB_OFF + 64 * j + 32 * c + 8 * (lane >> 4)), sb[c]);
 #pragma unroll
   for (int rt = 0; rt < C::RT; ++rt) {
-    const int m = m0 + 16 * rt + (lane & 15);
     const uint32_t w = sk_ld32(slot + SkEngine<C>::SA_OFF + 256 * rt + 4 * (16 * j + (lane & 15)));
-    const long eidx = (long)m * p.scale_cols + gidx + (sa_mis >> 1);
-    const float sa = __uint_as_float((eidx & 1) ? (w & 0xFFFF0000u) : (w << 16));
+    const float sa = __uint_as_float(((odd_a[rt] + g) & 1) ? (w & 0xFFFF0000u) : (w << 16));
 #pragma unroll
     for (int c = 0; c < C::CT; ++c)
 #pragma unroll
@@ -601,102 +625,173 @@ __device__ __forceinline__ void sk_fold(const DenseArgs& p, const uint8_t* slot,
         float v = (float)(acc[rt][c][q] >> C::SHIFT);
         v = v * sa;
         v = v * sb[c][q];
-        tot[rt][c][q] = tot[rt][c][q] + v;
+        x[rt][c][q] = __float_as_int(v);
       }
   }
 }
 
 template <class C>
 __device__ __forceinline__ void sk_unit_sc(const DenseArgs& p, uint8_t* smem, int lane, int wave, int tm, int tn) {
+  static_assert(C::GSPLIT && C::NW == 4, "four waves take the groups in turn");
   SkEngine<C> e(p, smem, lane, wave, tm * C::R, tn * C::BN);
-  const int nst = (p.K + C::KS - 1) / C::KS;
-  const int S = p.subchannel;
-  const int G = p.scale_cols;
-  const int g = lane >> 4;
-
-  float tot[C::RT][C::CT][4];
-  v4i acc[C::RT][C::CT], acc2[C::RT][C::CT];
-#pragma unroll
-  for (int rt = 0; rt < C::RT; ++rt)
-#pragma unroll
-    for (int c = 0; c < C::CT; ++c) {
-      acc[rt][c] = v4i{0, 0, 0, 0};
-      acc2[rt][c] = v4i{0, 0, 0, 0};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) tot[rt][c][q] = 0.0f;
-    }
-
-#pragma unroll
-  for (int i = 0; i < C::D - 1; ++i)
-    if (i < nst) e.issue(i, i);
-  for (int st = 0; st < nst; ++st) {
-    const bool ahead = st + C::D - 1 < nst;
-    if (ahead) {
-      sk_lds_drain();
-      e.issue(st + C::D - 1, (st + C::D - 1) % C::D);
-    }
-    sk_wait<(C::D - 1) * C::DPS>(ahead);
-    const uint8_t* slot = e.ringp + (st % C::D) * C::STAGE;
-    const int g0 = st * C::KS / S;
-#pragma unroll
-    for (int s = 0; s < C::STEPS; ++s) {
-      const int kb = st * C::KS + 64 * s;
-      if (kb >= p.K) break;
-      const bool kin = kb + 16 * g < p.K;
-      v4i y[C::RT], x[C::CT];
-#pragma unroll
-      for (int rt = 0; rt < C::RT; ++rt) {
-        const v4i f = SkEngine<C>::PA::template frag<C::BITS>(slot, rt, s, lane);
-        y[rt] = kin ? f : v4i{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int c = 0; c < C::CT; ++c) x[c] = SkEngine<C>::PB::template frag<C::BITS>(slot + C::A_BYTES, c, s, lane);
-      if (S == 32) {
-        // two groups per step: lanes 0-31 carry K [kb, kb + 32), lanes 32-63 the next 32
-        const v4i z{0, 0, 0, 0};
-#pragma unroll
-        for (int rt = 0; rt < C::RT; ++rt)
-#pragma unroll
-          for (int c = 0; c < C::CT; ++c) {
-            acc[rt][c] = mfma64(x[c], g < 2 ? y[rt] : z, z);
-            acc2[rt][c] = mfma64(x[c], g < 2 ? z : y[rt], z);
-          }
-        const int ga = kb / 32;
-        sk_fold<C>(p, slot, ga - g0, ga, lane, e.m0, e.sa_mis, acc, tot);
-        if (ga + 1 < G) sk_fold<C>(p, slot, ga + 1 - g0, ga + 1, lane, e.m0, e.sa_mis, acc2, tot);
-      } else {
-#pragma unroll
-        for (int rt = 0; rt < C::RT; ++rt)
-#pragma unroll
-          for (int c = 0; c < C::CT; ++c) acc[rt][c] = mfma64(x[c], y[rt], acc[rt][c]);
-        if ((kb + 64) % S == 0) {
-          const int gi = kb / S;
-          sk_fold<C>(p, slot, gi - g0, gi, lane, e.m0, e.sa_mis, acc, tot);
-#pragma unroll
-          for (int rt = 0; rt < C::RT; ++rt)
-#pragma unroll
-            for (int c = 0; c < C::CT; ++c) acc[rt][c] = v4i{0, 0, 0, 0};
-        }
-      }
-    }
-  }
-  wait_vmcnt<0>();
-
-  const int n = e.n0 + 16 * wave + 4 * g;
+  constexpr int KSH = C::BITS == 4 ? 7 : 6;  // log2(KS)
+  static_assert((1 << KSH) == C::KS, "stage K");
+  constexpr int CH = C::CH;
+  constexpr int CHSH = CH == 4 ? 2 : (CH == 2 ? 1 : 0);
+  static_assert((1 << CHSH) == CH, "CH is a power of two");
+  const int sh = e.sh;
+  const int S = 1 << sh;
+  const int G = p.scale_cols;                   // K / S
+  const int nch = (G + CH - 1) >> CHSH;         // chunks of CH groups
+  const int lsh = sh + CHSH;                    // log2 of a chunk's K
+  const int spc_sh = lsh > KSH ? lsh - KSH : 0;
+  const int spc = 1 << spc_sh;                  // stages per chunk (a chunk shorter than a stage: 1)
+  const int rounds = (nch + 3) >> 2;
+  const int my_chunks = wave < nch ? ((nch - 1 - wave) >> 2) + 1 : 0;
+  const int n_i = my_chunks << spc_sh;          // this wave's stages
+  const int lg = lane >> 4;
+  // this wave's stage i: stage i % spc of chunk 4 (i / spc) + wave
+  auto stage_of = [&](int i) { return (((4 * (i >> spc_sh) + wave) << lsh) >> KSH) + (i & (spc - 1)); };
+  uint8_t* chain = smem + (C::LDS_BYTES - C::CHAIN);
+  auto chain_at = [&](int par, int w, int cg, int rt, int c) {
+    return chain + ((((par * C::NW + w) * CH + cg) * C::RT + rt) * C::CT + c) * 1024 + 16 * lane;
+  };
+  int odd_a[C::RT];
 #pragma unroll
   for (int rt = 0; rt < C::RT; ++rt) {
     const int m = e.m0 + 16 * rt + (lane & 15);
-    float up[4], gt[4];
-    int iu[4], ig[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      up[q] = tot[rt][0][q];
-      gt[q] = tot[rt][C::CT - 1][q];
-      iu[q] = __float_as_int(up[q]);
-      ig[q] = __float_as_int(gt[q]);
-    }
-    sk_store<C>(p, m, n, up, gt, iu, ig);
+    odd_a[rt] = ((m & p.scale_cols) + (int)(e.sa_mis >> 1)) & 1;  // parity of m * G + sa_mis / 2
   }
+  // one 64-K MFMA step of a stage into a; A fragments zeroed off the lanes `on`
+  auto step = [&](const uint8_t* slot, int s, bool on, v4i (&a)[C::RT][C::CT]) {
+    v4i y[C::RT], xb[C::CT];
+#pragma unroll
+    for (int rt = 0; rt < C::RT; ++rt) {
+      const v4i f = SkEngine<C>::PA::template frag<C::BITS>(slot, rt, s, lane);
+      y[rt] = on ? f : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int c = 0; c < C::CT; ++c) xb[c] = SkEngine<C>::PB::template frag<C::BITS>(slot + C::A_BYTES, c, s, lane);
+#pragma unroll
+    for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+      for (int c = 0; c < C::CT; ++c) a[rt][c] = mfma64(xb[c], y[rt], a[rt][c]);
+  };
+  auto clear = [](v4i (&a)[C::RT][C::CT]) {
+#pragma unroll
+    for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+      for (int c = 0; c < C::CT; ++c) a[rt][c] = v4i{0, 0, 0, 0};
+  };
+  // group g's partials, scaled, into its place of the round's chain buffer
+  auto put = [&](const uint8_t* slot, int st, int g, int k, int par, const v4i (&a)[C::RT][C::CT]) {
+    v4i x[C::RT][C::CT];
+    sk_scale_group<C>(p, slot, g - ((st << KSH) >> sh), g, lane, odd_a, a, x);
+#pragma unroll
+    for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+      for (int c = 0; c < C::CT; ++c) sk_st128(chain_at(par, wave, g - (k << CHSH), rt, c), x[rt][c]);
+  };
+
+  float tot[C::RT][C::CT][4];
+#pragma unroll
+  for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+    for (int c = 0; c < C::CT; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) tot[rt][c][q] = 0.0f;
+
+#pragma unroll
+  for (int d = 0; d < C::D - 1; ++d)
+    if (d < n_i) e.issue(stage_of(d), d);
+  v4i acc[C::RT][C::CT];
+  clear(acc);
+  int i = 0;
+  for (int r = 0; r < rounds; ++r) {
+    const int k = 4 * r + wave;  // this wave's chunk: groups [k CH, (k + 1) CH)
+    const int par = r & 1;
+    if (k < nch) {
+      for (int j = 0; j < spc; ++j, ++i) {
+        const bool ahead = i + C::D - 1 < n_i;
+        if (ahead) {
+          sk_lds_drain();
+          e.issue(stage_of(i + C::D - 1), (i + C::D - 1) % C::D);
+        }
+        sk_wait<(C::D - 1) * C::DPS>(ahead);
+        const uint8_t* slot = e.ringp + (i % C::D) * C::STAGE;
+        const int st = stage_of(i);
+        if (S >= C::KS) {
+          // the stage is part of group (st KS) / S, whose last stage folds it
+#pragma unroll
+          for (int s = 0; s < C::STEPS; ++s) step(slot, s, (st << KSH) + 64 * s + 16 * lg < p.K, acc);
+          if ((((st + 1) << KSH) & (S - 1)) == 0) {
+            put(slot, st, (st << KSH) >> sh, k, par, acc);
+            clear(acc);
+          }
+        } else {
+          // groups q of the stage that belong to the chunk: K [q S, (q + 1) S)
+          // of the stage, one step (S = 64) or one half of one (S = 32)
+          const int gs = (st << KSH) >> sh;
+#pragma unroll
+          for (int q = 0; q < C::KS / 32; ++q) {
+            const int g = gs + q;
+            if ((q << sh) >= C::KS || g < (k << CHSH) || g >= ((k + 1) << CHSH) || g >= G) continue;
+            const int s = (q << sh) >> 6;
+            const int kb = (st << KSH) + 64 * s;
+            const bool on = (S >= 64 || (lg >> 1) == (q & 1)) && kb + 16 * lg < p.K;
+            v4i a[C::RT][C::CT];
+            clear(a);
+            step(slot, s, on, a);
+            put(slot, st, g, k, par, a);
+          }
+        }
+      }
+    }
+    // the round's partials are in LDS (no wait on the wave-private DMA)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int cg = 0; cg < CH; ++cg) {
+          if ((((4 * r + w) << CHSH) + cg) >= G) continue;
+#pragma unroll
+          for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+            for (int c = 0; c < C::CT; ++c) {
+              const v4i v = sk_ld128(chain_at(par, w, cg, rt, c));
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                if (p.out_mode == OUT_I32)
+                  tot[rt][c][q] = __int_as_float(__float_as_int(tot[rt][c][q]) + v[q]);
+                else
+                  tot[rt][c][q] = tot[rt][c][q] + __int_as_float(v[q]);
+              }
+            }
+        }
+    }
+  }
+  wait_vmcnt<0>();
+  if (wave != 0) return;
+
+  constexpr int OT = C::SWIGLU ? C::CT / 2 : C::CT;  // 16-column output tiles (SwiGLU: the gate's follow)
+#pragma unroll
+  for (int rt = 0; rt < C::RT; ++rt)
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot) {
+      const int m = e.m0 + 16 * rt + (lane & 15);
+      const int n = e.n0 + 16 * ot + 4 * lg;
+      float up[4], gt[4];
+      int iu[4], ig[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        up[q] = tot[rt][ot][q];
+        gt[q] = tot[rt][C::SWIGLU ? ot + OT : ot][q];
+        iu[q] = __float_as_int(up[q]);
+        ig[q] = __float_as_int(gt[q]);
+      }
+      sk_store<C>(p, m, n, up, gt, iu, ig);
+    }
 }
 
 // One workgroup per unit (standard schedule) or one per resident slot,

@@ -71,13 +71,19 @@ def test_registry_is_built_from_the_table():
          (4096, 4096, 4160), (64, 64)),
         (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 32), shk.Epilogue.RELU2,
          (4096, 16384, 4096), (128, 128)),
+        (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 128), shk.Epilogue.NONE,
+         (64, 4096, 4096), (32, 16)),
+        (shk.OperandDType.INT4, shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, 128), shk.Epilogue.NONE,
+         (576, 4096, 4096), (64, 64)),
     ],
 )
 def test_select_picks_the_fastest_then_the_largest_fitting_tile(dtype, scale, epilogue, shape, tile):
     """Measured MI355X throughput ranks first (C2-C4 pick the measured fp6
     and int8 32x32 entries, C1 the measured skinny tiles, the tallest of
-    them, subchannel 32 and 64 the fp6 subchannel entry), tile area next
-    (subchannel 64 with K not a multiple of the 128-K tiles)."""
+    them, subchannel 32 and 64 the fp6 subchannel entry, subchannel M = 64
+    the 32-row skinny subchannel tile, whose figure holds up to 256 rows), tile
+    area next (subchannel 64 with K not a multiple of the 128-K tiles,
+    subchannel M = 576)."""
     m, n, k = shape
     kernel = shk.default_registry.select(dtype=dtype, scale=scale, epilogue=epilogue, m=m, n=n, k=k)
     assert (kernel.tile.block_m, kernel.tile.block_n) == tile
@@ -85,7 +91,8 @@ def test_select_picks_the_fastest_then_the_largest_fitting_tile(dtype, scale, ep
     fitting = [c for c in shk.default_registry.all() if c.scale == scale and c.epilogue is epilogue
                and c.a_dtype is dtype and c.layout is kernel.layout
                and not tile_multiple_rejection_reasons(c, LaunchShape(m, n, k))]
-    assert (kernel.measured_tops or 0) == max(c.measured_tops or 0 for c in fitting)
+    assert (kt.selection_tops(kt.TABLE[kernel.table_index], m) or 0) == max(
+        kt.selection_tops(kt.TABLE[c.table_index], m) or 0 for c in fitting)
 
 
 def test_select_raises_for_shapes_no_kernel_accepts():
