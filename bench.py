@@ -7,11 +7,12 @@ C3 (int4 subchannel-256 ReLU2, 4096x16384x4096), C4 (int8 fused SwiGLU,
 4096 x 11008 x 4096, TOPS count up + gate), C5 (ragged MoE forward and
 K-ragged backward, G=8, M=8192, K=2048, N=1408), the C2 persistent schedule,
 the device quantize-and-pack of a C2-sized bf16 operand (GB/s against HBM),
-and the decode-sized skinny GEMM (int4 per-channel, M=16, N=K=8192; GB/s
-against HBM, weights streamed from HBM and MALL-resident).
+and the decode-sized skinny GEMM (int4 per-channel and with scale groups of
+128, M=16, N=K=8192; GB/s against HBM, weights streamed from HBM and
+MALL-resident).
 
     python bench.py [--steps K] [--warmup W] [--no-secondary] [--no-cpu-baseline]
-                    [--only c2|c3|c4|c5|c2p|quant|skinny]
+                    [--only c2|c3|c4|c5|c2p|quant|skinny|skinny_sc]
 
 A step is one API call over operands already resident in HBM; the timed region
 is exactly K steps bracketed by a device synchronisation on both sides.
@@ -344,9 +345,10 @@ SKINNY_COPIES = 16  # distinct 32 MiB weight matrices cycled by the HBM figure (
 SKINNY_LAUNCHES = 64  # launches per captured graph
 
 
-def bench_skinny(torch, shk, steps, warmup):
-    """Decode-sized int4 per-channel GEMM, M = 16, N = K = 8192, on the skinny
-    tile (packed B streamed straight from HBM), against the HBM roofline.
+def bench_skinny(torch, shk, steps, warmup, subchannel=None):
+    """Decode-sized int4 GEMM, M = 16, N = K = 8192, per-channel or with
+    subchannel scale groups (GPTQ-style groups of 128), on the skinny tile
+    (packed B streamed straight from HBM), against the HBM roofline.
 
     Device time per launch: HIP events around the replay of a HIP graph of
     SKINNY_LAUNCHES back-to-back C-ABI launches (no host work between them),
@@ -359,14 +361,16 @@ def bench_skinny(torch, shk, steps, warmup):
     from amd_strix_halo_kernels import native
 
     m, n, k = 16, 8192, 8192
+    s = subchannel or 0
     gen = torch.Generator(device="cuda").manual_seed(6)
     a = _rand_int4_packed(torch, m, k, gen)
     bs = [torch.randint(0, 256, (k // 2, n), dtype=torch.uint8, device="cuda", generator=gen)
           for _ in range(SKINNY_COPIES)]
-    sa = _uniform_bf16(torch, (m,), 0.005, 0.02, gen)
-    sbs = [_uniform_bf16(torch, (n,), 0.005, 0.02, gen) for _ in range(SKINNY_COPIES)]
-    kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL),
-                                         epilogue=shk.Epilogue.NONE, m=m, n=n, k=k)
+    sa = _uniform_bf16(torch, (m, k // s) if s else (m,), 0.005, 0.02, gen)
+    sbs = [_uniform_bf16(torch, (k // s, n) if s else (n,), 0.005, 0.02, gen) for _ in range(SKINNY_COPIES)]
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, s) if s else shk.ScaleSpec(shk.ScaleMode.PER_CHANNEL)
+    kernel = shk.default_registry.select(dtype=shk.OperandDType.INT4, scale=spec, epilogue=shk.Epilogue.NONE,
+                                         m=m, n=n, k=k)
     desc = kt.TABLE[kernel.table_index]
     lib = native.load_dispatch_library()
     ws = desc.workspace_bytes(m, n, k)
@@ -377,20 +381,21 @@ def bench_skinny(torch, shk, steps, warmup):
     def launch(i, stream):
         rc = lib.amd_strix_halo_kernels_launch_gemm_ws(
             kernel.table_index, dev, stream, a.data_ptr(), bs[i].data_ptr(), sa.data_ptr(), sbs[i].data_ptr(),
-            out.data_ptr(), m, n, k, 0, kt.EPILOGUE_NONE, kt.OUT_BF16, work.data_ptr() if ws else None, ws)
+            out.data_ptr(), m, n, k, s, kt.EPILOGUE_NONE, kt.OUT_BF16, work.data_ptr() if ws else None, ws)
         if rc:
             raise RuntimeError(lib.amd_strix_halo_kernels_last_error().decode())
 
     launch(0, torch.cuda.current_stream().cuda_stream)
-    want = shk.mm(a, bs[0], a_scale=sa, b_scale=sbs[0])
+    want = shk.mm(a, bs[0], a_scale=sa, b_scale=sbs[0], scale=spec)
     torch.cuda.synchronize()
     if not torch.equal(want, out):
         raise RuntimeError("skinny: the direct launch differs from mm()")
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
-    nbytes = m * k // 2 + k * n // 2 + 2 * m + 2 * n + 2 * m * n
-    res = {"m": m, "n": n, "k": k, "kernel": kernel.kernel_id, "splits": kt.sk_split_count(desc, m, n, k),
+    nbytes = m * k // 2 + k * n // 2 + 2 * m * n + (2 * (m + n) * (k // s) if s else 2 * m + 2 * n)
+    res = {"m": m, "n": n, "k": k, "subchannel": s or None, "kernel": kernel.kernel_id,
+           "splits": kt.sk_split_count(desc, m, n, k),
            "bytes": nbytes, "launches_per_graph": SKINNY_LAUNCHES, "weight_copies": SKINNY_COPIES}
     for name, rotate in (("warm", False), ("hbm", True)):
         graph = torch.cuda.CUDAGraph()
@@ -416,11 +421,11 @@ def bench_skinny(torch, shk, steps, warmup):
         del graph
     # the last replay's last launch read weight copy (SKINNY_LAUNCHES - 1) % SKINNY_COPIES
     last = (SKINNY_LAUNCHES - 1) % SKINNY_COPIES
-    if not torch.equal(shk.mm(a, bs[last], a_scale=sa, b_scale=sbs[last]), out):
+    if not torch.equal(shk.mm(a, bs[last], a_scale=sa, b_scale=sbs[last], scale=spec), out):
         raise RuntimeError("skinny: the graph replay's output differs from mm()")
     res["frac_hbm"] = res["hbm_gbs"] / HBM_PEAK_GBS
     res["warm_frac_hbm"] = res["warm_gbs"] / HBM_PEAK_GBS
-    wall, _, _ = _time_steps(torch, lambda: shk.mm(a, bs[0], a_scale=sa, b_scale=sbs[0]), steps, warmup)
+    wall, _, _ = _time_steps(torch, lambda: shk.mm(a, bs[0], a_scale=sa, b_scale=sbs[0], scale=spec), steps, warmup)
     res["mm_wall_us"] = wall * 1e3
     return res
 
@@ -671,6 +676,8 @@ _ONLY = {
     "c2p": ("c2_persistent_schedule_8192_cubed", bench_c2_persistent),
     "quant": ("quantize_pack_int4_8192x8192_bf16", bench_quant),
     "skinny": ("skinny_int4_pc_16x8192x8192", bench_skinny),
+    "skinny_sc": ("skinny_int4_sc128_16x8192x8192", lambda torch, shk, steps, warmup: bench_skinny(
+        torch, shk, steps, warmup, subchannel=128)),
 }
 
 
@@ -736,6 +743,9 @@ def main(argv=None) -> int:
                                                                      args.warmup)
         _log("bench: skinny int4 per-channel 16x8192x8192")
         secondary["skinny_int4_pc_16x8192x8192"] = bench_skinny(torch, shk, max(10, args.steps // 2), args.warmup)
+        _log("bench: skinny int4 subchannel-128 16x8192x8192")
+        secondary["skinny_int4_sc128_16x8192x8192"] = bench_skinny(torch, shk, max(10, args.steps // 2),
+                                                                   args.warmup, subchannel=128)
     for key, res in secondary.items():
         cpu_fn = res.pop("_cpu", None)
         if cpu_fn is not None and not args.no_cpu_baseline:
