@@ -203,13 +203,14 @@ def test_int4_long_k_needs_the_split_and_stays_exact(device):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("layout", ["nn", "nt", "tn"])
 @pytest.mark.parametrize("sub", [32, 64, 128, 256])
-@pytest.mark.parametrize("r", [16, 64])
+@pytest.mark.parametrize("r", [16, 32, 64])
 def test_subchannel_groups_fold_in_order(bits, layout, sub, r, device):
-    """Subchannel skinny tiles fold every group's exact partial in group
-    order (api.py:311-325): bit-exact for 1, 3 and 9 groups of each size, and
-    with scales over three decades."""
+    """Subchannel skinny tiles add every group's scaled partial in group
+    order (api.py:311-325): bit-exact for 1, 3, 9 and 37 groups of each size
+    (37: several rounds of the four waves' group chunks, the last one
+    partial), with scales over three decades."""
     n = 128
-    for groups in (1, 3, 9):
+    for groups in (1, 3, 9, 37):
         k = groups * sub
         seed = stable_seed("skinny-sc", bits, layout, sub, r, groups)
         a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=r, n=n, k=k, subchannel=sub,
@@ -224,6 +225,31 @@ def test_subchannel_groups_fold_in_order(bits, layout, sub, r, device):
         assert np.array_equal(raw.cpu().numpy(), ref.int_matmul(a_q, b_q))
         _check(bf16_bits(torch, out), a_arg, b_arg, bits=bits, layout=layout, sa=sa, sb=sb, sub=sub,
                epilogue="none")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("layout", ["nn", "nt"])
+@pytest.mark.parametrize("sub", [32, 128])
+@pytest.mark.parametrize("r", [16, 32])
+def test_subchannel_swiglu_groups_fold_in_order(bits, layout, sub, r, device):
+    """The SwiGLU subchannel skinny tiles (up and gate columns, two column
+    tiles per wave): 3 and 37 groups, int32 sums exact, outputs within 2 ulp."""
+    n = 64
+    for groups in (3, 37):
+        k = groups * sub
+        seed = stable_seed("skinny-sc-swiglu", bits, layout, sub, r, groups)
+        a_q, b_q, a_arg, b_arg, sa, sb = dense_case(seed, bits=bits, layout=layout, m=r, n=n, k=k, subchannel=sub,
+                                                     swiglu=True, scale_lo=1e-4, scale_hi=0.1)
+        kernel = _stream_kernel(bits, layout, r, sub=sub, epilogue="swiglu")
+        a, b = to_dev(torch, a_arg, device), to_dev(torch, b_arg, device)
+        ta, tb = to_dev(torch, sa, device), to_dev(torch, sb, device)
+        print(f"case {kernel.kernel_id} shape=({r},{n},{k})", flush=True)
+        out = shk.explicit_mm(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+        raw = native.launch_generated_kernel_i32(a, b, kernel=kernel, a_scale=ta, b_scale=tb)
+        torch.cuda.synchronize()
+        assert np.array_equal(raw.cpu().numpy(), ref.int_matmul(a_q, b_q))
+        _check(bf16_bits(torch, out), a_arg, b_arg, bits=bits, layout=layout, sa=sa, sb=sb, sub=sub,
+               epilogue="swiglu")
 
 
 def test_subchannel_a_scale_at_a_two_byte_offset(device):
