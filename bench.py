@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 quantized GEMM path on one MI355X.
 
-Headline (BASELINE.json metric): int4 x int4 per-channel GEMM TOPS at
+Headline metric: int4 x int4 per-channel GEMM TOPS at
 M=N=K=8192 (config C2) through ``amd_strix_halo_kernels.mm``, as a fraction of
 the gfx950 dense int8 MFMA peak.  Secondary lines in the same JSON object:
 C3 (int4 subchannel-256 ReLU2, 4096x16384x4096), C4 (int8 fused SwiGLU,

@@ -389,7 +389,7 @@ def tops_for_runtime(m: int, n: int, k: int, runtime_ms: float) -> float:
 
 
 # ---------------------------------------------------------------------------
-# Seeded inputs of the benchmark configs (scaled down
+# Seeded inputs of the benchmark configs (C1-C5, scaled down
 # where a test needs a small case)
 
 

@@ -320,6 +320,8 @@ def _build() -> tuple[KernelDesc, ...]:
         # fp6 entries lead each family (k_ragged.hip)
         add(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, group_m=1, bm=128, bn=128, bk=128, wm=2, wn=2,
             fp6_small=True)
+        add(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, group_m=1, bm=128, bn=128, bk=128, wm=2, wn=2,
+            subch=True, fp6_sub=True)
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             f = dict(family=FAMILY_RAGGED_FWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1)
             add(**f, bm=16, bn=128, bk=128, wm=1, wn=4)
@@ -463,10 +465,16 @@ def find_ragged(family: int, *, layout: int, subchannel: int | None, block_m: in
 
 def ragged_fp6_eligible(family: int, *, subchannel: int | None, m: int, n: int, k_packed: int) -> bool:
     """Whether a ragged call's sizes suit the fp6 entries (k_f6ragged.hip):
-    per-channel, N a multiple of 8 (whole 16-byte output units) and K at
-    most FP6_MAX_K.  The same for the forward and the backward (`family`)."""
-    del family, m
-    return subchannel is None and n % 8 == 0 and 2 * k_packed <= FP6_MAX_K
+    N a multiple of 8 (whole 16-byte output units) and K at most FP6_MAX_K;
+    per-channel, or for the forward subchannel groups with K a multiple of
+    128 and of the group size (whole groups of whole stages of the
+    subchannel tile) and M * K/S even (the tile reads a_scale in whole
+    dwords)."""
+    if subchannel is not None:
+        k = 2 * k_packed
+        if family != FAMILY_RAGGED_FWD or k % max(128, subchannel) or m * (k // subchannel) % 2:
+            return False
+    return n % 8 == 0 and 2 * k_packed <= FP6_MAX_K
 
 
 # Task rows of the forward kernels that read packed operands, and of the fp6

@@ -421,10 +421,21 @@ uint64_t ragged_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, 
 // whole 16-byte output units (N a multiple of 8, out 16-byte aligned) and
 // 4-scale loads (b_scale 8-byte aligned), 32-bit offsets within a tile, and
 // a large enough workspace.  Operands may have any alignment.
-int check_f6_ragged(const shk_kernel_desc& d, const void* b_scale, const void* out, int32_t m, int32_t n,
-                    int32_t k_packed, int32_t groups, const void* workspace, uint64_t workspace_bytes) {
+int check_f6_ragged(const shk_kernel_desc& d, int32_t subchannel, const void* b_scale, const void* out, int32_t m,
+                    int32_t n, int32_t k_packed, int32_t groups, const void* workspace, uint64_t workspace_bytes) {
   const int k = 2 * k_packed;
   if (k > shk::F6_MAX_K) return fail("fp6 kernels support K <= " + std::to_string(shk::F6_MAX_K));
+  // the subchannel tile runs whole groups of whole 64-K stages (128-K stages
+  // for groups of 256, two per group)
+  const int k_step = subchannel > 128 ? subchannel : 128;
+  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && k % k_step)
+    return fail("kernel " + std::to_string(d.index) + " needs K to be a multiple of " + std::to_string(k_step) +
+                " with subchannel " + std::to_string(subchannel) + "; got " + std::to_string(k));
+  // the tile reads a_scale [M, K/S] in whole dwords, which covers the last
+  // value only when M * K/S is even
+  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && (long long)m * (k / subchannel) % 2)
+    return fail("kernel " + std::to_string(d.index) + " needs M * K/subchannel to be even; got M=" +
+                std::to_string(m) + ", K/subchannel=" + std::to_string(k / subchannel));
   if (n % 8) return fail("kernel " + std::to_string(d.index) + " needs N to be a multiple of 8; got " + std::to_string(n));
   if (!aligned(out, 16) || !aligned(b_scale, 8)) return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
   if ((unsigned long long)n * 4ull * 256ull >= (1ull << 32)) return fail("ragged output rows are limited to 4194304 bytes");
@@ -765,7 +776,7 @@ int ragged_fwd(int kernel_index, int device_index, uintptr_t stream, const void*
   if (!fp6 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
   if (!aligned(tasks_i32, 16)) return fail("tasks buffer must be 16-byte aligned");
-  if (fp6 && check_f6_ragged(d, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
+  if (fp6 && check_f6_ragged(d, subchannel, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
   if (m == 0 || n == 0 || capacity == 0) {
     // nothing to multiply; a requested task list is still built
     if (job == nullptr) return 0;
@@ -901,7 +912,7 @@ int amd_strix_halo_kernels_launch_ragged_bwd_ws(int kernel_index, int device_ind
   const int k_cap = 2 * k_packed;
   if (!fp6 && d.scale_mode == SHK_SCALE_PER_CHANNEL && k_cap > kMaxInt4AccK)
     return fail("int4 per-channel kernels support K <= " + std::to_string(kMaxInt4AccK));
-  if (fp6 && check_f6_ragged(d, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
+  if (fp6 && check_f6_ragged(d, subchannel, b_scale, out, m, n, k_packed, groups, workspace, workspace_bytes)) return 1;
   if (m == 0 || n == 0 || groups == 0) return 0;
   shk::RaggedBwdArgs p{};
   p.lhs = static_cast<const uint8_t*>(lhs);

@@ -19,12 +19,20 @@
 // a multiple of 128.  Workspace: A as round32(M) rows x Kw, then per group
 // B as round32(N) rows x Kw.
 //
+// Subchannel forward: the same tasks and converted operands on the 128 x 128
+// subchannel tile of shk_f6sub.h (groups of 32 to 256 added into fp32 in
+// group order, api.py:311-325 as ragged.py applies it), two workgroups per
+// CU, its stores masked to the task's rows and the columns below N.  K is a
+// multiple of 128 (the entry's check), so every group count runs whole
+// stages of the tile's engine.
+//
 // Backward (ragged.py:1232-1402 semantics): out[g] = lhs[g] @ rhs[g] over
 // the first group_sizes[g] K values.  The conversion zeroes K at and past
 // that length, so group g runs ceil(len / 128) whole 128-K stages.
 // Workspace: per group A (round32(M) rows x Kw), then per group B
 // (round32(N) rows x Kw), Kw = K capacity rounded up to 128.
 #include "shk_f6small.h"
+#include "shk_f6sub.h"
 #include "shk_table.h"
 
 namespace shk {
@@ -81,6 +89,39 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_fwd_kernel(const RaggedFwdAr
   mfma32_prefetch_b_scales<F6R, MODE, true>(e, o, tn * kTile, e.lds0 + E::LDS_BYTES + 256u * e.wave);
   e.run(kw / 128);
   f6s_finish<MODE, true>(e, o, smem, m0, tn * kTile, sa);
+}
+
+// The subchannel tile (128 A rows x 128 B rows, 2 x 2 waves).
+using F6RS = Cfg<4, true, true, 128, 128, 128, 2, 2, false, true, 64, false, 0>;
+
+template <int MODE, int G32>
+__global__ __launch_bounds__(256, 2) void f6_ragged_sub_fwd_kernel(const RaggedFwdArgs p) {
+  using E = F6SubEngineFor<F6RS, G32>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  const int tiles_n = (p.N + kTile - 1) / kTile;
+  const int ntasks = *p.num_tasks;
+  const int live = ntasks * tiles_n;
+  if (ntasks > p.capacity || (int)blockIdx.x >= live) return;
+  const int w = xcd_contiguous(blockIdx.x, live);
+  const int task = w / tiles_n;
+  const int tn = w - task * tiles_n;
+  const int4 t = *reinterpret_cast<const int4*>(p.tasks + 4 * task);
+  const int g = t.x, m0 = t.y, n0 = tn * kTile;
+  const int kw = round128(p.K);
+  const unsigned long long a_bytes = f6_operand_bytes(round32(p.M), kw);
+  const unsigned long long b_bytes = f6_operand_bytes(round32(p.N), kw);
+  E e;
+  e.setup(smem, p.work, p.work + a_bytes + (unsigned long long)g * b_bytes, m0, n0, kw / 64, a_bytes, b_bytes,
+          p.a_scale, p.b_scale + (long)g * p.scale_cols * p.N, p.M, p.N, p.scale_cols);
+  e.template run<MODE == OUT_I32>(smem, p.K / (G32 == 8 ? 128 : 64));
+  const OutView o{p.out, nullptr, p.N, p.M, p.N, t.z, t.w, p.N};
+  if constexpr (MODE == OUT_I32 || MODE == OUT_F32) {
+    f6sub_store_words<true>(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
+  } else {
+    auto val = [&](int i, int j, int x) { return e.tot[i][j][x]; };
+    if (e.all_fast) f6sub_store_bf16<true, true>(e, o, smem, m0, n0, val);
+    else f6sub_store_bf16<false, true>(e, o, smem, m0, n0, val);
+  }
 }
 
 // Regions of the backward's per-group tile grid: sm x sn = 8, one per XCD;
@@ -180,6 +221,29 @@ hipError_t launch_f6_ragged_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s
   return hipGetLastError();
 }
 
+template <int MODE>
+void launch_ragged_sub(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
+  if (a.subchannel == 32) hipLaunchKernelGGL((f6_ragged_sub_fwd_kernel<MODE, 1>), grid, dim3(256), 0, s, a);
+  else if (a.subchannel == 64) hipLaunchKernelGGL((f6_ragged_sub_fwd_kernel<MODE, 2>), grid, dim3(256), 0, s, a);
+  else if (a.subchannel == 128) hipLaunchKernelGGL((f6_ragged_sub_fwd_kernel<MODE, 4>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((f6_ragged_sub_fwd_kernel<MODE, 8>), grid, dim3(256), 0, s, a);
+}
+hipError_t launch_f6_ragged_sub_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
+  const int kw = round128(a.K);
+  const unsigned long long a_bytes = f6_operand_bytes(round32(a.M), kw);
+  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda),
+                      false, 2};
+  const F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
+                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb), false, 2};
+  hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s,
+                                   a.job.sizes != nullptr ? &a.job : nullptr);
+  if (err != hipSuccess) return err;
+  if (a.out_mode == OUT_I32) launch_ragged_sub<OUT_I32>(a, grid, s);
+  else if (a.out_mode == OUT_F32) launch_ragged_sub<OUT_F32>(a, grid, s);
+  else launch_ragged_sub<OUT_BF16>(a, grid, s);
+  return hipGetLastError();
+}
+
 hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
   {
     // with XCD regions, every XCD's workgroups cover its widest region
@@ -230,6 +294,15 @@ shk_kernel_desc f6_ragged_desc(int family, int layout) {
 
 Entry f6_ragged_fwd_entry(int layout) {
   return Entry{f6_ragged_desc(SHK_FAMILY_RAGGED_FWD, layout), nullptr, &launch_f6_ragged_fwd, nullptr, nullptr};
+}
+Entry f6_ragged_sub_fwd_entry(int layout) {
+  shk_kernel_desc d = desc_of<F6RS>(SHK_FAMILY_RAGGED_FWD, layout, 1);
+  d.min_subchannel = 32;
+  d.max_subchannel = 256;
+  d.num_stages = F6SubEngine<F6RS>::P;
+  d.lds_bytes = f6_sub_lds_bytes<F6RS>();
+  d.operand_format = SHK_OPERANDS_FP6;
+  return Entry{d, nullptr, &launch_f6_ragged_sub_fwd, nullptr, nullptr};
 }
 Entry f6_ragged_bwd_entry(int layout) {
   return Entry{f6_ragged_desc(SHK_FAMILY_RAGGED_BWD, layout), nullptr, nullptr, &launch_f6_ragged_bwd, nullptr};

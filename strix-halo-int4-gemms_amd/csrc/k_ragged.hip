@@ -30,6 +30,7 @@ void append_fwd(std::vector<Entry>& t) {
 // The fp6 entries (k_f6ragged.hip) lead each family.
 void append_all(std::vector<Entry>& t) {
   t.push_back(f6_ragged_fwd_entry(kLayout));
+  t.push_back(f6_ragged_sub_fwd_entry(kLayout));
   append_fwd<false, 64>(t);
   append_fwd<true, 64>(t);
   append_fwd<true, 32>(t);

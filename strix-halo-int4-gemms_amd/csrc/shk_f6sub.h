@@ -976,8 +976,9 @@ struct F6SubEngine64 {
 // 128-byte row segment per 8 lanes.
 // NO_NAN: no value is NaN, so the hardware conversion (round to nearest
 // even, which keeps a NaN's payload where torch writes 0x7FC0) gives torch's
-// bits.
-template <bool NO_NAN, class E, class V>
+// bits.  MASK: only rows [o.row_lo, o.row_hi) and columns below o.col_hi (a
+// multiple of 8) are written (the ragged forward's tasks).
+template <bool NO_NAN, bool MASK = false, class E, class V>
 __device__ __forceinline__ void f6sub_store_bf16(const E& e, const OutView& o, uint8_t* smem, int m0, int n0,
                                                  V v) {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -1009,16 +1010,20 @@ __device__ __forceinline__ void f6sub_store_bf16(const E& e, const OutView& o, u
   const rsrc_t rs = make_rsrc(static_cast<uint8_t*>(o.out) + first * 2, ((unsigned long long)o.rows * ldo - first) * 2);
   const int rr = lane / 8, u = lane % 8;
   const uint32_t voff = ((uint32_t)(e.wm * 64 + rr) * ldo + (uint32_t)(e.wn * 64 + 8 * u)) * 2u;
+  const bool col_ok = !MASK || n0 + e.wn * 64 + 8 * u < o.col_hi;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int r = 8 * t + rr;
     const uint4 x = *reinterpret_cast<const uint4*>(region + r * 128 + 16 * (u ^ ((r >> 1) & 7)));
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(8 * t) * ldo * 2u, 0);
+    const int row = m0 + e.wm * 64 + r;
+    if (!MASK || (col_ok && row >= o.row_lo && row < o.row_hi))
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, x), rs, voff, (uint32_t)(8 * t) * ldo * 2u, 0);
   }
 }
 
-// fp32 / int32 results: four consecutive columns per store.
-template <class E, class V>
+// fp32 / int32 results: four consecutive columns per store (MASK as for
+// f6sub_store_bf16).
+template <bool MASK = false, class E, class V>
 __device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, int m0, int n0, V v) {
   const uint32_t ldo = (uint32_t)o.ld;
   const unsigned long long first = (unsigned long long)m0 * ldo + n0;
@@ -1031,9 +1036,11 @@ __device__ __forceinline__ void f6sub_store_words(const E& e, const OutView& o, 
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int x = 4 * q;
-        __builtin_amdgcn_raw_buffer_store_b128(v4i{v(i, j, x), v(i, j, x + 1), v(i, j, x + 2), v(i, j, x + 3)}, r,
-                                               voff + (uint32_t)(32 * j + 8 * q) * 4u,
-                                               (uint32_t)(32 * i) * ldo * 4u, 0);
+        const int row = m0 + e.out_row(i), col = n0 + e.out_col(j, q);
+        if (!MASK || (row >= o.row_lo && row < o.row_hi && col < o.col_hi))
+          __builtin_amdgcn_raw_buffer_store_b128(v4i{v(i, j, x), v(i, j, x + 1), v(i, j, x + 2), v(i, j, x + 3)},
+                                                 r, voff + (uint32_t)(32 * j + 8 * q) * 4u,
+                                                 (uint32_t)(32 * i) * ldo * 4u, 0);
       }
 }
 

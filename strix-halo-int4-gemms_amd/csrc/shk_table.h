@@ -342,6 +342,7 @@ int max_info_groups();
 // fp6 ragged entries of one layout (k_f6ragged.hip): the forward (task
 // tile 128) and the K-ragged backward, both per-channel.
 Entry f6_ragged_fwd_entry(int layout);
+Entry f6_ragged_sub_fwd_entry(int layout);
 Entry f6_ragged_bwd_entry(int layout);
 // Workspace bytes of the fp6 ragged paths.
 unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups);

@@ -305,8 +305,9 @@ def test_split_fp6_phases_validate_their_arguments(lib):
     assert "a_scale, b_scale, and out pointers must be non-null" in _err(lib)
 
 
-def _ragged_f6(family, layout=kt.LAYOUT_NN):
-    return next(d for d in kt.entries(family) if d.layout == layout and d.operand_format == kt.OPERANDS_FP6)
+def _ragged_f6(family, layout=kt.LAYOUT_NN, scale_mode=kt.SCALE_PER_CHANNEL):
+    return next(d for d in kt.entries(family)
+                if d.layout == layout and d.operand_format == kt.OPERANDS_FP6 and d.scale_mode == scale_mode)
 
 
 def _ragged_ws(lib, index, m, n, k_packed, groups):
@@ -318,11 +319,21 @@ def _ragged_ws(lib, index, m, n, k_packed, groups):
 def test_fp6_ragged_entries_report_their_workspace(lib):
     for family in (kt.FAMILY_RAGGED_FWD, kt.FAMILY_RAGGED_BWD):
         fp6 = [d for d in kt.entries(family) if d.operand_format == kt.OPERANDS_FP6]
-        assert sorted(d.layout for d in fp6) == [kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN, kt.LAYOUT_TT]
+        layouts = [kt.LAYOUT_NN, kt.LAYOUT_NT, kt.LAYOUT_TN, kt.LAYOUT_TT]
+        per_channel = [d for d in fp6 if d.scale_mode == kt.SCALE_PER_CHANNEL]
+        sub = [d for d in fp6 if d.scale_mode == kt.SCALE_SUBCHANNEL]
+        assert sorted(d.layout for d in per_channel) == layouts
+        # the forward also has one fp6 subchannel entry per layout; the backward has none
+        assert sorted(d.layout for d in sub) == (layouts if family == kt.FAMILY_RAGGED_FWD else [])
         for d in fp6:
-            # 128 x 128 tiles, two 24 KiB stages of 128 K and the B-scale slots: three per CU
-            assert d.scale_mode == kt.SCALE_PER_CHANNEL and (d.block_m, d.block_k, d.num_stages) == (128, 128, 2)
-            assert d.lds_bytes == 50176
+            if d.scale_mode == kt.SCALE_PER_CHANNEL:
+                # 128 x 128 tiles, two 24 KiB stages of 128 K and the B-scale slots: three per CU
+                assert (d.block_m, d.block_k, d.num_stages) == (128, 128, 2)
+                assert d.lds_bytes == 50176
+            else:
+                # the subchannel engine: a ring of 64-K stages, groups of 32 to 256
+                assert (d.block_m, d.block_n, d.min_subchannel, d.max_subchannel) == (128, 128, 32, 256)
+                assert d.lds_bytes == 81920
             for m, n, kp, g in ((8192, 1408, 1024, 8), (17, 24, 32, 3), (2048, 1408, 1001, 8), (1, 8, 1, 1)):
                 kw = -(-2 * kp // 128) * 128
                 m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
@@ -359,6 +370,15 @@ def test_fp6_ragged_launch_validation(lib):
     assert FW(fwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, kt.FP6_MAX_K // 2 + 64, 2, 0, 0,
               FAKE, 1 << 40) == 1
     assert "K <= 262144" in _err(lib)
+    sub = _ragged_f6(kt.FAMILY_RAGGED_FWD, scale_mode=kt.SCALE_SUBCHANNEL).index
+    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 96, 2, 64, 0, FAKE, 1 << 30) == 1
+    assert "K to be a multiple of 128 with subchannel 64; got 192" in _err(lib)
+    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 192, 2, 256, 0, FAKE, 1 << 30) == 1
+    assert "K to be a multiple of 256 with subchannel 256; got 384" in _err(lib)
+    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 128, 2, 16, 0, FAKE, 1 << 30) == 1
+    assert "subchannel size 16 is not served" in _err(lib)
+    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 63, 16, 384, 2, 256, 0, FAKE, 1 << 30) == 1
+    assert "M * K/subchannel to be even; got M=63, K/subchannel=3" in _err(lib)
     bwd = _ragged_f6(kt.FAMILY_RAGGED_BWD, kt.LAYOUT_TN).index
     B = lib.amd_strix_halo_kernels_launch_ragged_bwd
     BW = lib.amd_strix_halo_kernels_launch_ragged_bwd_ws
@@ -379,11 +399,21 @@ def test_fp6_ragged_eligibility():
     assert kt.ragged_fp6_eligible(fwd, subchannel=None, m=8192, n=1408, k_packed=1024)
     assert kt.ragged_fp6_eligible(bwd, subchannel=None, m=2048, n=1408, k_packed=1001)
     assert kt.ragged_fp6_eligible(fwd, subchannel=None, m=17, n=24, k_packed=32)
-    assert not kt.ragged_fp6_eligible(fwd, subchannel=32, m=8192, n=1408, k_packed=1024)
+    # subchannel: the forward only, and only when K is a whole number of
+    # 128-K blocks and of groups
+    assert kt.ragged_fp6_eligible(fwd, subchannel=32, m=8192, n=1408, k_packed=1024)
+    assert kt.ragged_fp6_eligible(fwd, subchannel=128, m=18, n=24, k_packed=64)
+    assert kt.ragged_fp6_eligible(fwd, subchannel=256, m=18, n=24, k_packed=128)
+    assert kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=256)
+    assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=128)  # M * K/S odd
+    assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=192)
+    assert not kt.ragged_fp6_eligible(fwd, subchannel=64, m=8192, n=1408, k_packed=1056)
+    assert not kt.ragged_fp6_eligible(bwd, subchannel=128, m=2048, n=1408, k_packed=1024)
     assert not kt.ragged_fp6_eligible(bwd, subchannel=None, m=16, n=20, k_packed=16)
     assert not kt.ragged_fp6_eligible(fwd, subchannel=None, m=16, n=16, k_packed=kt.FP6_MAX_K // 2 + 1)
     with pytest.raises(LookupError):
-        kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True)
+        kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True)
+    assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True).scale_mode == kt.SCALE_SUBCHANNEL
     assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=None, fp6=True).block_m == kt.RAGGED_FP6_BLOCK_M
     assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=None).operand_format == kt.OPERANDS_PACKED
     assert kt.RAGGED_FP6_CONFIG_BLOCK_M not in kt.RAGGED_FWD_BLOCK_M

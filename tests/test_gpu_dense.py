@@ -1,11 +1,11 @@
 """GPU parity of the dense path (mm / fused_swiglu_up_gate / explicit_mm)
 against the CPU oracle.
 
-Bar (BASELINE north_star): the int32 accumulators are bit-exact against the
+Bar: the int32 accumulators are bit-exact against the
 integer matmul; bf16 outputs are within 2 bf16 ulp of the oracle (per-channel
 and subchannel NONE / RELU2 come out bit-identical; SwiGLU may differ by an
 ulp through exp).  Mirrors the reference's every-registry-kernel check
-(tests/test_native_generated.py:74-108) and adds the BASELINE configs at full
+(tests/test_native_generated.py:74-108) and adds the benchmark configs C2-C4 at full
 size, every output checked.
 """
 
@@ -153,7 +153,7 @@ def test_config_c1_plumbing_exact(device):
 
 
 def _big_dense(device, *, bits, m, n, k, sub, epilogue, seed, scale_lo=0.005, scale_hi=0.02):
-    """A BASELINE config at full size through mm / fused_swiglu_up_gate, with
+    """A benchmark config at full size through mm / fused_swiglu_up_gate, with
     every output checked: the raw int32 accumulators against the C oracle's
     exact integer matmul, and the bf16 result against the oracle's whole
     dense path (the C restatement for int4 NONE / RELU2, numpy for SwiGLU)."""
@@ -205,7 +205,7 @@ def test_config_c2_8192_cubed(device):
 @pytest.mark.parametrize("sub", [256, 128, 64, 32])
 def test_config_c3_subchannel_relu2(sub, device):
     """C3 at full size, every output checked, for every group size the fp6
-    subchannel tile serves (256 is the BASELINE config): 16 to 128 groups
+    subchannel tile serves (256 is the C3 config): 16 to 128 groups
     folded in order, groups of 32 two to a 64-K stage."""
     print(f"case C3 shape subchannel {sub}", flush=True)
     got, want, _ = _big_dense(device, bits=4, m=4096, n=16384, k=4096, sub=sub, epilogue="relu2", seed=3)

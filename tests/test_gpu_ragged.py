@@ -4,12 +4,14 @@ ragged_dot_int4_bwd) against the CPU oracle.
 The cases mirror the reference's tests/test_ragged_dot.py (:154-586): every
 layout, per-channel and subchannel-32 scales, split_k 1 and 2, empty groups,
 odd K with garbage in the padding, and the even-K fast path; plus the
-BASELINE C5 MoE shape at full size.  Per-channel results are bit-identical to
+C5 MoE benchmark shape at full size.  Per-channel results are bit-identical to
 the oracle (same op order, exact int32 sums); subchannel split-K adds fp32
 partials in another order and is held to a relative 1e-5.
 """
 
 from __future__ import annotations
+
+import functools
 
 import numpy as np
 import pytest
@@ -167,7 +169,7 @@ FP6_FWD_SHAPES = [(17, 64, 24, [5, 0, 12]), (300, 200, 40, [100, 0, 37, 163]),
                   (640, 384, 264, [1, 300, 0, 339]), (96, 256, 8, [96])]
 
 
-def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode, fp6=False):
+def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode, fp6=False, subchannel=None):
     from amd_strix_halo_kernels import kernel_table as kt
     from amd_strix_halo_kernels import native
     lhs, rhs = _pack_fwd(a_q, b_q, layout)
@@ -176,7 +178,8 @@ def _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, block_m, out_mode, 
     out = torch.full((m, n), 7, dtype=dt, device=device)
     native.launch_ragged_fwd(
         to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
-        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), out=out, layout=layout, subchannel=None,
+        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), out=out, layout=layout,
+        subchannel=subchannel,
         block_m=block_m, align_tile=32 if fp6 else 8, rows=m, cols=n, k_packed=a_q.shape[1] // 2,
         out_mode=out_mode, fp6=fp6)
     torch.cuda.synchronize()
@@ -254,6 +257,41 @@ def test_ragged_fwd_fp6_all_layouts_and_modes(layout, shape, device):
     assert np.array_equal(bf16_bits(torch, got), ref.bf16_round(want))
     got = _run_fwd_native(device, a_q, b_q, sizes, sa, sb, layout, kt.RAGGED_FP6_BLOCK_M, kt.OUT_I32, fp6=True)
     assert np.array_equal(got.cpu().numpy().astype(np.int64), _ragged_int_reference(a_q, b_q, sizes))
+
+
+# fp6 subchannel forward (the 128 x 128 subchannel tile on the task list):
+# K a multiple of 128 and of the group size, M * K/S even; row and column
+# masks, groups that span several tiles and tiles that span two groups' rows
+FP6_SUB_SHAPES = [(17, 512, 24, [5, 0, 12]), (300, 512, 40, [100, 0, 37, 163]),
+                  (640, 384, 264, [1, 300, 0, 339]), (96, 1024, 8, [96])]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("subchannel", [32, 64, 128, 256])
+def test_ragged_fwd_fp6_subchannel(layout, subchannel, device):
+    """Every group size and layout in fp32 (bit-exact: the oracle's group
+    order and per-group rounding), bf16 (the fp32 result rounded once) and
+    int32 (the exact sums over all K)."""
+    from amd_strix_halo_kernels import kernel_table as kt
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
+    for m, k, n, sizes in FP6_SUB_SHAPES:
+        if k % subchannel or m * (k // subchannel) % 2:
+            continue
+        a_q, b_q, sa, sb = _fwd_case(stable_seed("fp6sub", layout.value, subchannel, m), m, k, n, sizes, spec)
+        if m == 300:
+            # zero and tiny scales: the tile's folds in the reference's operation order
+            sa[::7, 0] = 0
+            sb[:, -1, ::5] = 0x1C80  # 2^-70
+        print(f"case fp6 sub fwd {layout.value} S={subchannel} {(m, k, n, sizes)}", flush=True)
+        want = ref.ragged_fwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=subchannel)
+        run = functools.partial(_run_fwd_native, device, a_q, b_q, sizes, sa, sb, layout, kt.RAGGED_FP6_BLOCK_M,
+                                fp6=True, subchannel=subchannel)
+        got = run(kt.OUT_F32)
+        assert np.array_equal(got.cpu().numpy(), want)
+        got = run(kt.OUT_BF16)
+        assert np.array_equal(bf16_bits(torch, got), ref.bf16_round(want))
+        got = run(kt.OUT_I32)
+        assert np.array_equal(got.cpu().numpy().astype(np.int64), _ragged_int_reference(a_q, b_q, sizes))
 
 
 @pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
