@@ -147,12 +147,13 @@ class KernelDesc:
 
     def ragged_workspace_bytes(self, m: int, n: int, k_packed: int, groups: int) -> int:
         """Bytes of the operand workspace of a ragged call (0 for PACKED):
-        with K rounded up to 128, the forward holds A (round32(m) rows) and
-        per group B (round32(n) rows); the backward per group A, then per
-        group B (k_f6ragged.hip)."""
+        with K rounded up to 128 (256 for the subchannel backward), the
+        forward holds A (round32(m) rows) and per group B (round32(n) rows);
+        the backward per group A, then per group B (k_f6ragged.hip)."""
         if not self.needs_workspace or m == 0 or n == 0 or groups == 0:
             return 0
-        kw = -(-2 * k_packed // 128) * 128
+        step = 256 if self.family == FAMILY_RAGGED_BWD and self.scale_mode == SCALE_SUBCHANNEL else 128
+        kw = -(-2 * k_packed // step) * step
         m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
         if self.family == FAMILY_RAGGED_FWD:
             return (m32 * kw * 3) // 4 + groups * ((n32 * kw * 3) // 4)
@@ -260,7 +261,8 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         dtype_bits=bits,
         layout=layout,
         scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
-        min_subchannel=(32 if mk == 32 or fp6_sub else 64) if subch else 0,
+        # (the fp6 subchannel backward: groups of 64 and up)
+        min_subchannel=(32 if mk == 32 or (fp6_sub and family != FAMILY_RAGGED_BWD) else 64) if subch else 0,
         max_subchannel=(32 if mk == 32 else 256) if subch else 0,
         epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
         block_m=bm,
@@ -330,6 +332,8 @@ def _build() -> tuple[KernelDesc, ...]:
             add(**f, bm=128, bn=128, bk=128, wm=2, wn=2)
         add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, group_m=1, bm=128, bn=128, bk=128, wm=2, wn=2,
             fp6_small=True)
+        add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, group_m=1, bm=128, bn=128, bk=128, wm=2, wn=2,
+            subch=True, fp6_sub=True)
         for subch, mk in ((False, 64), (True, 64), (True, 32)):
             add(family=FAMILY_RAGGED_BWD, bits=4, layout=layout, subch=subch, mk=mk, group_m=1, bm=128, bn=128,
                 bk=128, wm=2, wn=2)
@@ -466,13 +470,17 @@ def find_ragged(family: int, *, layout: int, subchannel: int | None, block_m: in
 def ragged_fp6_eligible(family: int, *, subchannel: int | None, m: int, n: int, k_packed: int) -> bool:
     """Whether a ragged call's sizes suit the fp6 entries (k_f6ragged.hip):
     N a multiple of 8 (whole 16-byte output units) and K at most FP6_MAX_K;
-    per-channel, or for the forward subchannel groups with K a multiple of
-    128 and of the group size (whole groups of whole stages of the
-    subchannel tile) and M * K/S even (the tile reads a_scale in whole
-    dwords)."""
+    per-channel, or subchannel with M * ceil(K/S) even (the tile reads
+    a_scale in whole dwords): for the forward, K a multiple of 128 and of
+    the group size (whole groups of whole stages of the subchannel tile);
+    for the backward, which pads K, groups of 64 and up."""
     if subchannel is not None:
         k = 2 * k_packed
-        if family != FAMILY_RAGGED_FWD or k % max(128, subchannel) or m * (k // subchannel) % 2:
+        if family == FAMILY_RAGGED_FWD and k % max(128, subchannel):
+            return False
+        if family == FAMILY_RAGGED_BWD and subchannel < 64:
+            return False
+        if m * -(-k // subchannel) % 2:
             return False
     return n % 8 == 0 and 2 * k_packed <= FP6_MAX_K
 

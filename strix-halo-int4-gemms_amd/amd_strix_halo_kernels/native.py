@@ -661,7 +661,7 @@ def launch_ragged_fwd(
     """Device task list + grouped forward in one library call (replaces
     calculate_group_info + launch_ragged_fwd_kernel, ragged.py:201-323 and
     native.py:533-600).  No host synchronisation.  fp6: run the fp6 entry
-    (per-channel; block_m must be its task tile, kt.RAGGED_FP6_BLOCK_M),
+    (per-channel or subchannel; block_m must be its task tile, kt.RAGGED_FP6_BLOCK_M),
     whose operands are converted into a workspace and whose tasks need
     align_tile a multiple of 32.  The task list, its count and the
     workspace share one allocation."""
@@ -728,7 +728,7 @@ def launch_ragged_bwd(
     stream: Any | None = None,
 ) -> Any:
     """Grouped K-ragged backward (replaces launch_ragged_bwd_kernel,
-    native.py:603-667).  fp6: run the fp6 entry (per-channel), whose operands
+    native.py:603-667).  fp6: run the fp6 entry of the scale mode, whose operands
     are converted into a workspace."""
     torch = _torch()
     lib = _verified_library(library_path)

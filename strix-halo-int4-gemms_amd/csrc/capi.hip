@@ -414,7 +414,7 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
 uint64_t ragged_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k_packed, int32_t groups) {
   if (d.operand_format != SHK_OPERANDS_FP6) return 0;
   if (d.family == SHK_FAMILY_RAGGED_FWD) return shk::f6_ragged_fwd_workspace(m, n, 2 * k_packed, groups);
-  return shk::f6_ragged_bwd_workspace(m, n, 2 * k_packed, groups);
+  return shk::f6_ragged_bwd_workspace(m, n, 2 * k_packed, groups, d.scale_mode == SHK_SCALE_SUBCHANNEL);
 }
 
 // Requirements of the fp6 ragged entries: a K that keeps fp32 sums exact,
@@ -425,17 +425,19 @@ int check_f6_ragged(const shk_kernel_desc& d, int32_t subchannel, const void* b_
                     int32_t n, int32_t k_packed, int32_t groups, const void* workspace, uint64_t workspace_bytes) {
   const int k = 2 * k_packed;
   if (k > shk::F6_MAX_K) return fail("fp6 kernels support K <= " + std::to_string(shk::F6_MAX_K));
-  // the subchannel tile runs whole groups of whole 64-K stages (128-K stages
-  // for groups of 256, two per group)
+  // the forward's subchannel tile runs whole groups of whole 64-K stages
+  // (128-K stages for groups of 256, two per group); the backward pads K
   const int k_step = subchannel > 128 ? subchannel : 128;
-  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && k % k_step)
+  const bool sub = d.scale_mode == SHK_SCALE_SUBCHANNEL;
+  if (sub && d.family == SHK_FAMILY_RAGGED_FWD && k % k_step)
     return fail("kernel " + std::to_string(d.index) + " needs K to be a multiple of " + std::to_string(k_step) +
                 " with subchannel " + std::to_string(subchannel) + "; got " + std::to_string(k));
-  // the tile reads a_scale [M, K/S] in whole dwords, which covers the last
-  // value only when M * K/S is even
-  if (d.scale_mode == SHK_SCALE_SUBCHANNEL && (long long)m * (k / subchannel) % 2)
-    return fail("kernel " + std::to_string(d.index) + " needs M * K/subchannel to be even; got M=" +
-                std::to_string(m) + ", K/subchannel=" + std::to_string(k / subchannel));
+  // the tile reads a_scale [M, ceil(K/S)] in whole dwords, which covers the
+  // last value only when M * ceil(K/S) is even
+  const int scale_cols = sub ? (k + subchannel - 1) / subchannel : 1;
+  if (sub && (long long)m * scale_cols % 2)
+    return fail("kernel " + std::to_string(d.index) + " needs M * ceil(K/subchannel) to be even; got M=" +
+                std::to_string(m) + ", ceil(K/subchannel)=" + std::to_string(scale_cols));
   if (n % 8) return fail("kernel " + std::to_string(d.index) + " needs N to be a multiple of 8; got " + std::to_string(n));
   if (!aligned(out, 16) || !aligned(b_scale, 8)) return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
   if ((unsigned long long)n * 4ull * 256ull >= (1ull << 32)) return fail("ragged output rows are limited to 4194304 bytes");

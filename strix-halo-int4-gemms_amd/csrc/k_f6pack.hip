@@ -75,8 +75,11 @@ __device__ __forceinline__ uint4 f6_load(const uint8_t* q, int unit, int valid) 
     if (b < valid) w[b / 4] |= (uint32_t)q[b] << (8 * (b % 4));
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
-// 64-K blocks that the GEMM reads for K length `len`: whole 128-K stages.
-__device__ __forceinline__ int f6_blocks_read(int len) { return 2 * ((len + 127) / 128); }
+// 64-K blocks that the GEMM reads for K length `len`: whole stages of
+// p.k_stage K (128, or 256 for the subchannel tile's groups of 256).
+__device__ __forceinline__ int f6_blocks_read(const F6PackArgs& p, int len) {
+  return p.k_stage == 256 ? 4 * ((len + 255) / 256) : 2 * ((len + 127) / 128);
+}
 // bytes of one MN-major source tile in LDS: 32 K rows x 256 packed rows
 constexpr int F6_KTILE = 32 * 256;
 
@@ -107,7 +110,7 @@ __device__ __forceinline__ void pack_kmajor_nb(const F6PackArgs& p, int wg) {
   const long first = ((wg - (long)g * per_group) * 4 + (threadIdx.x >> 6)) * kNB;
   if (first >= blocks) return;
   const int len = f6_k_len(p, g);
-  const int nread = f6_blocks_read(len);
+  const int nread = f6_blocks_read(p, len);
   const uint8_t* src = p.src + g * p.src_group;
   int panel = (int)(first / p.kb);
   int kb = (int)(first - (long)panel * p.kb);
@@ -165,7 +168,7 @@ __device__ __forceinline__ void pack_mnmajor(const F6PackArgs& p, int wg, uint8_
   const int t = local / kgroups;
   const int kb0 = (local - t * kgroups) * kKW;
   const int len = f6_k_len(p, g);
-  const int nread = min(f6_blocks_read(len), p.kb);
+  const int nread = min(f6_blocks_read(p, len), p.kb);
   if (kb0 >= nread) return;  // uniform over the workgroup
   const int tid = threadIdx.x;
   const int u = tid & 15;  // 16-row unit of the tile

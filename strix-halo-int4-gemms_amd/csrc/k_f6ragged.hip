@@ -47,6 +47,7 @@ constexpr int kTile = 128;
 
 __host__ __device__ inline int round32(int x) { return (x + 31) & ~31; }
 __host__ __device__ inline int round128(int x) { return (x + 127) & ~127; }
+__host__ __device__ inline int round256(int x) { return (x + 255) & ~255; }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup w on XCD
 // w % 8), each with its own L2.  Maps the first `total` workgroup ids onto
@@ -134,23 +135,21 @@ __host__ __device__ inline void bwd_regions(int tiles_m, int tiles_n, int& sm, i
   else if (tiles_n % 8 == 0) sm = 1, sn = 8;
 }
 
-template <int MODE>
-__global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
-  using E = F6RE;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
+// The backward tile of this workgroup: group g, tile row tm, tile column tn;
+// false for the spare workgroups of the narrower column regions.  Each
+// group's tiles_m x tiles_n grid splits into 8 regions, sm along M and sn
+// along N, one per XCD, so an XCD reads each of its A tiles for the column
+// tiles of its region and each B tile for its row tiles from its own L2,
+// and holds tiles of every group, whatever their lengths.  Rows split
+// evenly, columns into floor or ceil(tiles_n / sn) (C5's 11 column tiles: 5
+// and 6, so a B tile is read by 4 XCDs instead of all 8 with 8 x 1
+// regions: the C5 backward 42.4 -> 41.8 us per call, A/B on one box).
+// Grids that split no such way run in order.
+__device__ __forceinline__ bool bwd_tile(const RaggedBwdArgs& p, int& g, int& tm, int& tn) {
   const int tiles_m = (p.M + kTile - 1) / kTile;
   const int tiles_n = (p.N + kTile - 1) / kTile;
-  // Each group's tiles_m x tiles_n grid splits into 8 regions, sm along M
-  // and sn along N, one per XCD, so an XCD reads each of its A tiles for the
-  // column tiles of its region and each B tile for its row tiles from its
-  // own L2, and holds tiles of every group, whatever their lengths.  Rows
-  // split evenly, columns into floor or ceil(tiles_n / sn) (C5's 11 column
-  // tiles: 5 and 6, so a B tile is read by 4 XCDs instead of all 8 with
-  // 8 x 1 regions: the C5 backward 42.4 -> 41.8 us per call, A/B on one
-  // box).  Grids that split no such way run in order.
   int sm = 0, sn = 0;  // region counts along M and N (sm * sn = 8)
   bwd_regions(tiles_m, tiles_n, sm, sn);
-  int g, tm, tn;
   if (sm) {
     const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
     // rows: bm per region; columns: regions of floor or ceil(tiles_n / sn),
@@ -160,7 +159,7 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdAr
     const int local = i - g * (bm * bn);
     const int xn = x % sn;
     const int c0 = tiles_n * xn / sn, width = tiles_n * (xn + 1) / sn - c0;
-    if (local % bn >= width) return;
+    if (local % bn >= width) return false;
     tm = (x / sn) * bm + local / bn;
     tn = c0 + local % bn;
   } else {
@@ -169,6 +168,15 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdAr
     tm = t / tiles_n;
     tn = t - tm * tiles_n;
   }
+  return true;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdArgs p) {
+  using E = F6RE;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES + MFMA32_SCALE_BYTES];
+  int g, tm, tn;
+  if (!bwd_tile(p, g, tm, tn)) return;
   const int m0 = tm * kTile;
   const int kw = round128(p.k_cap);
   int len = p.group_sizes[g];
@@ -192,6 +200,39 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdAr
   // whole 128-K stages: the conversion writes no block past the last one
   e.run((len + 127) / 128);
   f6s_finish<MODE, true>(e, o, smem, m0, tn * kTile, sa);
+}
+
+// The subchannel backward: group g's tile over the scale groups that start
+// below its length, ceil(len / S) of them, each folded into fp32 in group
+// order (the conversion zeroes K past len and writes the blocks up to whole
+// groups of 256 for S = 256, so the last group's partial sums cover exactly
+// its first len - S * (ceil(len / S) - 1) values).  K is padded to 256, so
+// those groups' stages never pass the converted blocks.
+// With one 64-K stage per group (S = 64) an odd count ends with a stage
+// past the last one, whose operands and scales load as zeros.
+template <int MODE, int G32>
+__global__ __launch_bounds__(256, 2) void f6_ragged_sub_bwd_kernel(const RaggedBwdArgs p) {
+  static_assert(G32 == 2 || G32 == 4 || G32 == 8, "groups of 64, 128 or 256");
+  using E = F6SubEngineFor<F6RS, G32>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
+  int g, tm, tn;
+  if (!bwd_tile(p, g, tm, tn)) return;
+  const int m0 = tm * kTile, n0 = tn * kTile;
+  const int kw = round256(p.k_cap);
+  int len = p.group_sizes[g];
+  len = len < 0 ? 0 : (len > p.k_cap ? p.k_cap : len);
+  const unsigned long long a_bytes = f6_operand_bytes(round32(p.M), kw);
+  const unsigned long long b_bytes = f6_operand_bytes(round32(p.N), kw);
+  const uint8_t* a6 = p.work + (unsigned long long)g * a_bytes;
+  const uint8_t* b6 = p.work + (unsigned long long)p.groups * a_bytes + (unsigned long long)g * b_bytes;
+  E e;
+  e.setup(smem, a6, b6, m0, n0, kw / 64, a_bytes, b_bytes, p.a_scale + (long)g * p.M * p.scale_cols,
+          p.b_scale + (long)g * p.scale_cols * p.N, p.M, p.N, p.scale_cols);
+  const int ng = (len + 32 * G32 - 1) / (32 * G32);
+  // stages: 128-K ones, two per group of 256; else 64-K ones, G32 / 2 per group
+  e.template run<MODE == OUT_I32>(smem, G32 == 8 ? 2 * ng : ng * (G32 / 2));
+  const OutView o{static_cast<float*>(p.out) + (long)g * p.M * p.N, nullptr, p.N, p.M, p.N, 0, p.M, p.N};
+  f6sub_store_words<true>(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
 }
 
 bool lhs_mn_major(int layout) { return layout == SHK_LAYOUT_TN || layout == SHK_LAYOUT_TT; }
@@ -244,24 +285,26 @@ hipError_t launch_f6_ragged_sub_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream
   return hipGetLastError();
 }
 
-hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
-  {
-    // with XCD regions, every XCD's workgroups cover its widest region
-    const int tiles_m = (a.M + kTile - 1) / kTile, tiles_n = (a.N + kTile - 1) / kTile;
-    int sm, sn;
-    bwd_regions(tiles_m, tiles_n, sm, sn);
-    if (sm) {
-      const long long n = 8LL * a.groups * (tiles_m / sm) * ((tiles_n + sn - 1) / sn);
-      if (n > 0x7FFFFFFFLL) return hipErrorInvalidValue;
-      grid.x = (unsigned)n;
-    }
+// The backward's grid (with XCD regions, every XCD's workgroups cover its
+// widest region) and its conversion of both operands, K padded to kw, each
+// group's blocks written up to whole k_stage-K stages past its length.
+hipError_t bwd_grid(const RaggedBwdArgs& a, dim3& grid) {
+  const int tiles_m = (a.M + kTile - 1) / kTile, tiles_n = (a.N + kTile - 1) / kTile;
+  int sm, sn;
+  bwd_regions(tiles_m, tiles_n, sm, sn);
+  if (sm) {
+    const long long n = 8LL * a.groups * (tiles_m / sm) * ((tiles_n + sn - 1) / sn);
+    if (n > 0x7FFFFFFFLL) return hipErrorInvalidValue;
+    grid.x = (unsigned)n;
   }
-  const int kw = round128(a.k_cap);
+  return hipSuccess;
+}
+hipError_t bwd_convert(const RaggedBwdArgs& a, int kw, int k_stage, hipStream_t s) {
   const unsigned long long a_group = f6_operand_bytes(round32(a.M), kw);
   const long kp = a.k_cap / 2;
-  const F6PackArgs pa{a.lhs,     a.work,  a.lda,         a.M,    kw / 64, 0, a.groups, kp * a.M, a_group,
+  F6PackArgs pa{a.lhs,     a.work,  a.lda,         a.M,    kw / 64, 0, a.groups, kp * a.M, a_group,
                       a.group_sizes, a.k_cap, piece_bytes(a.lhs, a.lda), true, 2};
-  const F6PackArgs pb{a.rhs,
+  F6PackArgs pb{a.rhs,
                       a.work + (unsigned long long)a.groups * a_group,
                       a.ldb,
                       a.N,
@@ -275,10 +318,32 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
                       piece_bytes(a.rhs, a.ldb),
                       true,
                       2};
-  hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
+  pa.k_stage = pb.k_stage = k_stage;
+  return launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s);
+}
+
+hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
+  hipError_t err = bwd_grid(a, grid);
+  if (err == hipSuccess) err = bwd_convert(a, round128(a.k_cap), 128, s);
   if (err != hipSuccess) return err;
   if (a.out_mode == OUT_I32) hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_I32>, grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(f6_ragged_bwd_kernel<OUT_F32>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int MODE>
+void launch_ragged_sub_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
+  if (a.subchannel == 64) hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 2>), grid, dim3(256), 0, s, a);
+  else if (a.subchannel == 128) hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 4>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 8>), grid, dim3(256), 0, s, a);
+}
+hipError_t launch_f6_ragged_sub_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
+  hipError_t err = bwd_grid(a, grid);
+  // groups of 256 run two 128-K stages each
+  if (err == hipSuccess) err = bwd_convert(a, round256(a.k_cap), a.subchannel > 128 ? 256 : 128, s);
+  if (err != hipSuccess) return err;
+  if (a.out_mode == OUT_I32) launch_ragged_sub_bwd<OUT_I32>(a, grid, s);
+  else launch_ragged_sub_bwd<OUT_F32>(a, grid, s);
   return hipGetLastError();
 }
 
@@ -304,6 +369,15 @@ Entry f6_ragged_sub_fwd_entry(int layout) {
   d.operand_format = SHK_OPERANDS_FP6;
   return Entry{d, nullptr, &launch_f6_ragged_sub_fwd, nullptr, nullptr};
 }
+Entry f6_ragged_sub_bwd_entry(int layout) {
+  shk_kernel_desc d = desc_of<F6RS>(SHK_FAMILY_RAGGED_BWD, layout, 1);
+  d.min_subchannel = 64;
+  d.max_subchannel = 256;
+  d.num_stages = F6SubEngine<F6RS>::P;
+  d.lds_bytes = f6_sub_lds_bytes<F6RS>();
+  d.operand_format = SHK_OPERANDS_FP6;
+  return Entry{d, nullptr, nullptr, &launch_f6_ragged_sub_bwd, nullptr};
+}
 Entry f6_ragged_bwd_entry(int layout) {
   return Entry{f6_ragged_desc(SHK_FAMILY_RAGGED_BWD, layout), nullptr, nullptr, &launch_f6_ragged_bwd, nullptr};
 }
@@ -312,8 +386,8 @@ unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups) {
   const int kw = round128(k);
   return f6_operand_bytes(round32(m), kw) + (unsigned long long)groups * f6_operand_bytes(round32(n), kw);
 }
-unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups) {
-  const int kw = round128(k_cap);
+unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups, bool subchannel) {
+  const int kw = subchannel ? round256(k_cap) : round128(k_cap);
   return (unsigned long long)groups * (f6_operand_bytes(round32(m), kw) + f6_operand_bytes(round32(n), kw));
 }
 

@@ -35,6 +35,7 @@ void append_all(std::vector<Entry>& t) {
   append_fwd<true, 64>(t);
   append_fwd<true, 32>(t);
   t.push_back(f6_ragged_bwd_entry(kLayout));
+  t.push_back(f6_ragged_sub_bwd_entry(kLayout));
   t.push_back(bwd_entry<C<128, 128, 128, 2, 2, false, 64>>(kLayout));
   t.push_back(bwd_entry<C<128, 128, 128, 2, 2, true, 64>>(kLayout));
   t.push_back(bwd_entry<C<128, 128, 128, 2, 2, true, 32>>(kLayout));

@@ -91,6 +91,7 @@ struct F6PackArgs {
   int vec;                      // source alignment: 16, 8 or 1
   bool write_through = false;   // the block stores write through the L2 (cache policy SC1)
   int kmajor_blocks = 1;        // K-major: 64-K blocks per wave (1 or 2)
+  int k_stage = 128;            // with k_len: the GEMM reads whole stages of this many K (128 or 256)
 };
 
 // 32-row panels of an operand with `rows` rows.

@@ -340,13 +340,14 @@ void append_ragged_2(std::vector<Entry>& t);
 void append_ragged_3(std::vector<Entry>& t);
 int max_info_groups();
 // fp6 ragged entries of one layout (k_f6ragged.hip): the forward (task
-// tile 128) and the K-ragged backward, both per-channel.
+// tile 128) and the K-ragged backward, each per-channel and subchannel.
 Entry f6_ragged_fwd_entry(int layout);
 Entry f6_ragged_sub_fwd_entry(int layout);
 Entry f6_ragged_bwd_entry(int layout);
+Entry f6_ragged_sub_bwd_entry(int layout);
 // Workspace bytes of the fp6 ragged paths.
 unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups);
-unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups);
+unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups, bool subchannel);
 
 // Non-table kernels (ragged.hip).
 hipError_t launch_group_info(const int32_t* sizes, int groups, int tile, int align, int capacity,

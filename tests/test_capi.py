@@ -323,19 +323,22 @@ def test_fp6_ragged_entries_report_their_workspace(lib):
         per_channel = [d for d in fp6 if d.scale_mode == kt.SCALE_PER_CHANNEL]
         sub = [d for d in fp6 if d.scale_mode == kt.SCALE_SUBCHANNEL]
         assert sorted(d.layout for d in per_channel) == layouts
-        # the forward also has one fp6 subchannel entry per layout; the backward has none
-        assert sorted(d.layout for d in sub) == (layouts if family == kt.FAMILY_RAGGED_FWD else [])
+        # and one fp6 subchannel entry per layout
+        assert sorted(d.layout for d in sub) == layouts
         for d in fp6:
             if d.scale_mode == kt.SCALE_PER_CHANNEL:
                 # 128 x 128 tiles, two 24 KiB stages of 128 K and the B-scale slots: three per CU
                 assert (d.block_m, d.block_k, d.num_stages) == (128, 128, 2)
                 assert d.lds_bytes == 50176
             else:
-                # the subchannel engine: a ring of 64-K stages, groups of 32 to 256
-                assert (d.block_m, d.block_n, d.min_subchannel, d.max_subchannel) == (128, 128, 32, 256)
+                # the subchannel engine: a ring of 64-K stages, groups of 32 (64 for the backward) to 256
+                low = 32 if family == kt.FAMILY_RAGGED_FWD else 64
+                assert (d.block_m, d.block_n, d.min_subchannel, d.max_subchannel) == (128, 128, low, 256)
                 assert d.lds_bytes == 81920
+            # the subchannel backward pads K to 256, the others to 128
+            step = 256 if family == kt.FAMILY_RAGGED_BWD and d.scale_mode == kt.SCALE_SUBCHANNEL else 128
             for m, n, kp, g in ((8192, 1408, 1024, 8), (17, 24, 32, 3), (2048, 1408, 1001, 8), (1, 8, 1, 1)):
-                kw = -(-2 * kp // 128) * 128
+                kw = -(-2 * kp // step) * step
                 m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
                 if family == kt.FAMILY_RAGGED_FWD:
                     want = (m32 * kw + g * n32 * kw) * 3 // 4
@@ -378,7 +381,7 @@ def test_fp6_ragged_launch_validation(lib):
     assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 128, 2, 16, 0, FAKE, 1 << 30) == 1
     assert "subchannel size 16 is not served" in _err(lib)
     assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 63, 16, 384, 2, 256, 0, FAKE, 1 << 30) == 1
-    assert "M * K/subchannel to be even; got M=63, K/subchannel=3" in _err(lib)
+    assert "M * ceil(K/subchannel) to be even; got M=63, ceil(K/subchannel)=3" in _err(lib)
     bwd = _ragged_f6(kt.FAMILY_RAGGED_BWD, kt.LAYOUT_TN).index
     B = lib.amd_strix_halo_kernels_launch_ragged_bwd
     BW = lib.amd_strix_halo_kernels_launch_ragged_bwd_ws
@@ -390,6 +393,15 @@ def test_fp6_ragged_launch_validation(lib):
     assert "fp32" in _err(lib)
     assert BW(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 64, 1, kt.OUT_F32, FAKE, need) == 1
     assert "subchannel = 0" in _err(lib)
+    sub = _ragged_f6(kt.FAMILY_RAGGED_BWD, kt.LAYOUT_TN, scale_mode=kt.SCALE_SUBCHANNEL).index
+    # the same call with K padded to 256
+    need_sub = 3 * (64 * 256 + 32 * 256) * 3 // 4
+    assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 64, 1, kt.OUT_F32, FAKE, need) == 1
+    assert f"workspace of {need_sub} bytes" in _err(lib)
+    assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 32, 1, kt.OUT_F32, FAKE, need_sub) == 1
+    assert "subchannel size 32 is not served" in _err(lib)
+    assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 47, 16, 20, 3, 64, 1, kt.OUT_F32, FAKE, need_sub) == 1
+    assert "M * ceil(K/subchannel) to be even; got M=47, ceil(K/subchannel)=1" in _err(lib)
     # nothing to run: no workspace needed
     assert BW(bwd, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 0, 0, 1, kt.OUT_F32, None, 0) == 0
 
@@ -408,11 +420,16 @@ def test_fp6_ragged_eligibility():
     assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=128)  # M * K/S odd
     assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=192)
     assert not kt.ragged_fp6_eligible(fwd, subchannel=64, m=8192, n=1408, k_packed=1056)
-    assert not kt.ragged_fp6_eligible(bwd, subchannel=128, m=2048, n=1408, k_packed=1024)
+    # the backward pads K: any capacity, groups of 64 and up
+    assert kt.ragged_fp6_eligible(bwd, subchannel=128, m=2048, n=1408, k_packed=1001)
+    assert kt.ragged_fp6_eligible(bwd, subchannel=256, m=2048, n=1408, k_packed=50)
+    assert not kt.ragged_fp6_eligible(bwd, subchannel=32, m=2048, n=1408, k_packed=1024)
+    assert not kt.ragged_fp6_eligible(bwd, subchannel=64, m=17, n=24, k_packed=96)  # 17 * 3 scale columns
     assert not kt.ragged_fp6_eligible(bwd, subchannel=None, m=16, n=20, k_packed=16)
     assert not kt.ragged_fp6_eligible(fwd, subchannel=None, m=16, n=16, k_packed=kt.FP6_MAX_K // 2 + 1)
     with pytest.raises(LookupError):
         kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True)
+    assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=64, fp6=True).scale_mode == kt.SCALE_SUBCHANNEL
     assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True).scale_mode == kt.SCALE_SUBCHANNEL
     assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=None, fp6=True).block_m == kt.RAGGED_FP6_BLOCK_M
     assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=None).operand_format == kt.OPERANDS_PACKED

@@ -404,11 +404,36 @@ FP6_BWD_SHAPES = [(3, 48, 39, 24, [5, 0, 37]), (5, 200, 1024, 136, [700, 0, 1, 1
                   (2, 1024, 64, 256, [64, 1]), (4, 256, 40, 512, [0, 40, 13, 2])]
 
 
+def _bwd_raw_garbage_ws(device, a_q, b_q, sizes, sa, sb, layout, subchannel):
+    """The fp6 backward's raw int32 sums through the C ABI, with a workspace
+    that starts as garbage: the GEMM reads only blocks the conversion wrote."""
+    import ctypes
+
+    from amd_strix_halo_kernels import kernel_table as kt
+    from amd_strix_halo_kernels import native
+    groups, m, n = a_q.shape[0], a_q.shape[1], b_q.shape[2]
+    lhs, rhs = _pack_bwd(a_q, b_q, layout)
+    kp = lhs.shape[-1] if layout in (shk.GemmLayout.NN, shk.GemmLayout.NT) else lhs.shape[1]
+    desc = kt.find_ragged(kt.FAMILY_RAGGED_BWD, layout=kt.LAYOUT_CODES[layout.value], subchannel=subchannel, fp6=True)
+    nbytes = desc.ragged_workspace_bytes(m, n, kp, groups)
+    work = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=device)
+    raw = torch.full((groups, m, n), 7, dtype=torch.int32, device=device)
+    lhs_d, rhs_d = to_dev(torch, lhs, device), to_dev(torch, rhs, device)
+    sa_d, sb_d = to_dev(torch, sa, device), to_dev(torch, sb, device)
+    gs = torch.tensor(sizes, dtype=torch.int32, device=device)
+    lib = native.load_dispatch_library()
+    rc = lib.amd_strix_halo_kernels_launch_ragged_bwd_ws(
+        desc.index, 0, torch.cuda.current_stream().cuda_stream, lhs_d.data_ptr(), rhs_d.data_ptr(), sa_d.data_ptr(),
+        sb_d.data_ptr(), gs.data_ptr(), raw.data_ptr(), m, n, kp, groups, subchannel or 0, 1, kt.OUT_I32,
+        work.data_ptr(), ctypes.c_uint64(nbytes))
+    assert rc == 0, native._library_last_error(lib)
+    torch.cuda.synchronize()
+    return raw.cpu().numpy().astype(np.int64)
+
+
 @pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
 @pytest.mark.parametrize("shape", FP6_BWD_SHAPES, ids=lambda s: f"g{s[0]}_{s[1]}x{s[2]}x{s[3]}")
 def test_ragged_bwd_fp6_all_layouts(layout, shape, device):
-    from amd_strix_halo_kernels import kernel_table as kt
-    from amd_strix_halo_kernels import native
     groups, m, kcap, n, sizes = shape
     a_q, b_q, sa, sb = _bwd_case(stable_seed("fp6bwd", layout.value, m), groups, m, kcap, n, SCALES[0])
     print(f"case fp6 bwd {layout.value} {shape}", flush=True)
@@ -416,16 +441,37 @@ def test_ragged_bwd_fp6_all_layouts(layout, shape, device):
     for split_k in (1, 2):  # the fp6 entry computes each output whole either way
         got = _run_bwd(device, a_q, b_q, sizes, sa, sb, SCALES[0], layout, split_k)
         assert np.array_equal(got, want)
-    lhs, rhs = _pack_bwd(a_q, b_q, layout)
-    raw = torch.full((groups, m, n), 7, dtype=torch.int32, device=device)
-    native.launch_ragged_bwd(
-        to_dev(torch, lhs, device), to_dev(torch, rhs, device), torch.tensor(sizes, dtype=torch.int32, device=device),
-        a_scale=to_dev(torch, sa, device), b_scale=to_dev(torch, sb, device), out=raw, layout=layout, subchannel=None,
-        split_k=1, rows=m, cols=n, k_packed=lhs.shape[-1] if layout in (shk.GemmLayout.NN, shk.GemmLayout.NT)
-        else lhs.shape[1], out_mode=kt.OUT_I32, fp6=True)
-    torch.cuda.synchronize()
     want_i = np.stack([ref.int_matmul(a_q[g][:, :sizes[g]], b_q[g][:sizes[g]]) for g in range(groups)])
-    assert np.array_equal(raw.cpu().numpy().astype(np.int64), want_i)
+    assert np.array_equal(_bwd_raw_garbage_ws(device, a_q, b_q, sizes, sa, sb, layout, None), want_i)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
+@pytest.mark.parametrize("subchannel", [64, 128, 256])
+def test_ragged_bwd_fp6_subchannel(layout, subchannel, device):
+    """The fp6 subchannel backward (groups of 64 to 256, K padded to 256):
+    every group's scale groups up to its length folded in order, bit-exact
+    for split_k 1 and 2 (each output is computed whole), and the raw int32
+    sums; one shape with zero and tiny scales (the folds in the reference's
+    operation order)."""
+    from amd_strix_halo_kernels import kernel_table as kt
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
+    for shape in FP6_BWD_SHAPES + [(2, 33, 256, 40, [256, 100])]:
+        groups, m, kcap, n, sizes = shape
+        kp = -(-kcap // 2)
+        if not kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_BWD, subchannel=subchannel, m=m, n=n, k_packed=kp):
+            assert m * -(-2 * kp // subchannel) % 2
+            continue
+        a_q, b_q, sa, sb = _bwd_case(stable_seed("fp6subbwd", layout.value, subchannel, m), groups, m, kcap, n, spec)
+        if m == 264:
+            sa[:, ::5, 0] = 0
+            sb[:, -1, ::3] = 0x1C80  # 2^-70
+        print(f"case fp6 sub bwd {layout.value} S={subchannel} {shape}", flush=True)
+        want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=subchannel)
+        for split_k in (1, 2):
+            got = _run_bwd(device, a_q, b_q, sizes, sa, sb, spec, layout, split_k)
+            assert np.array_equal(got, want)
+        want_i = np.stack([ref.int_matmul(a_q[g][:, :sizes[g]], b_q[g][:sizes[g]]) for g in range(groups)])
+        assert np.array_equal(_bwd_raw_garbage_ws(device, a_q, b_q, sizes, sa, sb, layout, subchannel), want_i)
 
 
 def test_config_c5_backward_full(device):
