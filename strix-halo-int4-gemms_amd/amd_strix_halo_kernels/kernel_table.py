@@ -261,8 +261,7 @@ def _desc(index, family, bits, layout, *, bm, bn, bk, wm, wn, swiglu=False, subc
         dtype_bits=bits,
         layout=layout,
         scale_mode=SCALE_SUBCHANNEL if subch else SCALE_PER_CHANNEL,
-        # (the fp6 subchannel backward: groups of 64 and up)
-        min_subchannel=(32 if mk == 32 or (fp6_sub and family != FAMILY_RAGGED_BWD) else 64) if subch else 0,
+        min_subchannel=(32 if mk == 32 or fp6_sub else 64) if subch else 0,
         max_subchannel=(32 if mk == 32 else 256) if subch else 0,
         epilogue_kind=EPI_KIND_SWIGLU if swiglu else EPI_KIND_PLAIN,
         block_m=bm,
@@ -471,16 +470,15 @@ def ragged_fp6_eligible(family: int, *, subchannel: int | None, m: int, n: int, 
     """Whether a ragged call's sizes suit the fp6 entries (k_f6ragged.hip):
     N a multiple of 8 (whole 16-byte output units) and K at most FP6_MAX_K;
     per-channel, or subchannel with M * ceil(K/S) even (the tile reads
-    a_scale in whole dwords): for the forward, K a multiple of 128 and of
-    the group size (whole groups of whole stages of the subchannel tile);
-    for the backward, which pads K, groups of 64 and up."""
+    a_scale in whole dwords; groups of 32 in pairs, so ceil(K/32) even):
+    for the forward, K a multiple of 128 and of the group size (whole
+    groups of whole stages of the subchannel tile); the backward pads K."""
     if subchannel is not None:
         k = 2 * k_packed
+        cols = -(-k // subchannel)
         if family == FAMILY_RAGGED_FWD and k % max(128, subchannel):
             return False
-        if family == FAMILY_RAGGED_BWD and subchannel < 64:
-            return False
-        if m * -(-k // subchannel) % 2:
+        if m * cols % 2 or (subchannel == 32 and cols % 2):
             return False
     return n % 8 == 0 and 2 * k_packed <= FP6_MAX_K
 

@@ -438,6 +438,10 @@ int check_f6_ragged(const shk_kernel_desc& d, int32_t subchannel, const void* b_
   if (sub && (long long)m * scale_cols % 2)
     return fail("kernel " + std::to_string(d.index) + " needs M * ceil(K/subchannel) to be even; got M=" +
                 std::to_string(m) + ", ceil(K/subchannel)=" + std::to_string(scale_cols));
+  // groups of 32 take their a_scale values in pairs, one dword per row
+  if (sub && subchannel == 32 && scale_cols % 2)
+    return fail("kernel " + std::to_string(d.index) + " needs ceil(K/32) to be even with subchannel 32; got " +
+                std::to_string(scale_cols));
   if (n % 8) return fail("kernel " + std::to_string(d.index) + " needs N to be a multiple of 8; got " + std::to_string(n));
   if (!aligned(out, 16) || !aligned(b_scale, 8)) return fail("out must be 16-byte aligned and b_scale 8-byte aligned");
   if ((unsigned long long)n * 4ull * 256ull >= (1ull << 32)) return fail("ragged output rows are limited to 4194304 bytes");

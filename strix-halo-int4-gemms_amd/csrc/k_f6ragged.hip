@@ -208,11 +208,14 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_bwd_kernel(const RaggedBwdAr
 // groups of 256 for S = 256, so the last group's partial sums cover exactly
 // its first len - S * (ceil(len / S) - 1) values).  K is padded to 256, so
 // those groups' stages never pass the converted blocks.
-// With one 64-K stage per group (S = 64) an odd count ends with a stage
-// past the last one, whose operands and scales load as zeros.
+// With one 64-K stage per group (S = 64), or two groups per stage (S = 32),
+// an odd stage count ends with a stage past the last one, whose operands
+// and scales load as zeros.  With groups of 32 the last stage may hold one
+// group past the length: the engine stops folding after group ng - 1, so
+// its scales are never read into the totals.
 template <int MODE, int G32>
 __global__ __launch_bounds__(256, 2) void f6_ragged_sub_bwd_kernel(const RaggedBwdArgs p) {
-  static_assert(G32 == 2 || G32 == 4 || G32 == 8, "groups of 64, 128 or 256");
+  static_assert(G32 == 1 || G32 == 2 || G32 == 4 || G32 == 8, "groups of 32, 64, 128 or 256");
   using E = F6SubEngineFor<F6RS, G32>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[E::LDS_BYTES];
   int g, tm, tn;
@@ -229,8 +232,10 @@ __global__ __launch_bounds__(256, 2) void f6_ragged_sub_bwd_kernel(const RaggedB
   e.setup(smem, a6, b6, m0, n0, kw / 64, a_bytes, b_bytes, p.a_scale + (long)g * p.M * p.scale_cols,
           p.b_scale + (long)g * p.scale_cols * p.N, p.M, p.N, p.scale_cols);
   const int ng = (len + 32 * G32 - 1) / (32 * G32);
-  // stages: 128-K ones, two per group of 256; else 64-K ones, G32 / 2 per group
-  e.template run<MODE == OUT_I32>(smem, G32 == 8 ? 2 * ng : ng * (G32 / 2));
+  if constexpr (G32 == 1) e.fold_last = ng - 1;
+  // stages: 128-K ones, two per group of 256; else 64-K ones, G32 / 2 per
+  // group, or one per two groups of 32
+  e.template run<MODE == OUT_I32>(smem, G32 == 8 ? 2 * ng : (G32 == 1 ? (ng + 1) / 2 : ng * (G32 / 2)));
   const OutView o{static_cast<float*>(p.out) + (long)g * p.M * p.N, nullptr, p.N, p.M, p.N, 0, p.M, p.N};
   f6sub_store_words<true>(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
 }
@@ -333,7 +338,8 @@ hipError_t launch_f6_ragged_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s
 
 template <int MODE>
 void launch_ragged_sub_bwd(const RaggedBwdArgs& a, dim3 grid, hipStream_t s) {
-  if (a.subchannel == 64) hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 2>), grid, dim3(256), 0, s, a);
+  if (a.subchannel == 32) hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 1>), grid, dim3(256), 0, s, a);
+  else if (a.subchannel == 64) hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 2>), grid, dim3(256), 0, s, a);
   else if (a.subchannel == 128) hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 4>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((f6_ragged_sub_bwd_kernel<MODE, 8>), grid, dim3(256), 0, s, a);
 }
@@ -371,7 +377,7 @@ Entry f6_ragged_sub_fwd_entry(int layout) {
 }
 Entry f6_ragged_sub_bwd_entry(int layout) {
   shk_kernel_desc d = desc_of<F6RS>(SHK_FAMILY_RAGGED_BWD, layout, 1);
-  d.min_subchannel = 64;
+  d.min_subchannel = 32;
   d.max_subchannel = 256;
   d.num_stages = F6SubEngine<F6RS>::P;
   d.lds_bytes = f6_sub_lds_bytes<F6RS>();

@@ -531,6 +531,11 @@ struct F6SubEngine64 {
   // every group so far took the fast fold: all totals are sums of finite
   // products below 2^110 in magnitude, so none is NaN
   bool all_fast;
+  // HALF: the last group folded; later ones are not (their partial sums
+  // are zeros; a caller whose K ends inside a stage sets it, so that no
+  // scale past its last group is read into the totals).  The default, the
+  // largest int, makes every comparison with it a constant.
+  int fold_last;
 
   __device__ __forceinline__ int out_row(int i) const { return wm * 64 + 32 * i + (lane & 31); }
   __device__ __forceinline__ int out_col(int j, int q) const { return wn * TN + 32 * j + 8 * q + 4 * (lane >> 5); }
@@ -578,6 +583,7 @@ struct F6SubEngine64 {
           tot[i][j][r] = 0.0f;
         }
     all_fast = true;
+    fold_last = 0x7FFFFFFF;
   }
 
   // byte offset of this lane's scale dword for stage st: waves 0-1 the
@@ -790,7 +796,7 @@ struct F6SubEngine64 {
     tick<S, 3, true, 1>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_lo);
     fence<7>();
     if constexpr (RAW) fold_raw();
-    else fold<false>(smem, 2 * k);
+    else if (2 * k <= fold_last) fold<false>(smem, 2 * k);
     tot_fence();
     tick<S, 0, true, 2>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_hi);
     tick<S, 1, true, 2>(r, rs_st, so, m0_st, rss_st, svo, sm0, s_hi);
@@ -799,7 +805,7 @@ struct F6SubEngine64 {
     frag_fence<1 - S>();
     fence<7>();
     if constexpr (RAW) fold_raw();
-    else fold<false>(smem, 2 * k + 1);
+    else if (2 * k + 1 <= fold_last) fold<false>(smem, 2 * k + 1);
     tot_fence();
   }
   static __device__ __forceinline__ void advance(Reads& r, int& slot) {

@@ -331,9 +331,8 @@ def test_fp6_ragged_entries_report_their_workspace(lib):
                 assert (d.block_m, d.block_k, d.num_stages) == (128, 128, 2)
                 assert d.lds_bytes == 50176
             else:
-                # the subchannel engine: a ring of 64-K stages, groups of 32 (64 for the backward) to 256
-                low = 32 if family == kt.FAMILY_RAGGED_FWD else 64
-                assert (d.block_m, d.block_n, d.min_subchannel, d.max_subchannel) == (128, 128, low, 256)
+                # the subchannel engine: a ring of 64-K stages, groups of 32 to 256
+                assert (d.block_m, d.block_n, d.min_subchannel, d.max_subchannel) == (128, 128, 32, 256)
                 assert d.lds_bytes == 81920
             # the subchannel backward pads K to 256, the others to 128
             step = 256 if family == kt.FAMILY_RAGGED_BWD and d.scale_mode == kt.SCALE_SUBCHANNEL else 128
@@ -398,8 +397,11 @@ def test_fp6_ragged_launch_validation(lib):
     need_sub = 3 * (64 * 256 + 32 * 256) * 3 // 4
     assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 64, 1, kt.OUT_F32, FAKE, need) == 1
     assert f"workspace of {need_sub} bytes" in _err(lib)
-    assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 32, 1, kt.OUT_F32, FAKE, need_sub) == 1
-    assert "subchannel size 32 is not served" in _err(lib)
+    assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 20, 3, 16, 1, kt.OUT_F32, FAKE, need_sub) == 1
+    assert "subchannel size 16 is not served" in _err(lib)
+    # K 72: three groups of 32 per row, whose a_scale values do not pair up in dwords
+    assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 48, 16, 36, 3, 32, 1, kt.OUT_F32, FAKE, need_sub) == 1
+    assert "ceil(K/32) to be even with subchannel 32; got 3" in _err(lib)
     assert BW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 47, 16, 20, 3, 64, 1, kt.OUT_F32, FAKE, need_sub) == 1
     assert "M * ceil(K/subchannel) to be even; got M=47, ceil(K/subchannel)=1" in _err(lib)
     # nothing to run: no workspace needed
@@ -420,16 +422,17 @@ def test_fp6_ragged_eligibility():
     assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=128)  # M * K/S odd
     assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=192)
     assert not kt.ragged_fp6_eligible(fwd, subchannel=64, m=8192, n=1408, k_packed=1056)
-    # the backward pads K: any capacity, groups of 64 and up
+    # the backward pads K: any capacity; groups of 32 need an even ceil(K/32)
     assert kt.ragged_fp6_eligible(bwd, subchannel=128, m=2048, n=1408, k_packed=1001)
     assert kt.ragged_fp6_eligible(bwd, subchannel=256, m=2048, n=1408, k_packed=50)
-    assert not kt.ragged_fp6_eligible(bwd, subchannel=32, m=2048, n=1408, k_packed=1024)
+    assert kt.ragged_fp6_eligible(bwd, subchannel=32, m=2048, n=1408, k_packed=990)  # 62 groups
+    assert not kt.ragged_fp6_eligible(bwd, subchannel=32, m=2048, n=1408, k_packed=1001)
     assert not kt.ragged_fp6_eligible(bwd, subchannel=64, m=17, n=24, k_packed=96)  # 17 * 3 scale columns
     assert not kt.ragged_fp6_eligible(bwd, subchannel=None, m=16, n=20, k_packed=16)
     assert not kt.ragged_fp6_eligible(fwd, subchannel=None, m=16, n=16, k_packed=kt.FP6_MAX_K // 2 + 1)
     with pytest.raises(LookupError):
-        kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True)
-    assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=64, fp6=True).scale_mode == kt.SCALE_SUBCHANNEL
+        kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=512, fp6=True)
+    assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True).scale_mode == kt.SCALE_SUBCHANNEL
     assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=32, fp6=True).scale_mode == kt.SCALE_SUBCHANNEL
     assert kt.find_ragged(fwd, layout=kt.LAYOUT_NN, subchannel=None, fp6=True).block_m == kt.RAGGED_FP6_BLOCK_M
     assert kt.find_ragged(bwd, layout=kt.LAYOUT_NN, subchannel=None).operand_format == kt.OPERANDS_PACKED

@@ -446,25 +446,31 @@ def test_ragged_bwd_fp6_all_layouts(layout, shape, device):
 
 
 @pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
-@pytest.mark.parametrize("subchannel", [64, 128, 256])
+@pytest.mark.parametrize("subchannel", [32, 64, 128, 256])
 def test_ragged_bwd_fp6_subchannel(layout, subchannel, device):
-    """The fp6 subchannel backward (groups of 64 to 256, K padded to 256):
+    """The fp6 subchannel backward (groups of 32 to 256, K padded to 256):
     every group's scale groups up to its length folded in order, bit-exact
     for split_k 1 and 2 (each output is computed whole), and the raw int32
     sums; one shape with zero and tiny scales (the folds in the reference's
-    operation order)."""
+    operation order).  The scales of groups past each length are NaN: the
+    reference never reads them, and neither may the kernel."""
     from amd_strix_halo_kernels import kernel_table as kt
     spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
-    for shape in FP6_BWD_SHAPES + [(2, 33, 256, 40, [256, 100])]:
+    for shape in FP6_BWD_SHAPES + [(2, 33, 256, 40, [256, 100]), (3, 64, 256, 24, [33, 97, 200])]:
         groups, m, kcap, n, sizes = shape
         kp = -(-kcap // 2)
+        cols = -(-2 * kp // subchannel)
         if not kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_BWD, subchannel=subchannel, m=m, n=n, k_packed=kp):
-            assert m * -(-2 * kp // subchannel) % 2
+            assert m * cols % 2 or (subchannel == 32 and cols % 2)
             continue
         a_q, b_q, sa, sb = _bwd_case(stable_seed("fp6subbwd", layout.value, subchannel, m), groups, m, kcap, n, spec)
         if m == 264:
             sa[:, ::5, 0] = 0
             sb[:, -1, ::3] = 0x1C80  # 2^-70
+        for g, size in enumerate(sizes):
+            used = -(-size // subchannel)
+            sa[g, :, used:] = 0x7FC0  # NaN
+            sb[g, used:, :] = 0x7FC0
         print(f"case fp6 sub bwd {layout.value} S={subchannel} {shape}", flush=True)
         want = ref.ragged_bwd_reference(a_q, b_q, np.array(sizes), sa, sb, subchannel=subchannel)
         for split_k in (1, 2):
