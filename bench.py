@@ -5,14 +5,15 @@ M=N=K=8192 (config C2) through ``amd_strix_halo_kernels.mm``, as a fraction of
 the gfx950 dense int8 MFMA peak.  Secondary lines in the same JSON object:
 C3 (int4 subchannel-256 ReLU2, 4096x16384x4096), C4 (int8 fused SwiGLU,
 4096 x 11008 x 4096, TOPS count up + gate), C5 (ragged MoE forward and
-K-ragged backward, G=8, M=8192, K=2048, N=1408), the C2 persistent schedule,
+K-ragged backward, G=8, M=8192, K=2048, N=1408; also with scale groups
+of 128 on the fp6 subchannel tile), the C2 persistent schedule,
 the device quantize-and-pack of a C2-sized bf16 operand (GB/s against HBM),
 and the decode-sized skinny GEMM (int4 per-channel and with scale groups of
 128, M=16, N=K=8192; GB/s against HBM, weights streamed from HBM and
 MALL-resident).
 
     python bench.py [--steps K] [--warmup W] [--no-secondary] [--no-cpu-baseline]
-                    [--only c2|c3|c4|c5|c2p|quant|skinny|skinny_sc]
+                    [--only c2|c3|c4|c5|c5_sc|c2p|quant|skinny|skinny_sc]
 
 A step is one API call over operands already resident in HBM; the timed region
 is exactly K steps bracketed by a device synchronisation on both sides.
@@ -533,6 +534,77 @@ def bench_c5(torch, shk, steps, warmup):
     }
 
 
+def bench_c5_subchannel(torch, shk, steps, warmup, subchannel=128):
+    """C5's shape with scale groups of `subchannel`: the device work of the
+    forward and backward calls on their fp6 subchannel entries (as the API
+    picks them: K a multiple of 128 and of the group size, the backward's K
+    capacity rounded up to 64 so that every group size qualifies), each
+    checked against the API call first."""
+    groups, rows, k, n = 8, 8192, 2048, 1408
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    sizes = _multinomial_sizes(torch, rows, groups, 5)
+    cols = k // subchannel
+    lhs = _rand_int4_packed(torch, rows, k, gen)
+    rhs = torch.stack([_rand_int4_packed(torch, n, k, gen).t().contiguous() for _ in range(groups)])
+    sa = _uniform_bf16(torch, (rows, cols), 0.005, 0.02, gen)
+    sb = _uniform_bf16(torch, (groups, cols, n), 0.005, 0.02, gen)
+    gs = sizes.to(device="cuda", dtype=torch.int32)
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
+
+    from amd_strix_halo_kernels import kernel_table as kt
+    from amd_strix_halo_kernels import native
+
+    if not kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_FWD, subchannel=subchannel, m=rows, n=n, k_packed=k // 2):
+        raise RuntimeError("C5 subchannel forward: the fp6 entry does not take this shape")
+    out_f = torch.empty((rows, n), device="cuda", dtype=torch.bfloat16)
+
+    def fwd():
+        return native.launch_ragged_fwd(lhs, rhs, gs, a_scale=sa, b_scale=sb, out=out_f, layout=shk.GemmLayout.NN,
+                                        subchannel=subchannel, block_m=kt.RAGGED_FP6_BLOCK_M,
+                                        align_tile=kt.RAGGED_FP6_ALIGN, rows=rows, cols=n, k_packed=k // 2,
+                                        out_mode=kt.OUT_BF16, fp6=True)
+
+    ref_out = shk.ragged_dot_int4(lhs, rhs, gs, a_scale=sa, b_scale=sb, scale=spec)
+    fwd()
+    torch.cuda.synchronize()
+    if not torch.equal(ref_out, out_f):
+        raise RuntimeError("subchannel ragged forward: direct launch differs from the API call")
+    wall_f, dev_f, kern_f, _ = _time_steps_device(torch, fwd, steps, warmup)
+    ops = 2 * rows * n * k
+
+    cap = -(-int(sizes.max()) // 64) * 64
+    bcols = -(-cap // subchannel)
+    x = _rand_int4_packed(torch, groups * 2048, cap, gen).view(groups, 2048, cap // 2)
+    dy = torch.stack([_rand_int4_packed(torch, n, cap, gen).t().contiguous() for _ in range(groups)])
+    sa_b = _uniform_bf16(torch, (groups, 2048, bcols), 0.005, 0.02, gen)
+    sb_b = _uniform_bf16(torch, (groups, bcols, n), 0.005, 0.02, gen)
+    if not kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_BWD, subchannel=subchannel, m=2048, n=n, k_packed=cap // 2):
+        raise RuntimeError("C5 subchannel backward: the fp6 entry does not take this shape")
+    out_b = torch.empty((groups, 2048, n), device="cuda", dtype=torch.float32)
+
+    def bwd():
+        return native.launch_ragged_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, out=out_b, layout=shk.GemmLayout.NN,
+                                        subchannel=subchannel, split_k=1, rows=2048, cols=n, k_packed=cap // 2,
+                                        fp6=True)
+
+    api_b = shk.ragged_dot_int4_bwd(x, dy, gs, a_scale=sa_b, b_scale=sb_b, scale=spec)
+    bwd()
+    torch.cuda.synchronize()
+    if not torch.equal(api_b, out_b):
+        raise RuntimeError("subchannel ragged backward: direct launch differs from the API call")
+    wall_b, dev_b, kern_b, _ = _time_steps_device(torch, bwd, steps, warmup)
+    ops_b = 2 * 2048 * n * rows
+    return {
+        "subchannel": subchannel, "group_sizes": sizes.tolist(), "bwd_k_capacity": cap,
+        "fwd": {"device_ms": dev_f, "wall_ms": wall_f, "event_ms_per_call": kern_f,
+                "tops": ops / (dev_f * 1e-3) / 1e12,
+                "frac_int8_peak": ops / (dev_f * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS},
+        "bwd": {"device_ms": dev_b, "wall_ms": wall_b, "event_ms_per_call": kern_b,
+                "tops": ops_b / (dev_b * 1e-3) / 1e12,
+                "frac_int8_peak": ops_b / (dev_b * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS},
+    }
+
+
 def _cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -673,6 +745,7 @@ _ONLY = {
     "c3": ("c3_int4_sc256_relu2_4096x16384x4096", bench_c3),
     "c4": ("c4_int8_swiglu_4096x11008x4096", bench_c4),
     "c5": ("c5_ragged_g8_m8192_k2048_n1408", bench_c5),
+    "c5_sc": ("c5_ragged_sc128_g8_m8192_k2048_n1408", bench_c5_subchannel),
     "c2p": ("c2_persistent_schedule_8192_cubed", bench_c2_persistent),
     "quant": ("quantize_pack_int4_8192x8192_bf16", bench_quant),
     "skinny": ("skinny_int4_pc_16x8192x8192", bench_skinny),
@@ -735,6 +808,9 @@ def main(argv=None) -> int:
         secondary["c4_int8_swiglu_4096x11008x4096"] = bench_c4(torch, shk, max(10, args.steps // 2), args.warmup)
         _log("bench: C5 ragged fwd/bwd")
         secondary["c5_ragged_g8_m8192_k2048_n1408"] = bench_c5(torch, shk, max(10, args.steps // 2), args.warmup)
+        _log("bench: C5 ragged fwd/bwd, scale groups of 128")
+        secondary["c5_ragged_sc128_g8_m8192_k2048_n1408"] = bench_c5_subchannel(torch, shk, max(10, args.steps // 2),
+                                                                               args.warmup)
         _log("bench: C2 on the persistent schedule")
         secondary["c2_persistent_schedule_8192_cubed"] = bench_c2_persistent(torch, shk, max(10, args.steps // 2),
                                                                             args.warmup)
