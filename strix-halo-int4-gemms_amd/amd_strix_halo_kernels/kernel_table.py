@@ -147,12 +147,12 @@ class KernelDesc:
 
     def ragged_workspace_bytes(self, m: int, n: int, k_packed: int, groups: int) -> int:
         """Bytes of the operand workspace of a ragged call (0 for PACKED):
-        with K rounded up to 128 (256 for the subchannel backward), the
+        with K rounded up to 128 (256 for the subchannel entries), the
         forward holds A (round32(m) rows) and per group B (round32(n) rows);
         the backward per group A, then per group B (k_f6ragged.hip)."""
         if not self.needs_workspace or m == 0 or n == 0 or groups == 0:
             return 0
-        step = 256 if self.family == FAMILY_RAGGED_BWD and self.scale_mode == SCALE_SUBCHANNEL else 128
+        step = 256 if self.scale_mode == SCALE_SUBCHANNEL else 128
         kw = -(-2 * k_packed // step) * step
         m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
         if self.family == FAMILY_RAGGED_FWD:
@@ -470,14 +470,9 @@ def ragged_fp6_eligible(family: int, *, subchannel: int | None, m: int, n: int, 
     """Whether a ragged call's sizes suit the fp6 entries (k_f6ragged.hip):
     N a multiple of 8 (whole 16-byte output units) and K at most FP6_MAX_K;
     per-channel, or subchannel with M * ceil(K/S) even (the tile reads
-    a_scale in whole dwords; groups of 32 in pairs, so ceil(K/32) even):
-    for the forward, K a multiple of 128 and of the group size (whole
-    groups of whole stages of the subchannel tile); the backward pads K."""
+    a_scale in whole dwords; groups of 32 in pairs, so ceil(K/32) even)."""
     if subchannel is not None:
-        k = 2 * k_packed
-        cols = -(-k // subchannel)
-        if family == FAMILY_RAGGED_FWD and k % max(128, subchannel):
-            return False
+        cols = -(-2 * k_packed // subchannel)
         if m * cols % 2 or (subchannel == 32 and cols % 2):
             return False
     return n % 8 == 0 and 2 * k_packed <= FP6_MAX_K

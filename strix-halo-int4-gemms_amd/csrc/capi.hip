@@ -413,7 +413,8 @@ int prepare_dense(DenseCall& c, int kernel_index, Phase phase, const void* a, co
 // group), nothing otherwise.
 uint64_t ragged_workspace_bytes(const shk_kernel_desc& d, int32_t m, int32_t n, int32_t k_packed, int32_t groups) {
   if (d.operand_format != SHK_OPERANDS_FP6) return 0;
-  if (d.family == SHK_FAMILY_RAGGED_FWD) return shk::f6_ragged_fwd_workspace(m, n, 2 * k_packed, groups);
+  if (d.family == SHK_FAMILY_RAGGED_FWD)
+    return shk::f6_ragged_fwd_workspace(m, n, 2 * k_packed, groups, d.scale_mode == SHK_SCALE_SUBCHANNEL);
   return shk::f6_ragged_bwd_workspace(m, n, 2 * k_packed, groups, d.scale_mode == SHK_SCALE_SUBCHANNEL);
 }
 
@@ -425,13 +426,7 @@ int check_f6_ragged(const shk_kernel_desc& d, int32_t subchannel, const void* b_
                     int32_t n, int32_t k_packed, int32_t groups, const void* workspace, uint64_t workspace_bytes) {
   const int k = 2 * k_packed;
   if (k > shk::F6_MAX_K) return fail("fp6 kernels support K <= " + std::to_string(shk::F6_MAX_K));
-  // the forward's subchannel tile runs whole groups of whole 64-K stages
-  // (128-K stages for groups of 256, two per group); the backward pads K
-  const int k_step = subchannel > 128 ? subchannel : 128;
   const bool sub = d.scale_mode == SHK_SCALE_SUBCHANNEL;
-  if (sub && d.family == SHK_FAMILY_RAGGED_FWD && k % k_step)
-    return fail("kernel " + std::to_string(d.index) + " needs K to be a multiple of " + std::to_string(k_step) +
-                " with subchannel " + std::to_string(subchannel) + "; got " + std::to_string(k));
   // the tile reads a_scale [M, ceil(K/S)] in whole dwords, which covers the
   // last value only when M * ceil(K/S) is even
   const int scale_cols = sub ? (k + subchannel - 1) / subchannel : 1;

@@ -22,9 +22,10 @@
 // Subchannel forward: the same tasks and converted operands on the 128 x 128
 // subchannel tile of shk_f6sub.h (groups of 32 to 256 added into fp32 in
 // group order, api.py:311-325 as ragged.py applies it), two workgroups per
-// CU, its stores masked to the task's rows and the columns below N.  K is a
-// multiple of 128 (the entry's check), so every group count runs whole
-// stages of the tile's engine.
+// CU, its stores masked to the task's rows and the columns below N.  Its
+// workspace pads K to 256 and the conversion writes whole 256-K stages for
+// groups of 256, so the ceil(K / S) groups (the last one ending at K, whose
+// values past K the conversion zeroes) run whole stages of the tile.
 //
 // Backward (ragged.py:1232-1402 semantics): out[g] = lhs[g] @ rhs[g] over
 // the first group_sizes[g] K values.  The conversion zeroes K at and past
@@ -95,6 +96,20 @@ __global__ __launch_bounds__(256, 3) void f6_ragged_fwd_kernel(const RaggedFwdAr
 // The subchannel tile (128 A rows x 128 B rows, 2 x 2 waves).
 using F6RS = Cfg<4, true, true, 128, 128, 128, 2, 2, false, true, 64, false, 0>;
 
+// Stages of the subchannel tile for ng groups of 32 * G32: 128-K stages,
+// two per group of 256; else 64-K stages, G32 / 2 per group, or one per two
+// groups of 32.  A count that the engine's loop does not divide ends with
+// stages past the last one, whose operands and scales load as zeros.
+// LIMIT, with groups of 32 and ng possibly odd: fold_last stops the folds at
+// group ng - 1 (the second half of the last stage starts past the length,
+// where the reference reads no scale).  Without it the limit stays the
+// engine's constant default, and the folds carry no test.
+template <int G32, bool LIMIT, class E>
+__device__ __forceinline__ int sub_stages(E& e, int ng) {
+  if constexpr (G32 == 1 && LIMIT) e.fold_last = ng - 1;
+  return G32 == 8 ? 2 * ng : (G32 == 1 ? (ng + 1) / 2 : ng * (G32 / 2));
+}
+
 template <int MODE, int G32>
 __global__ __launch_bounds__(256, 2) void f6_ragged_sub_fwd_kernel(const RaggedFwdArgs p) {
   using E = F6SubEngineFor<F6RS, G32>;
@@ -108,13 +123,14 @@ __global__ __launch_bounds__(256, 2) void f6_ragged_sub_fwd_kernel(const RaggedF
   const int tn = w - task * tiles_n;
   const int4 t = *reinterpret_cast<const int4*>(p.tasks + 4 * task);
   const int g = t.x, m0 = t.y, n0 = tn * kTile;
-  const int kw = round128(p.K);
+  const int kw = round256(p.K);
   const unsigned long long a_bytes = f6_operand_bytes(round32(p.M), kw);
   const unsigned long long b_bytes = f6_operand_bytes(round32(p.N), kw);
   E e;
   e.setup(smem, p.work, p.work + a_bytes + (unsigned long long)g * b_bytes, m0, n0, kw / 64, a_bytes, b_bytes,
           p.a_scale, p.b_scale + (long)g * p.scale_cols * p.N, p.M, p.N, p.scale_cols);
-  e.template run<MODE == OUT_I32>(smem, p.K / (G32 == 8 ? 128 : 64));
+  // (ceil(K/32) is even for groups of 32: every stage holds two live groups)
+  e.template run<MODE == OUT_I32>(smem, sub_stages<G32, false>(e, p.scale_cols));
   const OutView o{p.out, nullptr, p.N, p.M, p.N, t.z, t.w, p.N};
   if constexpr (MODE == OUT_I32 || MODE == OUT_F32) {
     f6sub_store_words<true>(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
@@ -231,11 +247,7 @@ __global__ __launch_bounds__(256, 2) void f6_ragged_sub_bwd_kernel(const RaggedB
   E e;
   e.setup(smem, a6, b6, m0, n0, kw / 64, a_bytes, b_bytes, p.a_scale + (long)g * p.M * p.scale_cols,
           p.b_scale + (long)g * p.scale_cols * p.N, p.M, p.N, p.scale_cols);
-  const int ng = (len + 32 * G32 - 1) / (32 * G32);
-  if constexpr (G32 == 1) e.fold_last = ng - 1;
-  // stages: 128-K ones, two per group of 256; else 64-K ones, G32 / 2 per
-  // group, or one per two groups of 32
-  e.template run<MODE == OUT_I32>(smem, G32 == 8 ? 2 * ng : (G32 == 1 ? (ng + 1) / 2 : ng * (G32 / 2)));
+  e.template run<MODE == OUT_I32>(smem, sub_stages<G32, true>(e, (len + 32 * G32 - 1) / (32 * G32)));
   const OutView o{static_cast<float*>(p.out) + (long)g * p.M * p.N, nullptr, p.N, p.M, p.N, 0, p.M, p.N};
   f6sub_store_words<true>(e, o, m0, n0, [&](int i, int j, int x) { return __float_as_int(e.tot[i][j][x]); });
 }
@@ -275,12 +287,14 @@ void launch_ragged_sub(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
   else hipLaunchKernelGGL((f6_ragged_sub_fwd_kernel<MODE, 8>), grid, dim3(256), 0, s, a);
 }
 hipError_t launch_f6_ragged_sub_fwd(const RaggedFwdArgs& a, dim3 grid, hipStream_t s) {
-  const int kw = round128(a.K);
+  const int kw = round256(a.K);
   const unsigned long long a_bytes = f6_operand_bytes(round32(a.M), kw);
-  const F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda),
-                      false, 2};
-  const F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
-                      f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb), false, 2};
+  F6PackArgs pa{a.lhs, a.work, a.lda, a.M, kw / 64, 0, 1, 0, 0, nullptr, a.K, piece_bytes(a.lhs, a.lda),
+                false, 2};
+  F6PackArgs pb{a.rhs,   a.work + a_bytes, a.ldb, a.N, kw / 64, 0, a.groups, (long)(a.K / 2) * a.N,
+                f6_operand_bytes(round32(a.N), kw), nullptr, a.K, piece_bytes(a.rhs, a.ldb), false, 2};
+  // groups of 256 run two 128-K stages each
+  pa.k_stage = pb.k_stage = a.subchannel > 128 ? 256 : 128;
   hipError_t err = launch_f6_pack2(pa, lhs_mn_major(a.layout), pb, rhs_mn_major(a.layout), s,
                                    a.job.sizes != nullptr ? &a.job : nullptr);
   if (err != hipSuccess) return err;
@@ -388,8 +402,8 @@ Entry f6_ragged_bwd_entry(int layout) {
   return Entry{f6_ragged_desc(SHK_FAMILY_RAGGED_BWD, layout), nullptr, nullptr, &launch_f6_ragged_bwd, nullptr};
 }
 
-unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups) {
-  const int kw = round128(k);
+unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups, bool subchannel) {
+  const int kw = subchannel ? round256(k) : round128(k);
   return f6_operand_bytes(round32(m), kw) + (unsigned long long)groups * f6_operand_bytes(round32(n), kw);
 }
 unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups, bool subchannel) {

@@ -346,7 +346,7 @@ Entry f6_ragged_sub_fwd_entry(int layout);
 Entry f6_ragged_bwd_entry(int layout);
 Entry f6_ragged_sub_bwd_entry(int layout);
 // Workspace bytes of the fp6 ragged paths.
-unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups);
+unsigned long long f6_ragged_fwd_workspace(int m, int n, int k, int groups, bool subchannel);
 unsigned long long f6_ragged_bwd_workspace(int m, int n, int k_cap, int groups, bool subchannel);
 
 // Non-table kernels (ragged.hip).

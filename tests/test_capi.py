@@ -334,8 +334,8 @@ def test_fp6_ragged_entries_report_their_workspace(lib):
                 # the subchannel engine: a ring of 64-K stages, groups of 32 to 256
                 assert (d.block_m, d.block_n, d.min_subchannel, d.max_subchannel) == (128, 128, 32, 256)
                 assert d.lds_bytes == 81920
-            # the subchannel backward pads K to 256, the others to 128
-            step = 256 if family == kt.FAMILY_RAGGED_BWD and d.scale_mode == kt.SCALE_SUBCHANNEL else 128
+            # the subchannel entries pad K to 256, the per-channel ones to 128
+            step = 256 if d.scale_mode == kt.SCALE_SUBCHANNEL else 128
             for m, n, kp, g in ((8192, 1408, 1024, 8), (17, 24, 32, 3), (2048, 1408, 1001, 8), (1, 8, 1, 1)):
                 kw = -(-2 * kp // step) * step
                 m32, n32 = -(-m // 32) * 32, -(-n // 32) * 32
@@ -373,10 +373,13 @@ def test_fp6_ragged_launch_validation(lib):
               FAKE, 1 << 40) == 1
     assert "K <= 262144" in _err(lib)
     sub = _ragged_f6(kt.FAMILY_RAGGED_FWD, scale_mode=kt.SCALE_SUBCHANNEL).index
-    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 96, 2, 64, 0, FAKE, 1 << 30) == 1
-    assert "K to be a multiple of 128 with subchannel 64; got 192" in _err(lib)
-    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 192, 2, 256, 0, FAKE, 1 << 30) == 1
-    assert "K to be a multiple of 256 with subchannel 256; got 384" in _err(lib)
+    # K 96: three groups of 32 per row, whose a_scale values do not pair up in dwords
+    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 48, 2, 32, 0, FAKE, 1 << 30) == 1
+    assert "ceil(K/32) to be even with subchannel 32; got 3" in _err(lib)
+    # the subchannel forward pads K to 256: 64 x 16 x 64, 2 groups
+    need_sub = (64 * 256 + 2 * 32 * 256) * 3 // 4
+    assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 32, 2, 64, 0, FAKE, need) == 1
+    assert f"workspace of {need_sub} bytes" in _err(lib)
     assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 64, 16, 128, 2, 16, 0, FAKE, 1 << 30) == 1
     assert "subchannel size 16 is not served" in _err(lib)
     assert FW(sub, 0, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, FAKE, 63, 16, 384, 2, 256, 0, FAKE, 1 << 30) == 1
@@ -413,15 +416,16 @@ def test_fp6_ragged_eligibility():
     assert kt.ragged_fp6_eligible(fwd, subchannel=None, m=8192, n=1408, k_packed=1024)
     assert kt.ragged_fp6_eligible(bwd, subchannel=None, m=2048, n=1408, k_packed=1001)
     assert kt.ragged_fp6_eligible(fwd, subchannel=None, m=17, n=24, k_packed=32)
-    # subchannel: the forward only, and only when K is a whole number of
-    # 128-K blocks and of groups
+    # subchannel: any K (padded to 256), M * ceil(K/S) even, ceil(K/32) even for groups of 32
     assert kt.ragged_fp6_eligible(fwd, subchannel=32, m=8192, n=1408, k_packed=1024)
     assert kt.ragged_fp6_eligible(fwd, subchannel=128, m=18, n=24, k_packed=64)
     assert kt.ragged_fp6_eligible(fwd, subchannel=256, m=18, n=24, k_packed=128)
     assert kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=256)
+    assert kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=192)  # 2 groups, the last half full
+    assert kt.ragged_fp6_eligible(fwd, subchannel=64, m=8192, n=1408, k_packed=1056)
+    assert kt.ragged_fp6_eligible(fwd, subchannel=32, m=8192, n=2880, k_packed=1440)  # K 2880: 90 groups
     assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=128)  # M * K/S odd
-    assert not kt.ragged_fp6_eligible(fwd, subchannel=256, m=17, n=24, k_packed=192)
-    assert not kt.ragged_fp6_eligible(fwd, subchannel=64, m=8192, n=1408, k_packed=1056)
+    assert not kt.ragged_fp6_eligible(fwd, subchannel=32, m=18, n=24, k_packed=48)  # 3 groups of 32
     # the backward pads K: any capacity; groups of 32 need an even ceil(K/32)
     assert kt.ragged_fp6_eligible(bwd, subchannel=128, m=2048, n=1408, k_packed=1001)
     assert kt.ragged_fp6_eligible(bwd, subchannel=256, m=2048, n=1408, k_packed=50)

@@ -260,10 +260,12 @@ def test_ragged_fwd_fp6_all_layouts_and_modes(layout, shape, device):
 
 
 # fp6 subchannel forward (the 128 x 128 subchannel tile on the task list):
-# K a multiple of 128 and of the group size, M * K/S even; row and column
-# masks, groups that span several tiles and tiles that span two groups' rows
+# M * ceil(K/S) even (and ceil(K/32) even for groups of 32); row and column
+# masks, groups that span several tiles and tiles that span two groups' rows,
+# K not a multiple of 128 or of the group size (the last group ends at K)
 FP6_SUB_SHAPES = [(17, 512, 24, [5, 0, 12]), (300, 512, 40, [100, 0, 37, 163]),
-                  (640, 384, 264, [1, 300, 0, 339]), (96, 1024, 8, [96])]
+                  (640, 384, 264, [1, 300, 0, 339]), (96, 1024, 8, [96]), (40, 200, 24, [10, 30]),
+                  (64, 2880, 40, [20, 0, 44]), (130, 96, 16, [65, 65])]
 
 
 @pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: l.value)
@@ -275,7 +277,9 @@ def test_ragged_fwd_fp6_subchannel(layout, subchannel, device):
     from amd_strix_halo_kernels import kernel_table as kt
     spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
     for m, k, n, sizes in FP6_SUB_SHAPES:
-        if k % subchannel or m * (k // subchannel) % 2:
+        cols = -(-k // subchannel)
+        if m * cols % 2 or (subchannel == 32 and cols % 2):
+            assert not kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_FWD, subchannel=subchannel, m=m, n=n, k_packed=k // 2)
             continue
         a_q, b_q, sa, sb = _fwd_case(stable_seed("fp6sub", layout.value, subchannel, m), m, k, n, sizes, spec)
         if m == 300:
