@@ -326,12 +326,12 @@ int amd_strix_halo_kernels_launch_ragged_fwd(int kernel_index, int device_index,
  * (groups of 32 to 256) entry per layout.  They take N a multiple of 8,
  * K <= 262144, out 16-byte and b_scale 8-byte aligned (lhs and rhs in any
  * alignment); subchannel: M * ceil(K/S) even, and ceil(K/32) even for
- * groups of 32.  Forward: task list built with tile 128 (the entry's
- * block_m) and an align_tile that is a multiple of 32; subchannel K a
- * multiple of 128 and of S.  Backward: split_k has no effect (each output
- * is computed whole and written, the result of split_k = 1); the
- * subchannel entry's workspace pads K to 256.  Otherwise the _ws calls
- * equal the calls above, which they replace for every entry. */
+ * groups of 32; the subchannel entries' workspace pads K to 256.
+ * Forward: task list built with tile 128 (the entry's block_m) and an
+ * align_tile that is a multiple of 32.  Backward: split_k has no effect
+ * (each output is computed whole and written, the result of split_k = 1).
+ * Otherwise the _ws calls equal the calls above, which they replace for
+ * every entry. */
 int amd_strix_halo_kernels_ragged_workspace_bytes(int kernel_index, int32_t m, int32_t n, int32_t k_packed,
                                                   int32_t groups, uint64_t* bytes);
 int amd_strix_halo_kernels_launch_ragged_fwd_ws(int kernel_index, int device_index, uintptr_t stream,
