@@ -537,9 +537,9 @@ def bench_c5(torch, shk, steps, warmup):
 def bench_c5_subchannel(torch, shk, steps, warmup, subchannel=128):
     """C5's shape with scale groups of `subchannel`: the device work of the
     forward and backward calls on their fp6 subchannel entries (as the API
-    picks them: K a multiple of 128 and of the group size, the backward's K
-    capacity rounded up to 64 so that every group size qualifies), each
-    checked against the API call first."""
+    picks them; the backward's K capacity is rounded up to 64, which keeps
+    ceil(K/32) even, so that every group size qualifies), each checked
+    against the API call first."""
     groups, rows, k, n = 8, 8192, 2048, 1408
     gen = torch.Generator(device="cuda").manual_seed(5)
     sizes = _multinomial_sizes(torch, rows, groups, 5)
