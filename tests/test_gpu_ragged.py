@@ -326,6 +326,27 @@ def test_config_c5_forward_full(device):
     assert np.array_equal(bf16_bits(torch, out), ref.bf16_round(want))
 
 
+@pytest.mark.parametrize("subchannel", [32, 128])
+def test_config_c5_forward_full_subchannel(subchannel, device):
+    """C5 with scale groups of 32 and 128 on the fp6 subchannel tile: every
+    output bit-exact in bf16 (the groups folded in order)."""
+    from amd_strix_halo_kernels import kernel_table as kt
+    r = ref.rng(50 + subchannel)
+    sizes = ref.multinomial_group_sizes(r, 8192, 8)
+    cols = 2048 // subchannel
+    a_q = ref.randint4(r, (8192, 2048))
+    b_q = ref.randint4(r, (8, 2048, 1408))
+    sa = ref.uniform_bf16(r, (8192, cols), 0.005, 0.02)
+    sb = ref.uniform_bf16(r, (8, cols, 1408), 0.005, 0.02)
+    assert kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_FWD, subchannel=subchannel, m=8192, n=1408, k_packed=1024)
+    print(f"case C5 forward full subchannel {subchannel}", flush=True)
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
+    out = _run_fwd(device, a_q, b_q, sizes.tolist(), sa, sb, spec, shk.GemmLayout.NN, shk.RaggedDotConfig(),
+                   torch.bfloat16)
+    want = ref.ragged_fwd_reference(a_q, b_q, sizes, sa, sb, subchannel=subchannel)
+    assert np.array_equal(bf16_bits(torch, out), ref.bf16_round(want))
+
+
 # ---------------------------------------------------------------------------
 # backward
 
@@ -495,6 +516,32 @@ def test_config_c5_backward_full(device):
     sb = ref.uniform_bf16(r, (8, 1408), 0.005, 0.02)
     got = _run_bwd(device, a_q, b_q, sizes.tolist(), sa, sb, SCALES[0], shk.GemmLayout.NN, 1)
     want = ref.ragged_bwd_reference(a_q, b_q, sizes, sa, sb)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("subchannel", [32, 128])
+def test_config_c5_backward_full_subchannel(subchannel, device):
+    """The C5 backward with scale groups of 32 and 128 on the fp6 subchannel
+    tile (K capacity rounded up to 64): all of dW bit-exact, each group's
+    scale groups past its length unread (NaN here)."""
+    from amd_strix_halo_kernels import kernel_table as kt
+    r = ref.rng(550 + subchannel)
+    sizes = ref.multinomial_group_sizes(r, 8192, 8)
+    cap = -(-int(sizes.max()) // 64) * 64
+    cols = -(-cap // subchannel)
+    a_q = ref.randint4(r, (8, 2048, cap))
+    b_q = ref.randint4(r, (8, cap, 1408))
+    sa = ref.uniform_bf16(r, (8, 2048, cols), 0.005, 0.02)
+    sb = ref.uniform_bf16(r, (8, cols, 1408), 0.005, 0.02)
+    for g, size in enumerate(sizes.tolist()):
+        used = -(-size // subchannel)
+        sa[g, :, used:] = 0x7FC0
+        sb[g, used:, :] = 0x7FC0
+    assert kt.ragged_fp6_eligible(kt.FAMILY_RAGGED_BWD, subchannel=subchannel, m=2048, n=1408, k_packed=cap // 2)
+    print(f"case C5 backward full subchannel {subchannel}", flush=True)
+    spec = shk.ScaleSpec(shk.ScaleMode.SUBCHANNEL, subchannel)
+    got = _run_bwd(device, a_q, b_q, sizes.tolist(), sa, sb, spec, shk.GemmLayout.NN, 1)
+    want = ref.ragged_bwd_reference(a_q, b_q, sizes, sa, sb, subchannel=subchannel)
     assert np.array_equal(got, want)
 
 
