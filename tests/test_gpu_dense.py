@@ -395,6 +395,32 @@ def test_fp6_subchannel_every_group_count(kernel, groups, device):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("kernel", [k for k in _FP6_SUB
+                                    if k.layout is shk.GemmLayout.NN and k.epilogue is shk.Epilogue.NONE],
+                         ids=lambda k: k.kernel_id)
+def test_fp6_subchannel_a_scale_at_two_byte_offset(kernel, device):
+    """a_scale needs only 2-byte alignment: the tile's dword loads of it then
+    start 2 bytes into a dword, and still pick each row's group scales."""
+    from amd_strix_halo_kernels import native
+    _, layout, sub, epi = _kernel_params(kernel)
+    m, n, k = 256, 256, 4 * max(sub, kernel.tile.block_k)
+    a_q, b_q, a_arg, b_arg, sa, sb = dense_case(stable_seed("sub-offset", kernel.kernel_id), bits=4, layout=layout,
+                                                 m=m, n=n, k=k, subchannel=sub, swiglu=False, scale_lo=0.001,
+                                                 scale_hi=0.1)
+    buf = torch.empty(sa.size + 1, dtype=torch.bfloat16, device=device)
+    ta = buf[1:].view(sa.shape)
+    ta.copy_(to_dev(torch, sa, device))
+    assert ta.data_ptr() % 4 == 2 and ta.is_contiguous()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    print(f"case {kernel.kernel_id} a_scale at +2 bytes", flush=True)
+    native.launch_generated_kernel(to_dev(torch, a_arg, device), to_dev(torch, b_arg, device), kernel=kernel,
+                                   a_scale=ta, b_scale=to_dev(torch, sb, device), c=out)
+    torch.cuda.synchronize()
+    want = ref.reference_gemm_bf16(a_arg, b_arg, bits=4, layout=layout, a_scale=sa, b_scale=sb, subchannel=sub,
+                                   epilogue=epi)
+    assert np.array_equal(bf16_bits(torch, out), want)
+
+
 @pytest.mark.parametrize("kernel", _FP6_SUB, ids=lambda k: k.kernel_id)
 def test_fp6_subchannel_special_scales(kernel, device):
     """The subchannel fold takes its two-operation form (a * b from a rank-1
